@@ -1,0 +1,46 @@
+// gsv_device.h — helpers shared by the gfx950 translation units of libgsvox.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gsvox.h"
+#include "gsv_numerics.h"
+
+namespace gsv {
+
+// Records the failing hipError_t for gsv_last_hip_error() (thread-local).
+int record_hip_error(hipError_t e);
+
+// Returns GSV_OK or GSV_ERR_HIP after checking the last launch on this thread.
+inline int check_launch() {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? GSV_OK : record_hip_error(e);
+}
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+constexpr int kWave = 64;    // CDNA wavefront width
+constexpr int kXcds = 8;     // MI355X: 8 XCDs, each with its own L2
+
+// Maps a launch-order block index to a work index so that consecutive work
+// items land on the same XCD.  The hardware dispatches workgroup b to XCD
+// (b mod 8); giving XCD k the contiguous range [k*per, (k+1)*per) keeps
+// neighbouring tiles (which share Gaussians) in one L2.  Launch 8*per blocks;
+// indices >= count must exit.
+__device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t per) {
+    return (b % kXcds) * per + b / kXcds;
+}
+__host__ __device__ inline int64_t xcd_per(int64_t count) { return (count + kXcds - 1) / kXcds; }
+__host__ __device__ inline int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
+__host__ __device__ inline int64_t imax64(int64_t a, int64_t b) { return a > b ? a : b; }
+
+// Zero-fills n 32-bit words with a kernel (graph-capture safe, unlike memset).
+int fill_zero_u32(void *ptr, int64_t n_words, hipStream_t stream);
+
+// Exclusive / inclusive int32 scans over device arrays (scan.hip).
+size_t scan_workspace_bytes(int64_t n);
+int scan_i32(const int32_t *in, int32_t *out, int64_t n, bool inclusive, int64_t *total_out,
+             void *ws, size_t ws_bytes, hipStream_t stream);
+
+}  // namespace gsv

@@ -1,0 +1,512 @@
+// voxelize.hip — forward and backward Gaussian voxelization for gfx950.
+//
+// Reference kernels: voxelize_forward (gs_voxelizer/cuda/voxelize.cu:39-164),
+// voxelize_backward (170-366) and voxelize_backward_per_gaussian (368-610),
+// launched by bindings.cu:362-781.  Semantics kept: 8x8x8 voxel tiles, each
+// voxel sums every Gaussian of its tile's list, voxel centres at index + 0.5,
+// the gates `sigma > 0 || nan || inf` and `alpha * mean(I) < 1e-6`.
+//
+// How the work maps to CDNA4 (not the reference's CUDA mapping):
+//  * exp is evaluated as exp2 on a log2-scaled quadratic form, and both gates
+//    collapse into one compare |s| <= h:  with sigma2 = sigma*log2(e) and
+//    t2 = log2(1e-6 / mean), a Gaussian contributes iff t2 <= sigma2 <= 0.
+//    Writing s = sigma2 - t2/2, h = -t2/2 makes that |s| <= h, and the factor
+//    2^(t2/2) is folded into the intensities (forward) or the final gradient
+//    scale (backward).
+//  * Along a voxel row (fixed y, z) the quadratic form is
+//    s(dx) = R0 + dx*(R1 + A2*dx): two FMAs per voxel once R0, R1 are set up.
+//  * Forward: one 64-lane wave per tile, lane = one x-row of 8 voxels.  Per
+//    batch of 64 Gaussians each lane prepares one Gaussian's row constants into
+//    LDS; the wave then walks the live ones, reading each record with a
+//    uniform-address (broadcast) LDS read, so no VALU slot is spent on
+//    broadcasting.
+//  * Backward: one wave per bucket of 64 (tile, Gaussian) pairs, lane = one
+//    Gaussian; the tile's vol_grad is staged once in LDS and read row by row
+//    with broadcast reads.  Each lane accumulates its Gaussian's moments
+//    sum(w), sum(w*d), sum(w*d*d^T) in registers and turns them into the conic
+//    and mean gradients once, then issues one atomic per output component.
+//  * Tile culling: a Gaussian whose gate ellipsoid sigma >= ln(1e-6/mean)
+//    (a bounded ellipsoid for positive-definite conics) misses every voxel
+//    centre of a tile contributes exactly nothing there in the reference; such
+//    (tile, Gaussian) pairs are skipped with a conservative axis-aligned test.
+#include <float.h>
+
+#include "gsv_device.h"
+
+namespace gsv {
+namespace {
+
+constexpr float kLog2e = 1.44269504088896341f;
+constexpr float kLn2 = 0.693147180559945309f;
+constexpr float kLog2MinContrib = -19.9315685693241741f;  // log2(1e-6)
+
+struct Gate {
+    float shift;  // s = sigma2 - shift
+    float half;   // contributes iff |s| <= half
+    float scale;  // 2^shift
+    float t2;     // log2(1e-6 / mean), or 0 when unbounded
+    bool live;
+    bool bounded;
+};
+
+// Gate constants from the mean intensity (voxelize.cu:138-148).
+__device__ __forceinline__ Gate make_gate(float mean) {
+    Gate g;
+    if (mean > 0.f && mean <= FLT_MAX) {
+        const float t2 = kLog2MinContrib - __log2f(mean);
+        g.t2 = t2;
+        g.shift = 0.5f * t2;
+        g.half = -0.5f * t2;
+        g.scale = exp2f(g.shift);
+        g.live = t2 <= 0.f;  // mean < 1e-6: alpha <= 1 can never reach the threshold
+        g.bounded = true;
+    } else if (mean > 0.f || mean != mean) {
+        // +inf or NaN mean: the reference's `alpha * mean < 1e-6` never holds,
+        // every finite sigma <= 0 contributes I * alpha.
+        g.t2 = 0.f;
+        g.shift = 0.f;
+        g.half = __builtin_inff();
+        g.scale = 1.f;
+        g.live = true;
+        g.bounded = false;
+    } else {
+        g.t2 = 0.f; g.shift = 0.f; g.half = -1.f; g.scale = 0.f;
+        g.live = false;  // mean <= 0: alpha * mean < 1e-6 always
+        g.bounded = false;
+    }
+    return g;
+}
+
+// Conservative test: can the ellipsoid {d^T Q d <= K^2}, K^2 = 2 ln(mean*1e6),
+// centred at (mx,my,mz), contain a point of the box [lo, hi]?  Only answers
+// "no" for a positive-definite Q; margins cover binary32 rounding of the gate.
+__device__ __forceinline__ bool may_touch(float mx, float my, float mz, float a, float b, float c,
+                                          float d, float e, float f, float t2, float xlo,
+                                          float xhi, float ylo, float yhi, float zlo, float zhi) {
+    const float cfx = d * f - e * e, cfy = a * f - c * c, cfz = a * d - b * b;
+    const float det = a * cfx - b * (b * f - c * e) + c * (b * e - c * d);
+    if (!(a > 0.f && cfz > 0.f && det > 0.f)) return true;
+    const float k2 = -2.0f * kLn2 * t2;
+    const float inv = 1.0f / det;
+    const float hx = sqrtf(k2 * cfx * inv) * 1.001f + 0.01f;
+    const float hy = sqrtf(k2 * cfy * inv) * 1.001f + 0.01f;
+    const float hz = sqrtf(k2 * cfz * inv) * 1.001f + 0.01f;
+    const bool miss = (mx + hx < xlo) || (mx - hx > xhi) || (my + hy < ylo) || (my - hy > yhi) ||
+                      (mz + hz < zlo) || (mz - hz > zhi);
+    return !miss;  // NaN anywhere -> comparisons false -> keep
+}
+
+struct TileGeom {
+    int x0, y0, z0;
+    float xlo, xhi, ylo, yhi, zlo, zhi;  // voxel-centre box of the tile's inside voxels
+};
+
+__device__ __forceinline__ TileGeom tile_geom(int64_t tile, int Tx, int Ty, int D, int H, int W) {
+    TileGeom t;
+    const int tx = (int)(tile % Tx), ty = (int)((tile / Tx) % Ty), tz = (int)(tile / ((int64_t)Tx * Ty));
+    t.x0 = tx * GSV_TILE; t.y0 = ty * GSV_TILE; t.z0 = tz * GSV_TILE;
+    t.xlo = (float)t.x0 + 0.5f; t.xhi = (float)min(t.x0 + GSV_TILE - 1, W - 1) + 0.5f;
+    t.ylo = (float)t.y0 + 0.5f; t.yhi = (float)min(t.y0 + GSV_TILE - 1, H - 1) + 0.5f;
+    t.zlo = (float)t.z0 + 0.5f; t.zhi = (float)min(t.z0 + GSV_TILE - 1, D - 1) + 0.5f;
+    return t;
+}
+
+// ---------------------------------------------------------------- forward --
+
+template <int C>
+__global__ __launch_bounds__(kWave) void k_vox_fwd(
+    int D, int H, int W, int Tx, int Ty, int64_t T, int64_t per, int n, int n_isect,
+    const int *__restrict__ ids, const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
+    const float2 *__restrict__ conics, const float *__restrict__ intens, float *__restrict__ vol) {
+    __shared__ float4 s_rec[kWave][4];
+    const int64_t tile = xcd_remap(blockIdx.x, per);
+    if (tile >= T) return;
+    const int lane = threadIdx.x;
+    const TileGeom tg = tile_geom(tile, Tx, Ty, D, H, W);
+    const float py = (float)(lane & 7) + 0.5f, pz = (float)(lane >> 3) + 0.5f;  // tile-local
+    int2 range = bins[tile];
+    range.x = max(range.x, 0);
+    range.y = min(range.y, n_isect);  // never index past the id array
+
+    float acc[GSV_TILE][C];
+#pragma unroll
+    for (int u = 0; u < GSV_TILE; ++u)
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc[u][c] = 0.f;
+
+    for (int b0 = range.x; b0 < range.y; b0 += kWave) {
+        const int idx = b0 + lane;
+        bool live = false;
+        if (idx < range.y) {
+            const int g = ids[idx];
+            if ((unsigned)g < (unsigned)n) {
+                const float4 p = pos_radii[g];
+                const float2 c01 = conics[3 * g], c23 = conics[3 * g + 1], c45 = conics[3 * g + 2];
+                float I[C], mean = 0.f;
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    I[c] = intens[(size_t)g * C + c];
+                    mean += I[c];
+                }
+                mean /= (float)C;
+                const Gate gt = make_gate(mean);
+                live = gt.live;
+                if (live && gt.bounded)
+                    live = may_touch(p.x, p.y, p.z, c01.x, c01.y, c23.x, c23.y, c45.x, c45.y, gt.t2,
+                                     tg.xlo, tg.xhi, tg.ylo, tg.yhi, tg.zlo, tg.zhi);
+                if (live) {
+                    s_rec[lane][0] = make_float4(p.x - (float)tg.x0 - 0.5f, p.y - (float)tg.y0,
+                                                 p.z - (float)tg.z0, -0.5f * kLog2e * c01.x);
+                    s_rec[lane][1] = make_float4(-kLog2e * c01.y, -kLog2e * c23.x,
+                                                 -0.5f * kLog2e * c23.y, -kLog2e * c45.x);
+                    s_rec[lane][2] = make_float4(-0.5f * kLog2e * c45.y, gt.shift, gt.half, 0.f);
+                    float iw[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int c = 0; c < C; ++c) iw[c] = I[c] * gt.scale;
+                    s_rec[lane][3] = make_float4(iw[0], iw[1], iw[2], iw[3]);
+                }
+            }
+        }
+        uint64_t mask = __ballot(live);
+        __syncthreads();
+        while (mask) {
+            const int j = __builtin_ctzll(mask);
+            mask &= mask - 1;
+            const float4 r0 = s_rec[j][0], r1 = s_rec[j][1], r2 = s_rec[j][2], r3 = s_rec[j][3];
+            const float iw[4] = {r3.x, r3.y, r3.z, r3.w};
+            const float dy = r0.y - py, dz = r0.z - pz;
+            const float R1 = fmaf(r1.x, dy, r1.y * dz);
+            const float R0 = fmaf(fmaf(r1.z, dy, r1.w * dz), dy, fmaf(r2.x * dz, dz, -r2.y));
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u) {
+                const float dx = r0.x - (float)u;
+                const float s = fmaf(dx, fmaf(dx, r0.w, R1), R0);
+                const float a = (fabsf(s) <= r2.z) ? __builtin_amdgcn_exp2f(s) : 0.f;
+#pragma unroll
+                for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
+            }
+        }
+        __syncthreads();
+    }
+    const int y = tg.y0 + (lane & 7), z = tg.z0 + (lane >> 3);
+    if (y < H && z < D) {
+        float *o = vol + (((int64_t)z * H + y) * W + tg.x0) * C;
+        const int nx = min(GSV_TILE, W - tg.x0);
+#pragma unroll
+        for (int u = 0; u < GSV_TILE; ++u)
+            if (u < nx)
+#pragma unroll
+                for (int c = 0; c < C; ++c) o[u * C + c] = acc[u][c];
+    }
+}
+
+// --------------------------------------------------------------- backward --
+
+constexpr int kBucket = kWave;  // (tile, Gaussian) pairs per wave
+
+__global__ __launch_bounds__(256) void k_bucket_counts(const int2 *__restrict__ bins, int64_t T,
+                                                       int *__restrict__ counts) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const int2 r = bins[t];
+    const int m = max(0, r.y - r.x);
+    counts[t] = (m + kBucket - 1) / kBucket;
+}
+
+__global__ __launch_bounds__(256) void k_bucket_fill(const int *__restrict__ counts,
+                                                     const int *__restrict__ offs, int64_t T,
+                                                     int64_t cap, int *__restrict__ bucket_tile) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const int c = counts[t];
+    const int64_t o = offs[t];
+    for (int k = 0; k < c; ++k)
+        if (o + k < cap) bucket_tile[o + k] = (int)t;
+}
+
+template <int C>
+__global__ __launch_bounds__(kWave) void k_vox_bwd(
+    int D, int H, int W, int Tx, int Ty, int n, int n_isect, const int *__restrict__ ids,
+    const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
+    const float2 *__restrict__ conics, const float *__restrict__ intens,
+    const float *__restrict__ vol_grad, const int *__restrict__ bucket_tile,
+    const int *__restrict__ bucket_off, const int64_t *__restrict__ total_buckets, int64_t cap,
+    float *__restrict__ dpos, float *__restrict__ dconic, float *__restrict__ dint) {
+    __shared__ float4 s_g[kWave][2 * C];  // vol_grad of the tile: row (ly + 8*lz), 8*C floats
+    const int64_t total = min<int64_t>(*total_buckets, cap);
+    const int64_t per = xcd_per(total);
+    const int64_t bkt = xcd_remap(blockIdx.x, per);
+    if (bkt >= total || blockIdx.x >= kXcds * per) return;
+    const int lane = threadIdx.x;
+    const int tile = bucket_tile[bkt];
+    const int chunk = (int)(bkt - bucket_off[tile]);
+    int2 range = bins[tile];
+    range.x = max(range.x, 0);
+    range.y = min(range.y, n_isect);  // never index past the id array
+    const TileGeom tg = tile_geom(tile, Tx, Ty, D, H, W);
+
+    {   // stage the tile's vol_grad, lane = row; outside voxels are zero
+        const int y = tg.y0 + (lane & 7), z = tg.z0 + (lane >> 3);
+        float v[GSV_TILE * C];
+#pragma unroll
+        for (int i = 0; i < GSV_TILE * C; ++i) v[i] = 0.f;
+        if (y < H && z < D) {
+            const float *src = vol_grad + (((int64_t)z * H + y) * W + tg.x0) * C;
+            const int nx = min(GSV_TILE, W - tg.x0);
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u)
+                if (u < nx)
+#pragma unroll
+                    for (int c = 0; c < C; ++c) v[u * C + c] = src[u * C + c];
+        }
+#pragma unroll
+        for (int q = 0; q < 2 * C; ++q)
+            s_g[lane][q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
+
+    // this lane's Gaussian
+    const int idx = range.x + chunk * kBucket + lane;
+    bool live = false;
+    int g = 0;
+    float mxl = 0.f, myl = 0.f, mzl = 0.f;
+    float ca = 0.f, cb = 0.f, cc = 0.f, cd = 0.f, ce = 0.f, cf = 0.f;
+    float I[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) I[c] = 0.f;
+    Gate gt = make_gate(0.f);
+    if (idx < range.y) {
+        g = ids[idx];
+        if ((unsigned)g < (unsigned)n) {
+            const float4 p = pos_radii[g];
+            const float2 c01 = conics[3 * g], c23 = conics[3 * g + 1], c45 = conics[3 * g + 2];
+            ca = c01.x; cb = c01.y; cc = c23.x; cd = c23.y; ce = c45.x; cf = c45.y;
+            float mean = 0.f;
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                I[c] = intens[(size_t)g * C + c];
+                mean += I[c];
+            }
+            mean /= (float)C;
+            gt = make_gate(mean);
+            live = gt.live;
+            if (live && gt.bounded)
+                live = may_touch(p.x, p.y, p.z, ca, cb, cc, cd, ce, cf, gt.t2, tg.xlo, tg.xhi,
+                                 tg.ylo, tg.yhi, tg.zlo, tg.zhi);
+            mxl = p.x - (float)tg.x0 - 0.5f;
+            myl = p.y - (float)tg.y0;
+            mzl = p.z - (float)tg.z0;
+        }
+    }
+    __syncthreads();
+    if (!__any(live)) return;
+
+    const float A2 = -0.5f * kLog2e * ca, Bn = -kLog2e * cb, Cn = -kLog2e * cc;
+    const float Dn = -0.5f * kLog2e * cd, En = -kLog2e * ce, Fn = -0.5f * kLog2e * cf;
+    const float shift = gt.shift, half = live ? gt.half : -1.f;
+
+    float S0 = 0.f, Sx = 0.f, Sy = 0.f, Sz = 0.f;
+    float Sxx = 0.f, Sxy = 0.f, Sxz = 0.f, Syy = 0.f, Syz = 0.f, Szz = 0.f;
+    float dIa[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) dIa[c] = 0.f;
+
+    const int ny = min(GSV_TILE, H - tg.y0), nz = min(GSV_TILE, D - tg.z0);
+    for (int lz = 0; lz < nz; ++lz) {
+        const float dz = mzl - ((float)lz + 0.5f);
+        const float Cdz = Cn * dz, Edz = En * dz;
+        const float R0z = fmaf(Fn * dz, dz, -shift);
+        for (int ly = 0; ly < ny; ++ly) {
+            const int row = lz * GSV_TILE + ly;
+            float gv[GSV_TILE * C];
+#pragma unroll
+            for (int q = 0; q < 2 * C; ++q) {
+                const float4 t4 = s_g[row][q];
+                gv[4 * q] = t4.x; gv[4 * q + 1] = t4.y; gv[4 * q + 2] = t4.z; gv[4 * q + 3] = t4.w;
+            }
+            const float dy = myl - ((float)ly + 0.5f);
+            const float R1 = fmaf(Bn, dy, Cdz);
+            const float R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
+            float W0 = 0.f, W1 = 0.f, W2 = 0.f;
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u) {
+                const float dx = mxl - (float)u;
+                const float s = fmaf(dx, fmaf(dx, A2, R1), R0);
+                const float a = (fabsf(s) <= half) ? __builtin_amdgcn_exp2f(s) : 0.f;
+                float h;
+                if (C == 1) {
+                    h = a * gv[u];
+                } else {
+                    float G = 0.f;
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        G = fmaf(I[c], gv[u * C + c], G);
+                        dIa[c] = fmaf(a, gv[u * C + c], dIa[c]);
+                    }
+                    h = a * G;
+                }
+                W0 += h;
+                const float t = h * dx;
+                W1 += t;
+                W2 = fmaf(t, dx, W2);
+            }
+            S0 += W0;
+            Sx += W1;
+            Sxx += W2;
+            Sxy = fmaf(W1, dy, Sxy);
+            Sxz = fmaf(W1, dz, Sxz);
+            const float t0 = W0 * dy, t1 = W0 * dz;
+            Sy += t0;
+            Syy = fmaf(t0, dy, Syy);
+            Syz = fmaf(t0, dz, Syz);
+            Sz += t1;
+            Szz = fmaf(t1, dz, Szz);
+        }
+    }
+    if (live) {
+        // sigma-gradient weight per unit of h: alpha = scale * a
+        const float w = (C == 1) ? gt.scale * I[0] : gt.scale;
+        float *dc = dconic + 6 * (size_t)g;
+        unsafeAtomicAdd(dc + 0, -0.5f * w * Sxx);
+        unsafeAtomicAdd(dc + 1, -w * Sxy);
+        unsafeAtomicAdd(dc + 2, -w * Sxz);
+        unsafeAtomicAdd(dc + 3, -0.5f * w * Syy);
+        unsafeAtomicAdd(dc + 4, -w * Syz);
+        unsafeAtomicAdd(dc + 5, -0.5f * w * Szz);
+        float *dp = dpos + 4 * (size_t)g;
+        unsafeAtomicAdd(dp + 0, -w * (ca * Sx + cb * Sy + cc * Sz));
+        unsafeAtomicAdd(dp + 1, -w * (cb * Sx + cd * Sy + ce * Sz));
+        unsafeAtomicAdd(dp + 2, -w * (cc * Sx + ce * Sy + cf * Sz));
+        float *di = dint + (size_t)C * g;
+        if (C == 1) {
+            unsafeAtomicAdd(di, gt.scale * S0);
+        } else {
+#pragma unroll
+            for (int c = 0; c < C; ++c) unsafeAtomicAdd(di + c, gt.scale * dIa[c]);
+        }
+    }
+}
+
+struct BwdLayout {
+    size_t counts, offs, scan, total, btile, end;
+    int64_t cap;
+};
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+BwdLayout bwd_layout(int64_t T, int64_t n_isect) {
+    BwdLayout L{};
+    L.cap = imin64(T, n_isect) + (n_isect + kBucket - 1) / kBucket;
+    size_t off = 0;
+    L.counts = off; off += align256((size_t)T * 4);
+    L.offs = off; off += align256((size_t)T * 4);
+    L.scan = off; off += scan_workspace_bytes(T);
+    L.total = off; off += 256;
+    L.btile = off; off += align256((size_t)imax64(L.cap, 1) * 4);
+    L.end = off;
+    return L;
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace
+}  // namespace gsv
+
+using namespace gsv;
+
+extern "C" int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                                int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                                const int32_t *tile_bins, const float *pos3d_radii,
+                                const float *conics, const float *intensities, float *volume,
+                                void *stream) {
+    if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
+    if (n < 0 || D <= 0 || H <= 0 || W <= 0 || !volume || !tile_bins) return GSV_ERR_INVALID_ARGUMENT;
+    const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
+    const int64_t T = (int64_t)Tx * Ty * Tz;
+    const int64_t vox = (int64_t)D * H * W;
+    if (vox * channels > ((int64_t)1 << 40) || T > INT32_MAX || num_intersects > INT32_MAX)
+        return GSV_ERR_SIZE_OVERFLOW;
+    hipStream_t s = as_stream(stream);
+    if (num_intersects <= 0 || n == 0) return fill_zero_u32(volume, vox * channels, s);
+    if (!gaussian_ids_sorted || !pos3d_radii || !conics || !intensities) return GSV_ERR_INVALID_ARGUMENT;
+    if (!aligned(pos3d_radii, 16) || !aligned(conics, 8)) return GSV_ERR_INVALID_ARGUMENT;
+    const int64_t per = xcd_per(T);
+    const dim3 grid((unsigned)(kXcds * per)), block(kWave);
+#define GSV_VF(CH)                                                                                 \
+    hipLaunchKernelGGL(k_vox_fwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, T, per, n,               \
+                       (int)num_intersects,                                                         \
+                       gaussian_ids_sorted, reinterpret_cast<const int2 *>(tile_bins),             \
+                       reinterpret_cast<const float4 *>(pos3d_radii),                              \
+                       reinterpret_cast<const float2 *>(conics), intensities, volume)
+    switch (channels) {
+        case 1: GSV_VF(1); break;
+        case 2: GSV_VF(2); break;
+        case 3: GSV_VF(3); break;
+        default: GSV_VF(4); break;
+    }
+#undef GSV_VF
+    return check_launch();
+}
+
+extern "C" int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W,
+                                                int64_t num_intersects, size_t *bytes) {
+    if (!bytes || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
+    const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
+    *bytes = bwd_layout(T, num_intersects > 0 ? num_intersects : 0).end;
+    return GSV_OK;
+}
+
+extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                                int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                                const int32_t *tile_bins, const float *pos3d_radii,
+                                const float *conics, const float *intensities,
+                                const float *vol_grad, float *dpos3d_radii, float *dconics,
+                                float *dintensities, int32_t variant, void *workspace,
+                                size_t workspace_bytes, void *stream) {
+    if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
+    if (n < 0 || D <= 0 || H <= 0 || W <= 0 || (variant != 0 && variant != 1))
+        return GSV_ERR_INVALID_ARGUMENT;
+    if (n == 0) return GSV_OK;
+    if (!dpos3d_radii || !dconics || !dintensities) return GSV_ERR_INVALID_ARGUMENT;
+    hipStream_t s = as_stream(stream);
+    if (int st = fill_zero_u32(dpos3d_radii, 4 * (int64_t)n, s)) return st;
+    if (int st = fill_zero_u32(dconics, 6 * (int64_t)n, s)) return st;
+    if (int st = fill_zero_u32(dintensities, (int64_t)channels * n, s)) return st;
+    if (num_intersects <= 0) return GSV_OK;
+    if (!gaussian_ids_sorted || !tile_bins || !pos3d_radii || !conics || !intensities || !vol_grad)
+        return GSV_ERR_INVALID_ARGUMENT;
+    if (!aligned(pos3d_radii, 16) || !aligned(conics, 8)) return GSV_ERR_INVALID_ARGUMENT;
+    const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
+    const int64_t T = (int64_t)Tx * Ty * Tz;
+    if (T > INT32_MAX || num_intersects > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
+    const BwdLayout L = bwd_layout(T, num_intersects);
+    if (!workspace || workspace_bytes < L.end) return GSV_ERR_WORKSPACE_TOO_SMALL;
+    char *ws = static_cast<char *>(workspace);
+    int *counts = reinterpret_cast<int *>(ws + L.counts);
+    int *offs = reinterpret_cast<int *>(ws + L.offs);
+    int64_t *total = reinterpret_cast<int64_t *>(ws + L.total);
+    int *btile = reinterpret_cast<int *>(ws + L.btile);
+    const unsigned tb = (unsigned)((T + 255) / 256);
+    hipLaunchKernelGGL(k_bucket_counts, dim3(tb), dim3(256), 0, s,
+                       reinterpret_cast<const int2 *>(tile_bins), T, counts);
+    if (int st = check_launch()) return st;
+    if (int st = scan_i32(counts, offs, T, false, total, ws + L.scan, scan_workspace_bytes(T), s))
+        return st;
+    hipLaunchKernelGGL(k_bucket_fill, dim3(tb), dim3(256), 0, s, counts, offs, T, L.cap, btile);
+    if (int st = check_launch()) return st;
+    const dim3 grid((unsigned)(L.cap + kXcds)), block(kWave);
+#define GSV_VB(CH)                                                                                  \
+    hipLaunchKernelGGL(k_vox_bwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, n, (int)num_intersects,   \
+                       gaussian_ids_sorted,                                                         \
+                       reinterpret_cast<const int2 *>(tile_bins),                                   \
+                       reinterpret_cast<const float4 *>(pos3d_radii),                               \
+                       reinterpret_cast<const float2 *>(conics), intensities, vol_grad, btile,      \
+                       offs, total, L.cap, dpos3d_radii, dconics, dintensities)
+    switch (channels) {
+        case 1: GSV_VB(1); break;
+        case 2: GSV_VB(2); break;
+        case 3: GSV_VB(3); break;
+        default: GSV_VB(4); break;
+    }
+#undef GSV_VB
+    return check_launch();
+}

@@ -1,0 +1,235 @@
+"""Native entry points of gs_voxelizer, backed by libgsvox.so (gfx950 HIP kernels).
+
+Same module path, function names, argument order and return values as the
+reference's pybind11 extension ``gs_voxelizer.cuda`` (gs_voxelizer/cuda/ext.cpp:4-11,
+bindings.h:40-194), so ``import gs_voxelizer.cuda as _C`` callers keep working.
+Outputs and workspaces are torch tensors allocated on the inputs' device; every
+kernel is enqueued on torch's current stream of that device.  Errors raise
+RuntimeError, as the reference's TORCH_CHECK / std::runtime_error do.
+
+``cumsum_tiles_hit`` is an addition: the reference computes that prefix sum with
+``torch.cumsum`` in voxelize.py:87; here it is a native kernel as well.
+"""
+import ctypes
+from typing import Tuple
+
+import torch
+
+from . import _lib
+
+MAX_CHANNELS = 4
+BLOCK = 8
+
+_L = _lib.load()
+
+
+def _status_error(name: str, status: int) -> RuntimeError:
+    text = _L.gsv_status_string(status).decode()
+    if status == 5:  # GSV_ERR_HIP
+        text += f" (hipError_t {_L.gsv_last_hip_error()})"
+    return RuntimeError(f"gs_voxelizer.{name}: {text}")
+
+
+def _call(name: str, *args) -> None:
+    st = getattr(_L, "gsv_" + name)(*args)
+    if st != 0:
+        raise _status_error(name, st)
+
+
+def _check_input(t: torch.Tensor, what: str) -> None:
+    # CHECK_INPUT of bindings.h:7-12
+    if not t.is_cuda:
+        raise RuntimeError(f"{what} must be a CUDA tensor")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{what} must be contiguous")
+
+
+def _check_dtype(t: torch.Tensor, what: str, dtype: torch.dtype) -> None:
+    if t.dtype != dtype:
+        raise RuntimeError(f"{what}: expected scalar type {dtype} but found {t.dtype}")
+
+
+def _ptr(t: torch.Tensor):
+    return ctypes.c_void_p(t.data_ptr()) if t.numel() > 0 else ctypes.c_void_p(0)
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _tiles(vol_size) -> Tuple[int, int, int]:
+    D, H, W = (int(v) for v in vol_size)
+    return (W + BLOCK - 1) // BLOCK, (H + BLOCK - 1) // BLOCK, (D + BLOCK - 1) // BLOCK
+
+
+def _channels(intensities: torch.Tensor) -> int:
+    channels = intensities.size(1)  # 2-D required, bindings.cu:59
+    if channels > MAX_CHANNELS:
+        raise RuntimeError("Number of channels exceeds MAX_CHANNELS")
+    return channels
+
+
+def optim_to_render_forward(num_gaussians: int, pos3d, scale3d, quat, intensities,
+                            vol_size_voxel, vol_size_world, vol_center_pos):
+    """bindings.cu:38-189. Returns (pos3d_radii, conics, tile_min, tile_max, num_tiles_hit)."""
+    for t, w in ((pos3d, "pos3d"), (scale3d, "scale3d"), (quat, "quat"), (intensities, "intensities")):
+        _check_input(t, w)
+        _check_dtype(t, w, torch.float32)
+    channels = _channels(intensities)
+    n = int(num_gaussians)
+    D, H, W = (int(v) for v in vol_size_voxel)
+    wz, wy, wx = (float(v) for v in vol_size_world)
+    cz, cy, cx = (float(v) for v in vol_center_pos)
+    dev = pos3d.device
+    f32 = dict(device=dev, dtype=torch.float32)
+    i32 = dict(device=dev, dtype=torch.int32)
+    pos3d_radii = torch.empty((n, 4), **f32)
+    conics = torch.empty((n, 6), **f32)
+    tile_min = torch.empty((n, 3), **i32)
+    tile_max = torch.empty((n, 3), **i32)
+    num_tiles_hit = torch.empty((n,), **i32)
+    with torch.cuda.device(dev):
+        _call("project_fwd", n, channels, _ptr(pos3d), _ptr(scale3d), _ptr(quat), _ptr(intensities),
+              D, H, W, wz, wy, wx, cz, cy, cx, _ptr(pos3d_radii), _ptr(conics), _ptr(tile_min),
+              _ptr(tile_max), _ptr(num_tiles_hit), _stream(dev))
+    return pos3d_radii, conics, tile_min, tile_max, num_tiles_hit
+
+
+def optim_to_render_backward(num_gaussians: int, pos3d, scale3d, quat, vol_size_voxel,
+                             vol_size_world, vol_center_pos, pos3d_radii_grad_in, conics_grad_in,
+                             pos3d_radii_out):
+    """bindings.cu:197-251. Returns (grad_pos3d, grad_scale3d, grad_quat)."""
+    n = int(num_gaussians)
+    dev = pos3d.device
+    scale3d, quat = scale3d.contiguous(), quat.contiguous()
+    dpr = pos3d_radii_grad_in.contiguous()
+    dcn = conics_grad_in.contiguous()
+    pr = pos3d_radii_out.contiguous()
+    for t, w in ((scale3d, "scale3d"), (quat, "quat"), (dpr, "pos3d_radii_grad_in"),
+                 (dcn, "conics_grad_in"), (pr, "pos3d_radii_out")):
+        _check_input(t, w)
+        _check_dtype(t, w, torch.float32)
+    D, H, W = (int(v) for v in vol_size_voxel)
+    wz, wy, wx = (float(v) for v in vol_size_world)
+    cz, cy, cx = (float(v) for v in vol_center_pos)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dpos = torch.empty((n, 3), **f32)
+    dscale = torch.empty((n, 3), **f32)
+    dquat = torch.empty((n, 4), **f32)
+    with torch.cuda.device(dev):
+        _call("project_bwd", n, _ptr(pos3d), _ptr(scale3d), _ptr(quat), D, H, W, wz, wy, wx,
+              cz, cy, cx, _ptr(dpr), _ptr(dcn), _ptr(pr), _ptr(dpos), _ptr(dscale), _ptr(dquat),
+              _stream(dev))
+    return dpos, dscale, dquat
+
+
+def cumsum_tiles_hit(num_tiles_hit):
+    """Inclusive int32 prefix sum of num_tiles_hit plus its total as a (1,) int64
+    device tensor (one scalar to read back instead of the whole array)."""
+    _check_input(num_tiles_hit, "num_tiles_hit")
+    _check_dtype(num_tiles_hit, "num_tiles_hit", torch.int32)
+    n = num_tiles_hit.numel()
+    dev = num_tiles_hit.device
+    cum = torch.empty((n,), device=dev, dtype=torch.int32)
+    total = torch.zeros((1,), device=dev, dtype=torch.int64)
+    nbytes = ctypes.c_size_t(0)
+    _call("scan_workspace_bytes", n, ctypes.byref(nbytes))
+    ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        _call("cumsum_tiles_hit", n, _ptr(num_tiles_hit), _ptr(cum), _ptr(total), _ptr(ws),
+              nbytes.value, _stream(dev))
+    return cum, total
+
+
+def bin_and_sort_gaussians(num_gaussians: int, num_intersects: int, tile_min, tile_max,
+                           cum_tiles_hit, vol_size):
+    """bindings.cu:259-360. Returns (gaussian_ids_sorted (I,), tile_bins (T,2))."""
+    for t, w in ((tile_min, "tile_min"), (tile_max, "tile_max"), (cum_tiles_hit, "cum_tiles_hit")):
+        _check_input(t, w)
+        _check_dtype(t, w, torch.int32)
+    Tx, Ty, Tz = _tiles(vol_size)
+    T = Tx * Ty * Tz
+    D, H, W = (int(v) for v in vol_size)
+    dev = tile_min.device
+    n, I = int(num_gaussians), int(num_intersects)
+    i32 = dict(device=dev, dtype=torch.int32)
+    tile_bins = torch.empty((T, 2), **i32)
+    ids = torch.empty((max(I, 0),), **i32)
+    nbytes = ctypes.c_size_t(0)
+    _call("bin_workspace_bytes", n, max(I, 0), D, H, W, ctypes.byref(nbytes))
+    ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        _call("bin_and_sort", n, I, _ptr(tile_min), _ptr(tile_max), _ptr(cum_tiles_hit), D, H, W,
+              _ptr(ws), nbytes.value, _ptr(ids), _ptr(tile_bins), _stream(dev))
+    return ids, tile_bins
+
+
+def _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities):
+    for t, w in ((gaussian_ids_sorted, "gaussian_ids_sorted"), (tile_bins, "tile_bins"),
+                 (pos3d, "pos3d"), (conics, "conics"), (intensities, "intensities")):
+        _check_input(t, w)
+    _check_dtype(gaussian_ids_sorted, "gaussian_ids_sorted", torch.int32)
+    _check_dtype(tile_bins, "tile_bins", torch.int32)
+    for t, w in ((pos3d, "pos3d"), (conics, "conics"), (intensities, "intensities")):
+        _check_dtype(t, w, torch.float32)
+
+
+def voxelize_forward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities):
+    """bindings.cu:362-457. Returns the (D, H, W, C) volume."""
+    _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
+    channels = _channels(intensities)
+    D, H, W = (int(v) for v in vol_size)
+    n = pos3d.size(0)
+    dev = pos3d.device
+    out = torch.empty((D, H, W, channels), device=dev, dtype=torch.float32)
+    Tx, Ty, Tz = _tiles(vol_size)
+    if tile_bins.numel() < 2 * Tx * Ty * Tz:
+        raise RuntimeError("tile_bins does not cover the volume's tile grid")
+    with torch.cuda.device(dev):
+        _call("voxelize_fwd", D, H, W, channels, n, gaussian_ids_sorted.numel(),
+              _ptr(gaussian_ids_sorted), _ptr(tile_bins), _ptr(pos3d), _ptr(conics),
+              _ptr(intensities), _ptr(out), _stream(dev))
+    return out
+
+
+def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
+                       intensities, vol_grad_in):
+    _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
+    _check_input(vol_grad_in, "vol_grad_in")
+    _check_dtype(vol_grad_in, "vol_grad_in", torch.float32)
+    channels = _channels(intensities)
+    D, H, W = (int(v) for v in vol_size)
+    if vol_grad_in.numel() != D * H * W * channels:
+        raise RuntimeError("vol_grad_in must have D*H*W*channels elements")
+    n = pos3d.size(0)
+    dev = pos3d.device
+    I = gaussian_ids_sorted.numel()
+    Tx, Ty, Tz = _tiles(vol_size)
+    if I > 0 and tile_bins.numel() < 2 * Tx * Ty * Tz:
+        raise RuntimeError("tile_bins does not cover the volume's tile grid")
+    f32 = dict(device=dev, dtype=torch.float32)
+    dpos = torch.empty((n, 4), **f32)
+    dconics = torch.empty((n, 6), **f32)
+    dint = torch.empty((n, channels), **f32)
+    nbytes = ctypes.c_size_t(0)
+    _call("voxelize_bwd_workspace_bytes", D, H, W, I, ctypes.byref(nbytes))
+    ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        _call("voxelize_bwd", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted), _ptr(tile_bins),
+              _ptr(pos3d), _ptr(conics), _ptr(intensities), _ptr(vol_grad_in), _ptr(dpos),
+              _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value, _stream(dev))
+    return dpos, dconics, dint
+
+
+def voxelize_backward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
+                      vol_grad_in):
+    """bindings.cu:459-584 (per-voxel variant). Returns (dpos3d_radii, dconics, dintensities)."""
+    return _voxelize_backward(0, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
+                              intensities, vol_grad_in)
+
+
+def voxelize_backward_per_gaussian(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
+                                   intensities, vol_grad_in):
+    """bindings.cu:586-781 (per-Gaussian variant). Returns (dpos3d_radii, dconics, dintensities)."""
+    return _voxelize_backward(1, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
+                              intensities, vol_grad_in)

@@ -1,0 +1,176 @@
+"""Seeded synthetic workloads for the five benchmark configurations.
+
+These play the role of the reference's test fixtures (test/utils.py:10-154:
+random-sphere phantom, smoothed-noise phantom, random_gauss_init) with every
+random draw taken from one CPU ``torch.Generator`` in a fixed order
+(positions, scales, quaternions, intensities, phantom), so the GPU run and any
+CPU check see bit-identical inputs.
+
+Conventions: positions are world units (x, y, z) in a world box of size
+``world`` (z, y, x) centred at ``center`` (z, y, x); a scale of "s voxels"
+on axis k means scale3d[:, k] = s * world_k / N_k.
+"""
+import math
+from dataclasses import dataclass, field
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+
+@dataclass(frozen=True)
+class Config:
+    name: str
+    vol: Tuple[int, int, int]              # (D, H, W)
+    n: int
+    channels: int
+    scale: Tuple                           # ("axis"|"iso", lo, hi) or ("mixture",)
+    quat: str                              # "random" | "identity"
+    intensity: Tuple[float, float]
+    position: str                          # "uniform" | "clustered"
+    phantom: str                           # "smooth" | "ellipsoids"
+    world: Tuple[float, float, float] = (1.0, 1.0, 1.0)
+    center: Tuple[float, float, float] = (0.5, 0.5, 0.5)
+
+
+CONFIGS: Dict[int, Config] = {
+    1: Config("cfg1_readme_100x150x80_5k", (100, 150, 80), 5_000, 1, ("axis", 0.5, 4.0), "random",
+              (0.0, 1.0), "uniform", "smooth"),
+    2: Config("cfg2_128cube_50k", (128, 128, 128), 50_000, 1, ("iso", 0.5, 3.0), "identity",
+              (0.0, 0.5), "uniform", "ellipsoids"),
+    3: Config("cfg3_256cube_200k", (256, 256, 256), 200_000, 1, ("axis", 0.5, 6.0), "random",
+              (0.0, 1.0), "uniform", "ellipsoids"),
+    4: Config("cfg4_512cube_1M", (512, 512, 512), 1_000_000, 1, ("axis", 0.5, 8.0), "random",
+              (0.0, 0.2), "uniform", "ellipsoids"),
+    5: Config("cfg5_256cube_500k_c4", (256, 256, 256), 500_000, 4, ("mixture",), "random",
+              (0.0, 1.0), "clustered", "ellipsoids"),
+}
+
+
+def _log_uniform(g, shape, lo, hi):
+    u = torch.rand(shape, generator=g, dtype=torch.float64)
+    return torch.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))
+
+
+def voxel_size_xyz(cfg: Config) -> torch.Tensor:
+    D, H, W = cfg.vol
+    wz, wy, wx = cfg.world
+    return torch.tensor([wx / W, wy / H, wz / D], dtype=torch.float64)
+
+
+@dataclass
+class Workload:
+    cfg: Config
+    pos3d: torch.Tensor
+    scale3d: torch.Tensor
+    quat: torch.Tensor
+    intensities: torch.Tensor
+    phantom_params: Optional[dict] = field(default=None)
+    seed: int = 0
+
+    def to(self, device):
+        return Workload(self.cfg, self.pos3d.to(device), self.scale3d.to(device),
+                        self.quat.to(device), self.intensities.to(device), self.phantom_params,
+                        self.seed)
+
+
+def make_gaussians(cfg: Config, seed: int = 0, n: Optional[int] = None) -> Workload:
+    """Draw the Gaussians of ``cfg`` (optionally only the first ``n``) on the CPU."""
+    n = cfg.n if n is None else int(n)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    # positions (world units, x y z)
+    if cfg.position == "uniform":
+        pos = torch.rand((n, 3), generator=g, dtype=torch.float64)
+    else:  # 16-component isotropic normal mixture, sigma 0.05, centres U[0,1]^3, unclipped
+        centres = torch.rand((16, 3), generator=g, dtype=torch.float64)
+        comp = torch.randint(0, 16, (n,), generator=g)
+        pos = centres[comp] + 0.05 * torch.randn((n, 3), generator=g, dtype=torch.float64)
+    cz, cy, cx = cfg.center
+    wz, wy, wx = cfg.world
+    origin = torch.tensor([cx - wx / 2, cy - wy / 2, cz - wz / 2], dtype=torch.float64)
+    extent = torch.tensor([wx, wy, wz], dtype=torch.float64)
+    pos = origin + pos * extent
+    # scales, in voxels, converted to world units per axis
+    kind = cfg.scale[0]
+    if kind == "axis":
+        s = _log_uniform(g, (n, 3), cfg.scale[1], cfg.scale[2])
+    elif kind == "iso":
+        s = _log_uniform(g, (n, 1), cfg.scale[1], cfg.scale[2]).expand(n, 3)
+    else:  # 90% LU[0.5,2], 10% LU[8,32] voxels, per axis
+        big = torch.rand((n,), generator=g, dtype=torch.float64) < 0.1
+        small_s = _log_uniform(g, (n, 3), 0.5, 2.0)
+        big_s = _log_uniform(g, (n, 3), 8.0, 32.0)
+        s = torch.where(big[:, None], big_s, small_s)
+    scale = s * voxel_size_xyz(cfg)
+    # rotations [w, x, y, z]
+    if cfg.quat == "random":
+        q = torch.randn((n, 4), generator=g, dtype=torch.float64)
+        q = q / q.norm(dim=1, keepdim=True)
+    else:
+        q = torch.zeros((n, 4), dtype=torch.float64)
+        q[:, 0] = 1.0
+    lo, hi = cfg.intensity
+    inten = lo + (hi - lo) * torch.rand((n, cfg.channels), generator=g, dtype=torch.float64)
+    # phantom parameters (drawn last, so they do not perturb the Gaussians)
+    params = {"kind": cfg.phantom}
+    if cfg.phantom == "ellipsoids":
+        k = 20
+        params.update(
+            centres=torch.rand((k, 3), generator=g, dtype=torch.float64),
+            semi=0.05 + 0.15 * torch.rand((k, 3), generator=g, dtype=torch.float64),
+            rot=torch.randn((k, 4), generator=g, dtype=torch.float64),
+            value=0.5 + 0.5 * torch.rand((k,), generator=g, dtype=torch.float64))
+    else:
+        params.update(noise_seed=int(torch.randint(0, 2**31 - 1, (1,), generator=g)))
+    return Workload(cfg, pos.float().contiguous(), scale.float().contiguous(),
+                    q.float().contiguous(), inten.float().contiguous(), params, seed)
+
+
+def _rotmat(q: torch.Tensor) -> torch.Tensor:
+    q = q / q.norm(dim=-1, keepdim=True)
+    w, x, y, z = q.unbind(-1)
+    return torch.stack([
+        torch.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)], -1),
+        torch.stack([2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)], -1),
+        torch.stack([2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)], -1),
+    ], -2)
+
+
+def phantom(work: Workload, device="cpu") -> torch.Tensor:
+    """Target volume (D, H, W) float32 in [0, 1] (test/utils.py:10-71 analogues)."""
+    cfg = work.cfg
+    D, H, W = cfg.vol
+    p = work.phantom_params
+    if p["kind"] == "smooth":
+        gn = torch.Generator(device="cpu").manual_seed(p["noise_seed"])
+        noise = torch.rand((1, 1, D, H, W), generator=gn, dtype=torch.float32).to(device)
+        vol = 0.1 + 0.9 * F.avg_pool3d(noise, kernel_size=5, stride=1, padding=2)
+        return vol.clamp(0.0, 1.0)[0, 0].contiguous()
+    wz, wy, wx = cfg.world
+    cz, cy, cx = cfg.center
+    vol = torch.full((D, H, W), 0.1, dtype=torch.float32, device=device)
+    xs = (cx - wx / 2) + (torch.arange(W, device=device, dtype=torch.float32) + 0.5) * (wx / W)
+    ys = (cy - wy / 2) + (torch.arange(H, device=device, dtype=torch.float32) + 0.5) * (wy / H)
+    zs = (cz - wz / 2) + (torch.arange(D, device=device, dtype=torch.float32) + 0.5) * (wz / D)
+    origin = torch.tensor([cx - wx / 2, cy - wy / 2, cz - wz / 2], dtype=torch.float64)
+    extent = torch.tensor([wx, wy, wz], dtype=torch.float64)
+    centres = (origin + p["centres"] * extent).float().to(device)
+    R = _rotmat(p["rot"]).float().to(device)
+    semi = p["semi"].float().to(device)
+    val = p["value"].float().to(device)
+    chunk = max(1, (1 << 24) // (H * W))
+    for z0 in range(0, D, chunk):
+        zz = zs[z0:z0 + chunk]
+        P = torch.stack(torch.meshgrid(xs, ys, zz, indexing="ij"), -1)  # (W, H, dz, 3)
+        acc = torch.zeros(P.shape[:3], dtype=torch.float32, device=device)
+        for e in range(centres.shape[0]):
+            d = (P - centres[e]) @ R[e]  # body-frame coordinates
+            inside = ((d / semi[e]) ** 2).sum(-1) <= 1.0
+            acc += inside.float() * val[e]
+        vol[z0:z0 + chunk] += acc.permute(2, 1, 0)
+    return vol.clamp_(0.0, 1.0)
+
+
+def tile_grid(vol):
+    D, H, W = vol
+    return (W + 7) // 8, (H + 7) // 8, (D + 7) // 8

@@ -1,0 +1,143 @@
+/*
+ * gsvox.h — C ABI of libgsvox.so, the gfx950 Gaussian voxelizer.
+ *
+ * Drop-in boundary for the reference's native module `gs_voxelizer.cuda`
+ * (PaPieta/gs-voxelizer v0.1.0, gs_voxelizer/cuda/ext.cpp:4-11, signatures in
+ * gs_voxelizer/cuda/bindings.h:40-194).  The reference binds torch tensors with
+ * pybind11 and allocates its outputs; this ABI takes plain device pointers and
+ * sizes instead, the caller allocates every output and workspace, and each call
+ * only enqueues work on `stream` (a hipStream_t; NULL = the default stream).
+ *
+ * Conventions shared by every entry point
+ *   - Volume tuples are (z, y, x) = (D, H, W); pos3d / scale3d / tile indices
+ *     are (x, y, z); quat is [w, x, y, z]; the volume is (D, H, W, C) row-major.
+ *   - All arrays are contiguous, device-resident, 4-byte aligned; pos3d_radii
+ *     rows are float4 (16-byte aligned); conics rows are 6 floats (8-byte aligned).
+ *   - Return value: GSV_OK (0) or a gsv_status code; nothing is ever printed and
+ *     the process is never terminated.  A HIP launch error is reported as
+ *     GSV_ERR_HIP; gsv_last_hip_error() returns the underlying hipError_t.
+ *   - Outputs are fully written (zero where the reference zero-fills) with
+ *     kernels, never hipMemset, so a caller may capture the calls in a graph.
+ *   - Calls are stateless and may be issued from any host thread; calls on one
+ *     stream execute in order.
+ */
+#ifndef GSVOX_H
+#define GSVOX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum gsv_status {
+    GSV_OK = 0,
+    GSV_ERR_INVALID_ARGUMENT = 1,   /* negative size, NULL pointer, bad variant */
+    GSV_ERR_UNSUPPORTED_CHANNELS = 2, /* channels outside [1, 4] (bindings.cu:61-63) */
+    GSV_ERR_WORKSPACE_TOO_SMALL = 3,
+    GSV_ERR_SIZE_OVERFLOW = 4,      /* an index would not fit the int32 layout */
+    GSV_ERR_HIP = 5                 /* a HIP runtime call or launch failed */
+} gsv_status;
+
+/* Library version, MAJOR*10000 + MINOR*100 + PATCH. */
+int gsv_version(void);
+
+/* Human-readable text for a gsv_status value (static storage). */
+const char *gsv_status_string(int status);
+
+/* hipError_t of the most recent failing HIP call made by this thread. */
+int gsv_last_hip_error(void);
+
+/*
+ * Projection forward: optimisation parameters -> rendering parameters.
+ * Replaces optim_to_render_forward_torch (bindings.cu:38-189; kernel
+ * optim_to_render.cu:48-172).  Outputs per Gaussian: pos3d_radii (n,4) = voxel
+ * position xyz + integer-valued radius, conics (n,6) = inverse covariance
+ * (00,01,02,11,12,22) in voxel units, tile_min / tile_max (n,3) int32 [min, max)
+ * tile box, num_tiles_hit (n,) int32.  Culled Gaussians get all-zero rows.
+ * intensities is (n, channels); channels in [1, 4].
+ */
+int gsv_project_fwd(int32_t n, int32_t channels, const float *pos3d, const float *scale3d,
+                    const float *quat, const float *intensities, int32_t D, int32_t H, int32_t W,
+                    float world_z, float world_y, float world_x, float center_z, float center_y,
+                    float center_x, float *pos3d_radii, float *conics, int32_t *tile_min,
+                    int32_t *tile_max, int32_t *num_tiles_hit, void *stream);
+
+/*
+ * Projection backward.  Replaces optim_to_render_backward_torch
+ * (bindings.cu:197-251; kernel optim_to_render.cu:246-336).  Gradients w.r.t.
+ * pos3d (n,3), scale3d (n,3), quat (n,4) from the gradients of pos3d_radii (n,4)
+ * and conics (n,6); rows whose pos3d_radii[:,3] <= 0 get zeros.  Same formulas
+ * as the reference: dpos = dpix * voxel_size, dquat without the normalisation
+ * Jacobian, 1e-7 regulariser on det^2.
+ */
+int gsv_project_bwd(int32_t n, const float *pos3d, const float *scale3d, const float *quat,
+                    int32_t D, int32_t H, int32_t W, float world_z, float world_y, float world_x,
+                    float center_z, float center_y, float center_x, const float *dpos3d_radii,
+                    const float *dconics, const float *pos3d_radii, float *dpos3d,
+                    float *dscale3d, float *dquat, void *stream);
+
+/*
+ * Inclusive int32 prefix sum of num_tiles_hit.  Replaces the
+ * `torch.cumsum(num_tiles_hit, dim=0, dtype=torch.int32)` of voxelize.py:87.
+ * If total_out is non-NULL the last element (the intersection count) is also
+ * written to that device int64, so a caller can read one scalar.
+ * Workspace size from gsv_scan_workspace_bytes.
+ */
+int gsv_scan_workspace_bytes(int64_t n, size_t *bytes);
+int gsv_cumsum_tiles_hit(int32_t n, const int32_t *num_tiles_hit, int32_t *cum_tiles_hit,
+                         int64_t *total_out, void *workspace, size_t workspace_bytes,
+                         void *stream);
+
+/*
+ * Binning.  Replaces bin_and_sort_gaussians_torch (bindings.cu:259-360):
+ * map_gaussian_to_intersects (bin_and_sort_gaussians.cu:11-35), the stable
+ * 32-bit CUB radix sort (bindings.cu:313-345) and get_tile_bin_edges
+ * (bin_and_sort_gaussians.cu:40-62).  Outputs gaussian_ids_sorted (I,) int32,
+ * ordered by (tile id, gaussian id), and tile_bins (T,2) int32 [start, end)
+ * with (0,0) for empty tiles, T = ceil(W/8)*ceil(H/8)*ceil(D/8).
+ * cum_tiles_hit is the inclusive scan of the per-Gaussian tile counts and must
+ * end at num_intersects.  num_intersects <= 0 only zero-fills tile_bins.
+ */
+int gsv_bin_workspace_bytes(int32_t n, int64_t num_intersects, int32_t D, int32_t H, int32_t W,
+                            size_t *bytes);
+int gsv_bin_and_sort(int32_t n, int64_t num_intersects, const int32_t *tile_min,
+                     const int32_t *tile_max, const int32_t *cum_tiles_hit, int32_t D, int32_t H,
+                     int32_t W, void *workspace, size_t workspace_bytes,
+                     int32_t *gaussian_ids_sorted, int32_t *tile_bins, void *stream);
+
+/*
+ * Forward voxelization.  Replaces voxelize_forward_torch (bindings.cu:362-457;
+ * kernel voxelize.cu:39-164).  volume (D,H,W,channels) float32 is fully written.
+ * n = number of Gaussians (rows of pos3d_radii / conics / intensities).
+ */
+int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                     int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                     const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
+                     const float *intensities, float *volume, void *stream);
+
+/*
+ * Backward voxelization.  Replaces voxelize_backward_per_gaussian_torch
+ * (bindings.cu:586-781; kernel voxelize.cu:368-574) when variant = 1 and
+ * voxelize_backward_torch (bindings.cu:459-584; kernel voxelize.cu:170-366)
+ * when variant = 0.  Both variants compute the same gradients (up to float
+ * summation order); this library serves both with one kernel.  Outputs
+ * dpos3d_radii (n,4) (column 3 stays 0), dconics (n,6), dintensities
+ * (n,channels), all fully written.  No host synchronisation happens inside.
+ * Workspace size from gsv_voxelize_bwd_workspace_bytes.
+ */
+int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W, int64_t num_intersects,
+                                     size_t *bytes);
+int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                     int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                     const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
+                     const float *intensities, const float *vol_grad, float *dpos3d_radii,
+                     float *dconics, float *dintensities, int32_t variant, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSVOX_H */

@@ -1,0 +1,26 @@
+"""Test setup: import paths and the `gpu` marker.
+
+`-m "not gpu"` runs on any machine (oracle pinning, host logic, C-ABI loading);
+`-m gpu` runs the HIP parity tests on an MI355X.
+"""
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for p in (os.path.join(ROOT, "gs-voxelizer_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X); parity against the oracle")
+
+
+@pytest.fixture(scope="session")
+def device():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device visible")
+    return torch.device("cuda:0")
