@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Benchmark: one full differentiable voxelization iteration on one MI355X.
+
+A step is the reference's training iteration through the drop-in API
+(README.md:28-83 of PaPieta/gs-voxelizer): optim_to_render -> voxelize_gaussians
+-> L1 loss against the phantom -> loss.backward() (voxelize backward +
+projection backward), on the headline workload of BASELINE.json: 256^3 volume,
+200,000 Gaussians, 1 channel, synthetic seeded inputs already resident in HBM.
+
+Prints one JSON line.  `value` is ms per iteration (lower is better).  The
+`roofline` object reports the dominant kernel (voxelize backward), timed with
+HIP events recorded on the stream it is launched on, against the FP32 vector
+peak; `cpu_baseline` times the CPU oracle (a binary32 C restatement of the
+reference, OpenMP over the host cores) on the same inputs.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 3]
+                       [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gs-voxelizer_amd"))
+
+METRIC = "voxelize fwd+bwd ms/iter @256^3,200k G; Gaussian-voxel evals/s; % FP32 peak"
+FP32_PEAK_TFLOPS = 157.3   # MI355X vector FP32, AMD published
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, AMD published
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, help="workload number 1-5 (BASELINE.json)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one elementwise kernel that reads and writes 256 MiB (a "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    return ap.parse_args()
+
+
+class KernelTimer:
+    """Wraps native entry points of gs_voxelizer.cuda and records HIP events on
+    the current stream (the one the kernels are launched on) around each call."""
+
+    def __init__(self, module, names):
+        import torch
+        self.torch = torch
+        self.module = module
+        self.names = names
+        self.orig = {n: getattr(module, n) for n in names}
+        self.events = {n: [] for n in names}
+        self.active = False
+
+    def install(self):
+        for n in self.names:
+            fn = self.orig[n]
+
+            def wrapped(*a, __fn=fn, __n=n, **k):
+                if not self.active:
+                    return __fn(*a, **k)
+                s = self.torch.cuda.Event(enable_timing=True)
+                e = self.torch.cuda.Event(enable_timing=True)
+                s.record()
+                out = __fn(*a, **k)
+                e.record()
+                self.events[__n].append((s, e))
+                return out
+            setattr(self.module, n, wrapped)
+
+    def uninstall(self):
+        for n, fn in self.orig.items():
+            setattr(self.module, n, fn)
+
+    def mean_ms(self, n):
+        ev = self.events[n]
+        if not ev:
+            return None
+        return sum(s.elapsed_time(e) for s, e in ev) / len(ev)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is "
+                                   "designed (DESIGN.md) but not built", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    import torch.nn.functional as F
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device visible"}))
+        sys.exit(1)
+    import gs_voxelizer.cuda as _C
+    from gs_voxelizer import optim_to_render, synthetic as S, voxelize
+
+    dev = torch.device("cuda:0")
+    cfg = S.CONFIGS[args.config]
+    work = S.make_gaussians(cfg, seed=args.seed)
+    target = S.phantom(work, device=dev)
+    w = work.to(dev)
+    leaves = [t.clone().requires_grad_() for t in (w.pos3d, w.scale3d, w.quat, w.intensities)]
+    tgt = target[..., None].expand(cfg.vol + (cfg.channels,))
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        pos3d, scale3d, quat, inten = leaves
+        pr, cn, tmin, tmax, nt = optim_to_render.optim_to_render(
+            pos3d, scale3d, quat, inten, cfg.vol, cfg.world, cfg.center)
+        vol = voxelize.voxelize_gaussians(pr, cn, inten, cfg.vol, tmin, tmax, nt,
+                                          use_per_gaussian_backward=True)
+        loss = F.l1_loss(vol, tgt)
+        loss.backward()
+        return vol
+
+    # workload statistics (intersections, evaluations) from one untimed pass
+    with torch.no_grad():
+        pr, cn, tmin, tmax, nt = _C.optim_to_render_forward(cfg.n, w.pos3d, w.scale3d, w.quat,
+                                                            w.intensities, cfg.vol, cfg.world,
+                                                            cfg.center)
+        cum, total = _C.cumsum_tiles_hit(nt)
+        n_isect = int(total.item())
+        ids, bins = _C.bin_and_sort_gaussians(cfg.n, n_isect, tmin, tmax, cum, cfg.vol)
+        D, H, W = cfg.vol
+        Tx, Ty, Tz = S.tile_grid(cfg.vol)
+        t = torch.arange(Tx * Ty * Tz, device=dev)
+        inside = ((torch.clamp(W - (t % Tx) * 8, max=8)) * (torch.clamp(H - ((t // Tx) % Ty) * 8, max=8))
+                  * (torch.clamp(D - (t // (Tx * Ty)) * 8, max=8)))
+        evals = int(((bins[:, 1] - bins[:, 0]).long() * inside).sum().item())
+        del pr, cn, tmin, tmax, nt, cum, ids, bins
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    timer = KernelTimer(_C, ["optim_to_render_forward", "cumsum_tiles_hit", "bin_and_sort_gaussians",
+                             "voxelize_forward", "voxelize_backward_per_gaussian",
+                             "optim_to_render_backward"])
+    timer.install()
+    timer.active = True
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    timer.active = False
+    timer.uninstall()
+    ms = (t1 - t0) * 1e3 / args.steps
+
+    C = cfg.channels
+    fwd_ms = timer.mean_ms("voxelize_forward")
+    bwd_ms = timer.mean_ms("voxelize_backward_per_gaussian")
+    fwd_flops = evals * (22 + 2 * C)
+    bwd_flops = evals * (65 + 4 * C)
+    stages = {k: round(timer.mean_ms(k), 4) for k in timer.names if timer.mean_ms(k) is not None}
+    bwd_tflops = bwd_flops / (bwd_ms * 1e-3) / 1e12
+    fwd_tflops = fwd_flops / (fwd_ms * 1e-3) / 1e12
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{cfg.name}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("voxelize_backward_hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(ms, 4),
+        "unit": "ms/iter",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded CPU torch.Generator, inputs resident in HBM)",
+        "config": {"workload": cfg.name, "volume_zyx": list(cfg.vol), "gaussians": cfg.n,
+                   "channels": C, "intersections": n_isect, "evals": evals,
+                   "loss": f"l1 vs {cfg.phantom} phantom", "seed": args.seed,
+                   "step": "optim_to_render + voxelize_gaussians + l1 + backward"},
+        "evals_per_s": round(2 * evals / (ms * 1e-3), 1),
+        "fwd_evals_per_s": round(evals / (fwd_ms * 1e-3), 1),
+        "bwd_evals_per_s": round(evals / (bwd_ms * 1e-3), 1),
+        "fwd_ms": round(fwd_ms, 4),
+        "bwd_ms": round(bwd_ms, 4),
+        "fwd_fp32_peak_frac": round(fwd_tflops / FP32_PEAK_TFLOPS, 4),
+        "bwd_fp32_peak_frac": round(bwd_tflops / FP32_PEAK_TFLOPS, 4),
+        "stage_ms": stages,
+        "roofline": {"kernel": "k_vox_bwd (voxelize backward)", "bound": "valu",
+                     "achieved": round(bwd_tflops, 3), "peak": FP32_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(bwd_tflops / FP32_PEAK_TFLOPS, 4),
+                     "traffic": traffic,
+                     "flops_per_launch": bwd_flops, "flops_per_eval": 65 + 4 * C},
+        "cpu_baseline": None,
+    }
+    if args.calibrate_copy:
+        # an elementwise kernel that reads 256 MiB and writes 256 MiB (a plain
+        # hipMemcpy D2D may run on a DMA engine, invisible to the counters)
+        src = torch.ones((64 << 20,), device=dev)
+        dst = torch.empty_like(src)
+        torch.mul(src, 2.0, out=dst)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = src.numel() * 4
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(work)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(work, repeats=3):
+    """The CPU oracle (test infrastructure: binary32 C restatement of the
+    reference, OpenMP over all host cores) on the same inputs: one whole
+    iteration (projection, binning, voxelize forward, voxelize backward,
+    projection backward), median of `repeats` after one warm-up on a slice."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+    import oracle as O
+    cfg = work.cfg
+    p, s, q, I = (t.numpy() for t in (work.pos3d, work.scale3d, work.quat, work.intensities))
+    g = np.full(cfg.vol + (cfg.channels,), 1.0 / np.prod(cfg.vol), np.float32)
+
+    def one(tile_range=None):
+        tm = {}
+        t0 = time.perf_counter()
+        pr, cn, tmin, tmax, nt = O.project_fwd(p, s, q, I, cfg.vol, cfg.world, cfg.center)
+        cum = O.cumsum(nt)
+        ids, bins = O.bin_and_sort(cfg.n, int(cum[-1]), tmin, tmax, cum, cfg.vol)
+        t1 = time.perf_counter()
+        O.voxelize_fwd(cfg.vol, ids, bins, pr, cn, I, tile_range=tile_range)
+        t2 = time.perf_counter()
+        dpr, dcn, _ = O.voxelize_bwd(cfg.vol, ids, bins, pr, cn, I, g, tile_range=tile_range)
+        t3 = time.perf_counter()
+        O.project_bwd(p, s, q, cfg.vol, cfg.world, cfg.center, dpr, dcn, pr)
+        t4 = time.perf_counter()
+        tm.update(project_and_bin=t1 - t0, voxelize_fwd=t2 - t1, voxelize_bwd=t3 - t2,
+                  project_bwd=t4 - t3, total=t4 - t0)
+        return tm
+
+    Tx, Ty, _ = O.tile_grid(cfg.vol)
+    one(tile_range=(0, Tx * Ty))  # warm-up: page in, spin up the thread pool
+    runs = sorted((one() for _ in range(repeats)), key=lambda r: r["total"])
+    med = runs[len(runs) // 2]
+    return {"value": round(med["total"] * 1e3, 1), "unit": "ms/iter", "cores": O.num_threads(),
+            "kind": "port",
+            "sample": (f"the whole {cfg.name} iteration (no subsampling) through oracle/gsv_oracle.c, "
+                       f"a binary32 C restatement of the reference (OpenMP); median of {repeats}"),
+            "measured_s": {k: round(v, 3) for k, v in med.items()},
+            "cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+if __name__ == "__main__":
+    main()

@@ -231,7 +231,9 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
     const float2 *__restrict__ conics, const float *__restrict__ intens,
     const float *__restrict__ vol_grad, const int *__restrict__ bucket_tile,
     const int *__restrict__ bucket_off, const int64_t *__restrict__ total_buckets, int64_t cap,
-    float *__restrict__ dpos, float *__restrict__ dconic, float *__restrict__ dint) {
+    float *__restrict__ dpos, float *__restrict__ dconic, float *__restrict__ dint,
+    const int *__restrict__ tile_min, const int *__restrict__ tile_max,
+    const int *__restrict__ cum, float *__restrict__ partial) {
     __shared__ float4 s_g[kWave][2 * C];  // vol_grad of the tile: row (ly + 8*lz), 8*C floats
     const int64_t total = min<int64_t>(*total_buckets, cap);
     const int64_t per = xcd_per(total);
@@ -298,7 +300,8 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
         }
     }
     __syncthreads();
-    if (!__any(live)) return;
+    const bool any_live = __any(live);
+    if (!any_live && partial == nullptr) return;
 
     const float A2 = -0.5f * kLog2e * ca, Bn = -kLog2e * cb, Cn = -kLog2e * cc;
     const float Dn = -0.5f * kLog2e * cd, En = -kLog2e * ce, Fn = -0.5f * kLog2e * cf;
@@ -310,7 +313,7 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
 #pragma unroll
     for (int c = 0; c < C; ++c) dIa[c] = 0.f;
 
-    const int ny = min(GSV_TILE, H - tg.y0), nz = min(GSV_TILE, D - tg.z0);
+    const int ny = min(GSV_TILE, H - tg.y0), nz = any_live ? min(GSV_TILE, D - tg.z0) : 0;
     for (int lz = 0; lz < nz; ++lz) {
         const float dz = mzl - ((float)lz + 0.5f);
         const float Cdz = Cn * dz, Edz = En * dz;
@@ -362,38 +365,92 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
             Szz = fmaf(t1, dz, Szz);
         }
     }
-    if (live) {
-        // sigma-gradient weight per unit of h: alpha = scale * a
-        const float w = (C == 1) ? gt.scale * I[0] : gt.scale;
-        float *dc = dconic + 6 * (size_t)g;
-        unsafeAtomicAdd(dc + 0, -0.5f * w * Sxx);
-        unsafeAtomicAdd(dc + 1, -w * Sxy);
-        unsafeAtomicAdd(dc + 2, -w * Sxz);
-        unsafeAtomicAdd(dc + 3, -0.5f * w * Syy);
-        unsafeAtomicAdd(dc + 4, -w * Syz);
-        unsafeAtomicAdd(dc + 5, -0.5f * w * Szz);
-        float *dp = dpos + 4 * (size_t)g;
-        unsafeAtomicAdd(dp + 0, -w * (ca * Sx + cb * Sy + cc * Sz));
-        unsafeAtomicAdd(dp + 1, -w * (cb * Sx + cd * Sy + ce * Sz));
-        unsafeAtomicAdd(dp + 2, -w * (cc * Sx + ce * Sy + cf * Sz));
-        float *di = dint + (size_t)C * g;
-        if (C == 1) {
-            unsafeAtomicAdd(di, gt.scale * S0);
-        } else {
+    // sigma-gradient weight per unit of h: alpha = scale * a
+    const float w = live ? ((C == 1) ? gt.scale * I[0] : gt.scale) : 0.f;
+    float out[9 + C];
+    out[0] = -0.5f * w * Sxx;
+    out[1] = -w * Sxy;
+    out[2] = -w * Sxz;
+    out[3] = -0.5f * w * Syy;
+    out[4] = -w * Syz;
+    out[5] = -0.5f * w * Szz;
+    out[6] = -w * (ca * Sx + cb * Sy + cc * Sz);
+    out[7] = -w * (cb * Sx + cd * Sy + ce * Sz);
+    out[8] = -w * (cc * Sx + ce * Sy + cf * Sz);
+    const float sc = live ? gt.scale : 0.f;
+    if (C == 1) {
+        out[9] = sc * S0;
+    } else {
 #pragma unroll
-            for (int c = 0; c < C; ++c) unsafeAtomicAdd(di + c, gt.scale * dIa[c]);
+        for (int c = 0; c < C; ++c) out[9 + c] = sc * dIa[c];
+    }
+    if (partial != nullptr) {
+        // Deterministic path: this pair's partial goes to its emission slot
+        // e = cum[g-1] + ((tz-min.z)*ny + (ty-min.y))*nx + (tx-min.x), the order
+        // the pairs were duplicated in (gaussian-major, tiles z->y->x), so each
+        // Gaussian's partials are contiguous for the reduction pass.
+        if (idx < range.y && (unsigned)g < (unsigned)n) {
+            const int tx = tg.x0 / GSV_TILE, ty = tg.y0 / GSV_TILE, tz = tg.z0 / GSV_TILE;
+            const int mnx = tile_min[3 * g], mny = tile_min[3 * g + 1], mnz = tile_min[3 * g + 2];
+            const int nxb = tile_max[3 * g] - mnx, nyb = tile_max[3 * g + 1] - mny;
+            const int64_t base = g == 0 ? 0 : cum[g - 1];
+            const int64_t e = base + ((int64_t)(tz - mnz) * nyb + (ty - mny)) * nxb + (tx - mnx);
+            if (e >= base && e < (int64_t)cum[g] && e < n_isect) {
+                float *dst = partial + e * (9 + C);
+#pragma unroll
+                for (int q = 0; q < 9 + C; ++q) dst[q] = out[q];
+            }
         }
+    } else if (live) {
+        float *dc = dconic + 6 * (size_t)g;
+#pragma unroll
+        for (int q = 0; q < 6; ++q) unsafeAtomicAdd(dc + q, out[q]);
+        float *dp = dpos + 4 * (size_t)g;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) unsafeAtomicAdd(dp + q, out[6 + q]);
+        float *di = dint + (size_t)C * g;
+#pragma unroll
+        for (int c = 0; c < C; ++c) unsafeAtomicAdd(di + c, out[9 + c]);
     }
 }
 
+// Deterministic reduction of the per-pair partials: Gaussian g sums its slots
+// [cum[g-1], cum[g]) in emission order and writes every output element.
+template <int C>
+__global__ __launch_bounds__(256) void k_pair_reduce(int n, int n_isect, const int *__restrict__ cum,
+                                                     const float *__restrict__ partial,
+                                                     float *__restrict__ dpos,
+                                                     float *__restrict__ dconic,
+                                                     float *__restrict__ dint) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n) return;
+    const int64_t b = g == 0 ? 0 : max(0, cum[g - 1]);
+    const int64_t e = min<int64_t>(cum[g], n_isect);
+    float acc[9 + C];
+#pragma unroll
+    for (int q = 0; q < 9 + C; ++q) acc[q] = 0.f;
+    for (int64_t k = b; k < e; ++k) {
+        const float *src = partial + k * (9 + C);
+#pragma unroll
+        for (int q = 0; q < 9 + C; ++q) acc[q] += src[q];
+    }
+    float2 *dc = reinterpret_cast<float2 *>(dconic + 6 * (size_t)g);
+    dc[0] = make_float2(acc[0], acc[1]);
+    dc[1] = make_float2(acc[2], acc[3]);
+    dc[2] = make_float2(acc[4], acc[5]);
+    reinterpret_cast<float4 *>(dpos)[g] = make_float4(acc[6], acc[7], acc[8], 0.f);
+#pragma unroll
+    for (int c = 0; c < C; ++c) dint[(size_t)C * g + c] = acc[9 + c];
+}
+
 struct BwdLayout {
-    size_t counts, offs, scan, total, btile, end;
+    size_t counts, offs, scan, total, btile, partial, end;
     int64_t cap;
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-BwdLayout bwd_layout(int64_t T, int64_t n_isect) {
+BwdLayout bwd_layout(int64_t T, int64_t n_isect, int channels, bool pairs) {
     BwdLayout L{};
     L.cap = imin64(T, n_isect) + (n_isect + kBucket - 1) / kBucket;
     size_t off = 0;
@@ -402,6 +459,8 @@ BwdLayout bwd_layout(int64_t T, int64_t n_isect) {
     L.scan = off; off += scan_workspace_bytes(T);
     L.total = off; off += 256;
     L.btile = off; off += align256((size_t)imax64(L.cap, 1) * 4);
+    L.partial = off;
+    if (pairs) off += align256((size_t)n_isect * (9 + channels) * 4);
     L.end = off;
     return L;
 }
@@ -448,10 +507,12 @@ extern "C" int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channel
 }
 
 extern "C" int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W,
-                                                int64_t num_intersects, size_t *bytes) {
+                                                int32_t channels, int64_t num_intersects,
+                                                int32_t deterministic, size_t *bytes) {
     if (!bytes || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
+    if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
     const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
-    *bytes = bwd_layout(T, num_intersects > 0 ? num_intersects : 0).end;
+    *bytes = bwd_layout(T, num_intersects > 0 ? num_intersects : 0, channels, deterministic != 0).end;
     return GSV_OK;
 }
 
@@ -459,32 +520,41 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
                                 int64_t num_intersects, const int32_t *gaussian_ids_sorted,
                                 const int32_t *tile_bins, const float *pos3d_radii,
                                 const float *conics, const float *intensities,
-                                const float *vol_grad, float *dpos3d_radii, float *dconics,
-                                float *dintensities, int32_t variant, void *workspace,
-                                size_t workspace_bytes, void *stream) {
+                                const float *vol_grad, const int32_t *tile_min,
+                                const int32_t *tile_max, const int32_t *cum_tiles_hit,
+                                float *dpos3d_radii, float *dconics, float *dintensities,
+                                int32_t variant, void *workspace, size_t workspace_bytes,
+                                void *stream) {
     if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
     if (n < 0 || D <= 0 || H <= 0 || W <= 0 || (variant != 0 && variant != 1))
         return GSV_ERR_INVALID_ARGUMENT;
     if (n == 0) return GSV_OK;
     if (!dpos3d_radii || !dconics || !dintensities) return GSV_ERR_INVALID_ARGUMENT;
+    const bool pairs = tile_min && tile_max && cum_tiles_hit;
+    if (!pairs && (tile_min || tile_max || cum_tiles_hit)) return GSV_ERR_INVALID_ARGUMENT;
     hipStream_t s = as_stream(stream);
-    if (int st = fill_zero_u32(dpos3d_radii, 4 * (int64_t)n, s)) return st;
-    if (int st = fill_zero_u32(dconics, 6 * (int64_t)n, s)) return st;
-    if (int st = fill_zero_u32(dintensities, (int64_t)channels * n, s)) return st;
+    if (num_intersects <= 0 || !pairs) {
+        if (int st = fill_zero_u32(dpos3d_radii, 4 * (int64_t)n, s)) return st;
+        if (int st = fill_zero_u32(dconics, 6 * (int64_t)n, s)) return st;
+        if (int st = fill_zero_u32(dintensities, (int64_t)channels * n, s)) return st;
+    }
     if (num_intersects <= 0) return GSV_OK;
     if (!gaussian_ids_sorted || !tile_bins || !pos3d_radii || !conics || !intensities || !vol_grad)
         return GSV_ERR_INVALID_ARGUMENT;
-    if (!aligned(pos3d_radii, 16) || !aligned(conics, 8)) return GSV_ERR_INVALID_ARGUMENT;
+    if (!aligned(pos3d_radii, 16) || !aligned(conics, 8) || !aligned(dpos3d_radii, 16) ||
+        !aligned(dconics, 8))
+        return GSV_ERR_INVALID_ARGUMENT;
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
     const int64_t T = (int64_t)Tx * Ty * Tz;
     if (T > INT32_MAX || num_intersects > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
-    const BwdLayout L = bwd_layout(T, num_intersects);
+    const BwdLayout L = bwd_layout(T, num_intersects, channels, pairs);
     if (!workspace || workspace_bytes < L.end) return GSV_ERR_WORKSPACE_TOO_SMALL;
     char *ws = static_cast<char *>(workspace);
     int *counts = reinterpret_cast<int *>(ws + L.counts);
     int *offs = reinterpret_cast<int *>(ws + L.offs);
     int64_t *total = reinterpret_cast<int64_t *>(ws + L.total);
     int *btile = reinterpret_cast<int *>(ws + L.btile);
+    float *partial = pairs ? reinterpret_cast<float *>(ws + L.partial) : nullptr;
     const unsigned tb = (unsigned)((T + 255) / 256);
     hipLaunchKernelGGL(k_bucket_counts, dim3(tb), dim3(256), 0, s,
                        reinterpret_cast<const int2 *>(tile_bins), T, counts);
@@ -494,18 +564,24 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
     hipLaunchKernelGGL(k_bucket_fill, dim3(tb), dim3(256), 0, s, counts, offs, T, L.cap, btile);
     if (int st = check_launch()) return st;
     const dim3 grid((unsigned)(L.cap + kXcds)), block(kWave);
+    const int ni = (int)num_intersects;
 #define GSV_VB(CH)                                                                                  \
-    hipLaunchKernelGGL(k_vox_bwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, n, (int)num_intersects,   \
-                       gaussian_ids_sorted,                                                         \
-                       reinterpret_cast<const int2 *>(tile_bins),                                   \
+    hipLaunchKernelGGL(k_vox_bwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, n, ni,                    \
+                       gaussian_ids_sorted, reinterpret_cast<const int2 *>(tile_bins),              \
                        reinterpret_cast<const float4 *>(pos3d_radii),                               \
                        reinterpret_cast<const float2 *>(conics), intensities, vol_grad, btile,      \
-                       offs, total, L.cap, dpos3d_radii, dconics, dintensities)
+                       offs, total, L.cap, dpos3d_radii, dconics, dintensities, tile_min,           \
+                       tile_max, cum_tiles_hit, partial);                                           \
+    if (int st = check_launch()) return st;                                                         \
+    if (pairs) {                                                                                    \
+        hipLaunchKernelGGL(k_pair_reduce<CH>, dim3((n + 255) / 256), dim3(256), 0, s, n, ni,        \
+                           cum_tiles_hit, partial, dpos3d_radii, dconics, dintensities);            \
+    }
     switch (channels) {
-        case 1: GSV_VB(1); break;
-        case 2: GSV_VB(2); break;
-        case 3: GSV_VB(3); break;
-        default: GSV_VB(4); break;
+        case 1: { GSV_VB(1) break; }
+        case 2: { GSV_VB(2) break; }
+        case 3: { GSV_VB(3) break; }
+        default: { GSV_VB(4) break; }
     }
 #undef GSV_VB
     return check_launch();

@@ -193,8 +193,18 @@ def voxelize_forward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, in
 
 
 def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
-                       intensities, vol_grad_in):
+                       intensities, vol_grad_in, tile_min=None, tile_max=None,
+                       cum_tiles_hit=None):
     _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
+    given = [t is not None for t in (tile_min, tile_max, cum_tiles_hit)]
+    if any(given) and not all(given):
+        raise RuntimeError("tile_min, tile_max and cum_tiles_hit must be given together")
+    deterministic = all(given)
+    if deterministic:
+        for t, w in ((tile_min, "tile_min"), (tile_max, "tile_max"),
+                     (cum_tiles_hit, "cum_tiles_hit")):
+            _check_input(t, w)
+            _check_dtype(t, w, torch.int32)
     _check_input(vol_grad_in, "vol_grad_in")
     _check_dtype(vol_grad_in, "vol_grad_in", torch.float32)
     channels = _channels(intensities)
@@ -212,24 +222,36 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
     dconics = torch.empty((n, 6), **f32)
     dint = torch.empty((n, channels), **f32)
     nbytes = ctypes.c_size_t(0)
-    _call("voxelize_bwd_workspace_bytes", D, H, W, I, ctypes.byref(nbytes))
+    _call("voxelize_bwd_workspace_bytes", D, H, W, channels, I, int(deterministic),
+          ctypes.byref(nbytes))
     ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
+    null = ctypes.c_void_p(0)
+    boxes = ((_ptr(tile_min), _ptr(tile_max), _ptr(cum_tiles_hit)) if deterministic
+             else (null, null, null))
     with torch.cuda.device(dev):
         _call("voxelize_bwd", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted), _ptr(tile_bins),
-              _ptr(pos3d), _ptr(conics), _ptr(intensities), _ptr(vol_grad_in), _ptr(dpos),
-              _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value, _stream(dev))
+              _ptr(pos3d), _ptr(conics), _ptr(intensities), _ptr(vol_grad_in), *boxes,
+              _ptr(dpos), _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value,
+              _stream(dev))
     return dpos, dconics, dint
 
 
 def voxelize_backward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
-                      vol_grad_in):
-    """bindings.cu:459-584 (per-voxel variant). Returns (dpos3d_radii, dconics, dintensities)."""
+                      vol_grad_in, tile_min=None, tile_max=None, cum_tiles_hit=None):
+    """bindings.cu:459-584 (per-voxel variant). Returns (dpos3d_radii, dconics, dintensities).
+
+    The optional tile_min / tile_max / cum_tiles_hit (the projection's tile boxes
+    and the prefix sum used for binning) select the atomic-free, bitwise
+    reproducible reduction; without them float atomics are used, as in the
+    reference."""
     return _voxelize_backward(0, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
-                              intensities, vol_grad_in)
+                              intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit)
 
 
 def voxelize_backward_per_gaussian(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
-                                   intensities, vol_grad_in):
-    """bindings.cu:586-781 (per-Gaussian variant). Returns (dpos3d_radii, dconics, dintensities)."""
+                                   intensities, vol_grad_in, tile_min=None, tile_max=None,
+                                   cum_tiles_hit=None):
+    """bindings.cu:586-781 (per-Gaussian variant). Returns (dpos3d_radii, dconics, dintensities).
+    Optional arguments as in voxelize_backward."""
     return _voxelize_backward(1, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
-                              intensities, vol_grad_in)
+                              intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit)

@@ -65,6 +65,7 @@ class _VoxelizeGaussians(Function):
         ctx.use_per_gaussian_backward = use_per_gaussian_backward
         dev = pos3d_radii.device
         D, H, W = (int(v) for v in vol_size_voxel)
+        boxes = ()
         if num_gaussians == 0:
             out = torch.zeros(D, H, W, intensities.shape[-1], device=dev, dtype=pos3d_radii.dtype)
             gaussian_ids_sorted = torch.zeros(0, 1, device=dev, dtype=torch.int32)
@@ -87,13 +88,19 @@ class _VoxelizeGaussians(Function):
                     vol_size_voxel)
                 out = _C.voxelize_forward(vol_size_voxel, gaussian_ids_sorted, tile_bins,
                                           pos3d_radii, conics, intensities)
-        ctx.save_for_backward(pos3d_radii, conics, intensities, gaussian_ids_sorted, tile_bins)
+                # the backward reduces per-pair partials in duplication order (no atomics)
+                boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit)
+        ctx.n_boxes = len(boxes)
+        ctx.save_for_backward(pos3d_radii, conics, intensities, gaussian_ids_sorted, tile_bins,
+                              *boxes)
         return out
 
     @staticmethod
     def backward(ctx, vol_grad):
         vol_size_voxel = ctx.vol_size_voxel
-        pos3d_radii, conics, intensities, gaussian_ids_sorted, tile_bins = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        pos3d_radii, conics, intensities, gaussian_ids_sorted, tile_bins = saved[:5]
+        boxes = saved[5:]
         if ctx.num_intersects < 1:
             pos3d_grad = torch.zeros_like(pos3d_radii)
             conics_grad = torch.zeros_like(conics)
@@ -103,5 +110,5 @@ class _VoxelizeGaussians(Function):
                   else _C.voxelize_backward)
             pos3d_grad, conics_grad, intensities_grad = fn(
                 vol_size_voxel, gaussian_ids_sorted, tile_bins, pos3d_radii, conics, intensities,
-                vol_grad.contiguous())
+                vol_grad.contiguous(), *boxes)
         return pos3d_grad, conics_grad, intensities_grad, None, None, None, None, None

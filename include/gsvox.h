@@ -125,14 +125,26 @@ int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
  * summation order); this library serves both with one kernel.  Outputs
  * dpos3d_radii (n,4) (column 3 stays 0), dconics (n,6), dintensities
  * (n,channels), all fully written.  No host synchronisation happens inside.
- * Workspace size from gsv_voxelize_bwd_workspace_bytes.
+ *
+ * Reduction across tiles:
+ *   - tile_min, tile_max, cum_tiles_hit all NULL: float atomics (the
+ *     reference's scheme; summation order, hence the last bits, vary run to run);
+ *   - all three given (the projection's tile boxes and the prefix sum the
+ *     binning used): each (tile, Gaussian) pair writes its partial gradient to
+ *     its duplication slot and one pass sums each Gaussian's slots in order.
+ *     No atomics, bitwise reproducible; the workspace grows by
+ *     num_intersects * (9 + channels) * 4 bytes.
+ * Workspace size from gsv_voxelize_bwd_workspace_bytes (deterministic = 1 for
+ * the second mode).
  */
-int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W, int64_t num_intersects,
+int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W, int32_t channels,
+                                     int64_t num_intersects, int32_t deterministic,
                                      size_t *bytes);
 int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
                      int64_t num_intersects, const int32_t *gaussian_ids_sorted,
                      const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
-                     const float *intensities, const float *vol_grad, float *dpos3d_radii,
+                     const float *intensities, const float *vol_grad, const int32_t *tile_min,
+                     const int32_t *tile_max, const int32_t *cum_tiles_hit, float *dpos3d_radii,
                      float *dconics, float *dintensities, int32_t variant, void *workspace,
                      size_t workspace_bytes, void *stream);
 

@@ -42,7 +42,7 @@ def _prepare(work, device):
     np.testing.assert_array_equal(np32(ids), rids)
     np.testing.assert_array_equal(np32(bins), rbins)
     return dict(w=w, pr=pr, cn=cn, I=I, ids=ids, bins=bins, rpr=rpr, rcn=rcn, rids=rids,
-                rbins=rbins)
+                rbins=rbins, tmin=tmin, tmax=tmax, cum=cum)
 
 
 def _fwd_cases():
@@ -83,21 +83,30 @@ def test_forward_cfg3_full_size_tile_slab(device):
     assert float(vol[16:].abs().sum()) > 0
 
 
-def _bwd(work, device, vol_grad_np, variant=1):
+MODES = ["pairs", "atomic"]  # deterministic per-pair reduction / float atomics
+
+
+def _gpu_bwd(P, cfg, g, variant=1, mode="pairs"):
     import gs_voxelizer.cuda as _C
+    fn = _C.voxelize_backward_per_gaussian if variant == 1 else _C.voxelize_backward
+    extra = (P["tmin"], P["tmax"], P["cum"]) if mode == "pairs" else ()
+    return fn(cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"], P["w"].intensities, g, *extra)
+
+
+def _bwd(work, device, vol_grad_np, variant=1, mode="pairs"):
     cfg = work.cfg
     P = _prepare(work, device)
-    fn = _C.voxelize_backward_per_gaussian if variant == 1 else _C.voxelize_backward
     g = torch.from_numpy(vol_grad_np).to(device)
-    dp, dc, di = fn(cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"], P["w"].intensities, g)
+    dp, dc, di = _gpu_bwd(P, cfg, g, variant, mode)
     torch.cuda.synchronize()
     ref, absum, amb = O.voxelize_bwd(cfg.vol, P["rids"], P["rbins"], P["rpr"], P["rcn"],
                                      work.intensities.numpy(), vol_grad_np, diagnostics=True)
     return P, (np32(dp), np32(dc), np32(di)), ref, absum, amb
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("name,work", list(_fwd_cases()), ids=lambda v: v if isinstance(v, str) else "")
-def test_backward_l1_gradient_matches_oracle(device, name, work):
+def test_backward_l1_gradient_matches_oracle(device, name, work, mode):
     """The benchmark's gradient: L1 loss against the config's phantom."""
     cfg = work.cfg
     P = _prepare(work, device)
@@ -105,17 +114,18 @@ def test_backward_l1_gradient_matches_oracle(device, name, work):
                              work.intensities.numpy())
     target = S.phantom(work).numpy()[..., None]
     g = l1_vol_grad(ref_vol, np.broadcast_to(target, ref_vol.shape))
-    _, got, ref, _, amb = _bwd(work, device, g)
+    _, got, ref, _, amb = _bwd(work, device, g, mode=mode)
     for nm, a, b, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, ref, amb):
         report_close(f"{name}: {nm}", a, b, RTOL, ATOL, bound=m)
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("name,work", list(_fwd_cases())[:5], ids=lambda v: v if isinstance(v, str) else "")
-def test_backward_random_gradient_conditioned(device, name, work):
+def test_backward_random_gradient_conditioned(device, name, work, mode):
     cfg = work.cfg
     C = work.intensities.shape[1]
     g = np.random.default_rng(5).standard_normal(cfg.vol + (C,)).astype(np.float32)
-    _, got, ref, absum, amb = _bwd(work, device, g)
+    _, got, ref, absum, amb = _bwd(work, device, g, mode=mode)
     for nm, a, b, s, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, ref, absum, amb):
         report_close(f"{name}: {nm}", a, b, RTOL, ATOL, bound=1e-5 * s + m)
 
@@ -123,10 +133,28 @@ def test_backward_random_gradient_conditioned(device, name, work):
 def test_backward_variants_agree(device):
     work = S.make_gaussians(S.CONFIGS[1], seed=2)
     g = np.random.default_rng(1).standard_normal(work.cfg.vol + (1,)).astype(np.float32)
-    _, got1, _, absum, _ = _bwd(work, device, g, variant=1)
-    _, got0, _, _, _ = _bwd(work, device, g, variant=0)
+    _, got1, _, absum, _ = _bwd(work, device, g, variant=1, mode="atomic")
+    _, got0, _, _, _ = _bwd(work, device, g, variant=0, mode="atomic")
     for nm, a, b, s in zip(("dpos3d_radii", "dconics", "dintensities"), got0, got1, absum):
         report_close(f"variants {nm}", a, b, 1e-6, 0.0, bound=1e-6 * s)
+
+
+def test_backward_pairs_bitwise_reproducible(device):
+    """The per-pair reduction has a fixed summation order: two runs, and both
+    variants, give identical bits; atomics agree with it to rounding."""
+    work = S.make_gaussians(small_config(3, 40000, vol=(96, 128, 80)), seed=6)
+    cfg = work.cfg
+    P = _prepare(work, device)
+    g = torch.randn(cfg.vol + (1,), generator=torch.Generator().manual_seed(2)).to(device)
+    a = [t.cpu() for t in _gpu_bwd(P, cfg, g, 1, "pairs")]
+    b = [t.cpu() for t in _gpu_bwd(P, cfg, g, 1, "pairs")]
+    c = [t.cpu() for t in _gpu_bwd(P, cfg, g, 0, "pairs")]
+    for x, y, z in zip(a, b, c):
+        assert torch.equal(x, y) and torch.equal(x, z)
+    d = [t.cpu().numpy() for t in _gpu_bwd(P, cfg, g, 1, "atomic")]
+    for nm, x, y in zip(("dpos3d_radii", "dconics", "dintensities"), a, d):
+        scale = float(np.abs(y).max())
+        report_close(f"pairs vs atomic {nm}", x.numpy(), y, 1e-4, 1e-5 * scale)
 
 
 def test_backward_cfg3_full_size_identity(device):
@@ -141,7 +169,7 @@ def test_backward_cfg3_full_size_identity(device):
     gen = torch.Generator(device="cpu").manual_seed(3)
     g = torch.randn(vol.shape, generator=gen).to(device)
     dp, dc, di = _C.voxelize_backward_per_gaussian(cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"],
-                                                   I, g)
+                                                   I, g, P["tmin"], P["tmax"], P["cum"])
     lhs = float((I.double() * di.double()).sum())
     rhs = float((vol.double() * g.double()).sum())
     scale = float((vol.double() * g.double()).abs().sum())
