@@ -17,6 +17,7 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 3]
                        [--no-cpu-baseline]
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -39,7 +40,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--calibrate-copy", action="store_true",
-                    help="also run one elementwise kernel that reads and writes 256 MiB (a "
+                    help="also run one elementwise kernel that reads and writes 1 GiB (a "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
@@ -143,6 +144,7 @@ def main():
                              "optim_to_render_backward"])
     timer.install()
     timer.active = True
+    _C._L.gsv_kernel_timing_enable(1)   # HIP events around the hot kernels, on their stream
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -152,13 +154,20 @@ def main():
     timer.active = False
     timer.uninstall()
     ms = (t1 - t0) * 1e3 / args.steps
+    kern = {}
+    for slot, name in ((0, "k_vox_fwd"), (1, "k_vox_bwd"), (2, "k_pair_reduce")):
+        tot, cnt = ctypes.c_double(0), ctypes.c_int32(0)
+        _C._L.gsv_kernel_timing_collect(slot, ctypes.byref(tot), ctypes.byref(cnt))
+        kern[name] = (tot.value / cnt.value) if cnt.value else None
+    _C._L.gsv_kernel_timing_enable(0)
 
     C = cfg.channels
-    fwd_ms = timer.mean_ms("voxelize_forward")
-    bwd_ms = timer.mean_ms("voxelize_backward_per_gaussian")
+    fwd_ms = kern["k_vox_fwd"]          # kernel alone
+    bwd_ms = kern["k_vox_bwd"]          # kernel alone (the dominant one)
     fwd_flops = evals * (22 + 2 * C)
     bwd_flops = evals * (65 + 4 * C)
     stages = {k: round(timer.mean_ms(k), 4) for k in timer.names if timer.mean_ms(k) is not None}
+    stages.update({f"kernel:{k}": round(v, 4) for k, v in kern.items() if v is not None})
     bwd_tflops = bwd_flops / (bwd_ms * 1e-3) / 1e12
     fwd_tflops = fwd_flops / (fwd_ms * 1e-3) / 1e12
 
@@ -201,13 +210,16 @@ def main():
         "cpu_baseline": None,
     }
     if args.calibrate_copy:
-        # an elementwise kernel that reads 256 MiB and writes 256 MiB (a plain
-        # hipMemcpy D2D may run on a DMA engine, invisible to the counters)
-        src = torch.ones((64 << 20,), device=dev)
+        # an elementwise kernel that reads 1 GiB and writes 1 GiB (a plain hipMemcpy
+        # D2D may run on a DMA engine, invisible to the counters); a second 1 GiB
+        # fill in between evicts the source from the 256 MB last-level cache
+        src = torch.ones((256 << 20,), device=dev)
+        flush = torch.ones((256 << 20,), device=dev)
         dst = torch.empty_like(src)
         torch.mul(src, 2.0, out=dst)
         torch.cuda.synchronize()
         result["calibration_copy_bytes"] = src.numel() * 4
+        del src, flush, dst
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(work)
     print(json.dumps(result), flush=True)

@@ -35,6 +35,18 @@ __host__ __device__ inline int64_t xcd_per(int64_t count) { return (count + kXcd
 __host__ __device__ inline int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
 __host__ __device__ inline int64_t imax64(int64_t a, int64_t b) { return a > b ? a : b; }
 
+// Optional per-kernel timing (gsv_kernel_timing_*): when enabled, the hot
+// kernels are bracketed by HIP events recorded on their launch stream.
+struct KernelTimer {
+    int slot;
+    hipStream_t stream;
+    hipEvent_t stop;
+    bool on;
+    KernelTimer(int slot, hipStream_t s);
+    ~KernelTimer();
+};
+enum TimedKernel { kTimedVoxFwd = 0, kTimedVoxBwd = 1, kTimedPairReduce = 2, kTimedCount = 3 };
+
 // Zero-fills n 32-bit words with a kernel (graph-capture safe, unlike memset).
 int fill_zero_u32(void *ptr, int64_t n_words, hipStream_t stream);
 

@@ -6,6 +6,9 @@
 // partials in one workgroup, and a block scan that adds each block's offset.
 // Every pass is HBM-bound: 4 B read + 4 B written per element, plus 4 B read in
 // the reduce pass.
+#include <mutex>
+#include <vector>
+
 #include "gsv_device.h"
 
 namespace gsv {
@@ -108,6 +111,42 @@ __global__ __launch_bounds__(256) void k_fill_zero(uint32_t *__restrict__ p, int
 
 }  // namespace
 
+namespace {
+struct TimingState {
+    std::mutex mu;
+    bool enabled = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pending[kTimedCount];
+    double total_ms[kTimedCount] = {0, 0, 0};
+    int count[kTimedCount] = {0, 0, 0};
+};
+TimingState &timing() {
+    static TimingState st;
+    return st;
+}
+}  // namespace
+
+KernelTimer::KernelTimer(int s, hipStream_t st) : slot(s), stream(st), stop(nullptr), on(false) {
+    TimingState &T = timing();
+    std::lock_guard<std::mutex> lk(T.mu);
+    if (!T.enabled) return;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess) return;
+    if (hipEventCreate(&b) != hipSuccess) {
+        (void)hipEventDestroy(a);
+        return;
+    }
+    (void)hipEventRecord(a, stream);
+    T.pending[slot].push_back({a, b});
+    stop = b;
+    on = true;
+}
+
+// The stop event is recorded right after the launch.  gsv_kernel_timing_collect
+// must be called after the launches it measures have been issued.
+KernelTimer::~KernelTimer() {
+    if (on) (void)hipEventRecord(stop, stream);
+}
+
 int record_hip_error(hipError_t e) {
     t_last_hip_error = (int)e;
     return GSV_ERR_HIP;
@@ -166,6 +205,38 @@ extern "C" const char *gsv_status_string(int status) {
 }
 
 extern "C" int gsv_last_hip_error(void) { return t_last_hip_error; }
+
+extern "C" int gsv_kernel_timing_enable(int32_t enable) {
+    TimingState &T = timing();
+    std::lock_guard<std::mutex> lk(T.mu);
+    T.enabled = enable != 0;
+    return GSV_OK;
+}
+
+extern "C" int gsv_kernel_timing_collect(int32_t kernel, double *total_ms, int32_t *count) {
+    if (kernel < 0 || kernel >= kTimedCount || !total_ms || !count) return GSV_ERR_INVALID_ARGUMENT;
+    TimingState &T = timing();
+    std::lock_guard<std::mutex> lk(T.mu);
+    for (auto &ev : T.pending[kernel]) {
+        float ms = 0.f;
+        hipError_t e = hipEventSynchronize(ev.second);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev.first, ev.second);
+        (void)hipEventDestroy(ev.first);
+        (void)hipEventDestroy(ev.second);
+        if (e != hipSuccess) {
+            T.pending[kernel].clear();
+            return record_hip_error(e);
+        }
+        T.total_ms[kernel] += ms;
+        T.count[kernel] += 1;
+    }
+    T.pending[kernel].clear();
+    *total_ms = T.total_ms[kernel];
+    *count = T.count[kernel];
+    T.total_ms[kernel] = 0;
+    T.count[kernel] = 0;
+    return GSV_OK;
+}
 
 extern "C" int gsv_scan_workspace_bytes(int64_t n, size_t *bytes) {
     if (n < 0 || !bytes) return GSV_ERR_INVALID_ARGUMENT;

@@ -426,21 +426,21 @@ __global__ __launch_bounds__(256) void k_pair_reduce(int n, int n_isect, const i
     if (g >= n) return;
     const int64_t b = g == 0 ? 0 : max(0, cum[g - 1]);
     const int64_t e = min<int64_t>(cum[g], n_isect);
-    float acc[9 + C];
+    double acc[9 + C];  // this pass is memory-bound; binary64 costs nothing here
 #pragma unroll
-    for (int q = 0; q < 9 + C; ++q) acc[q] = 0.f;
+    for (int q = 0; q < 9 + C; ++q) acc[q] = 0.0;
     for (int64_t k = b; k < e; ++k) {
         const float *src = partial + k * (9 + C);
 #pragma unroll
-        for (int q = 0; q < 9 + C; ++q) acc[q] += src[q];
+        for (int q = 0; q < 9 + C; ++q) acc[q] += (double)src[q];
     }
     float2 *dc = reinterpret_cast<float2 *>(dconic + 6 * (size_t)g);
-    dc[0] = make_float2(acc[0], acc[1]);
-    dc[1] = make_float2(acc[2], acc[3]);
-    dc[2] = make_float2(acc[4], acc[5]);
-    reinterpret_cast<float4 *>(dpos)[g] = make_float4(acc[6], acc[7], acc[8], 0.f);
+    dc[0] = make_float2((float)acc[0], (float)acc[1]);
+    dc[1] = make_float2((float)acc[2], (float)acc[3]);
+    dc[2] = make_float2((float)acc[4], (float)acc[5]);
+    reinterpret_cast<float4 *>(dpos)[g] = make_float4((float)acc[6], (float)acc[7], (float)acc[8], 0.f);
 #pragma unroll
-    for (int c = 0; c < C; ++c) dint[(size_t)C * g + c] = acc[9 + c];
+    for (int c = 0; c < C; ++c) dint[(size_t)C * g + c] = (float)acc[9 + c];
 }
 
 struct BwdLayout {
@@ -490,6 +490,7 @@ extern "C" int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channel
     if (!aligned(pos3d_radii, 16) || !aligned(conics, 8)) return GSV_ERR_INVALID_ARGUMENT;
     const int64_t per = xcd_per(T);
     const dim3 grid((unsigned)(kXcds * per)), block(kWave);
+    KernelTimer timer(kTimedVoxFwd, s);
 #define GSV_VF(CH)                                                                                 \
     hipLaunchKernelGGL(k_vox_fwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, T, per, n,               \
                        (int)num_intersects,                                                         \
@@ -566,14 +567,18 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
     const dim3 grid((unsigned)(L.cap + kXcds)), block(kWave);
     const int ni = (int)num_intersects;
 #define GSV_VB(CH)                                                                                  \
-    hipLaunchKernelGGL(k_vox_bwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, n, ni,                    \
-                       gaussian_ids_sorted, reinterpret_cast<const int2 *>(tile_bins),              \
-                       reinterpret_cast<const float4 *>(pos3d_radii),                               \
-                       reinterpret_cast<const float2 *>(conics), intensities, vol_grad, btile,      \
-                       offs, total, L.cap, dpos3d_radii, dconics, dintensities, tile_min,           \
-                       tile_max, cum_tiles_hit, partial);                                           \
+    {                                                                                               \
+        KernelTimer timer(kTimedVoxBwd, s);                                                         \
+        hipLaunchKernelGGL(k_vox_bwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, n, ni,                \
+                           gaussian_ids_sorted, reinterpret_cast<const int2 *>(tile_bins),          \
+                           reinterpret_cast<const float4 *>(pos3d_radii),                           \
+                           reinterpret_cast<const float2 *>(conics), intensities, vol_grad, btile,  \
+                           offs, total, L.cap, dpos3d_radii, dconics, dintensities, tile_min,       \
+                           tile_max, cum_tiles_hit, partial);                                       \
+    }                                                                                               \
     if (int st = check_launch()) return st;                                                         \
     if (pairs) {                                                                                    \
+        KernelTimer timer(kTimedPairReduce, s);                                                     \
         hipLaunchKernelGGL(k_pair_reduce<CH>, dim3((n + 255) / 256), dim3(256), 0, s, n, ni,        \
                            cum_tiles_hit, partial, dpos3d_radii, dconics, dintensities);            \
     }

@@ -36,6 +36,8 @@ SIGNATURES = {
                                          ctypes.POINTER(_c_size_t)],
     "gsv_voxelize_bwd": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P, _P,
                          _P, _P, _P, _P, _P, _P, _c_int, _P, _c_size_t, _P],
+    "gsv_kernel_timing_enable": [_c_int],
+    "gsv_kernel_timing_collect": [_c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_int)],
 }
 
 _lib = None

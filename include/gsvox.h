@@ -148,6 +148,18 @@ int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
                      float *dconics, float *dintensities, int32_t variant, void *workspace,
                      size_t workspace_bytes, void *stream);
 
+/*
+ * Kernel timing (no counterpart in the reference; for benchmarks and
+ * profiling).  While enabled, each launch of the hot kernels is bracketed by
+ * two HIP events recorded on its launch stream.  collect() waits for the
+ * recorded events and returns the summed duration and launch count of one
+ * kernel since the previous collect: 0 = forward voxelize kernel, 1 = backward
+ * voxelize kernel, 2 = backward per-Gaussian reduction.  Off by default; costs
+ * nothing when off.
+ */
+int gsv_kernel_timing_enable(int32_t enable);
+int gsv_kernel_timing_collect(int32_t kernel, double *total_ms, int32_t *count);
+
 #ifdef __cplusplus
 }
 #endif
