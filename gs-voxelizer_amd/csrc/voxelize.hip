@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
     if (tile >= T) return;
     const int lane = threadIdx.x;
     const TileGeom tg = tile_geom(tile, Tx, Ty, D, H, W);
-    const float py = (float)(lane & 7) + 0.5f, pz = (float)(lane >> 3) + 0.5f;  // tile-local
+    const float py = (float)(lane & 7) - 3.5f, pz = (float)(lane >> 3) - 3.5f;  // centred, tile-local
     int2 range = bins[tile];
     range.x = max(range.x, 0);
     range.y = min(range.y, n_isect);  // never index past the id array
@@ -155,11 +155,14 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                     live = may_touch(p.x, p.y, p.z, c01.x, c01.y, c23.x, c23.y, c45.x, c45.y, gt.t2,
                                      tg.xlo, tg.xhi, tg.ylo, tg.yhi, tg.zlo, tg.zhi);
                 if (live) {
-                    s_rec[lane][0] = make_float4(p.x - (float)tg.x0 - 0.5f, p.y - (float)tg.y0,
-                                                 p.z - (float)tg.z0, -0.5f * kLog2e * c01.x);
+                    // centred offsets: delta = c - p', p' = local index - 3.5
+                    const float cx = p.x - (float)tg.x0 - 4.0f;
+                    const float A2 = -0.5f * kLog2e * c01.x;
+                    s_rec[lane][0] = make_float4(cx, p.y - (float)tg.y0 - 4.0f,
+                                                 p.z - (float)tg.z0 - 4.0f, A2);
                     s_rec[lane][1] = make_float4(-kLog2e * c01.y, -kLog2e * c23.x,
                                                  -0.5f * kLog2e * c23.y, -kLog2e * c45.x);
-                    s_rec[lane][2] = make_float4(-0.5f * kLog2e * c45.y, gt.shift, gt.half, 0.f);
+                    s_rec[lane][2] = make_float4(-0.5f * kLog2e * c45.y, gt.shift, gt.half, A2 * cx);
                     float iw[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int c = 0; c < C; ++c) iw[c] = I[c] * gt.scale;
@@ -177,10 +180,14 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
             const float dy = r0.y - py, dz = r0.z - pz;
             const float R1 = fmaf(r1.x, dy, r1.y * dz);
             const float R0 = fmaf(fmaf(r1.z, dy, r1.w * dz), dy, fmaf(r2.x * dz, dz, -r2.y));
+            // along the row: s(u') = R0 + R1*dx + A2*dx^2, dx = cx - u', rewritten
+            // around the row centre as T0 + u' * (A2 * u' - T1)
+            const float T1 = R1 + 2.0f * r2.w;
+            const float T0 = fmaf(r0.x, R1 + r2.w, R0);
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
-                const float dx = r0.x - (float)u;
-                const float s = fmaf(dx, fmaf(dx, r0.w, R1), R0);
+                const float uc = (float)u - 3.5f;
+                const float s = fmaf(uc, fmaf(uc, r0.w, -T1), T0);
                 const float a = (fabsf(s) <= r2.z) ? __builtin_amdgcn_exp2f(s) : 0.f;
 #pragma unroll
                 for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
@@ -294,9 +301,10 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
             if (live && gt.bounded)
                 live = may_touch(p.x, p.y, p.z, ca, cb, cc, cd, ce, cf, gt.t2, tg.xlo, tg.xhi,
                                  tg.ylo, tg.yhi, tg.zlo, tg.zhi);
-            mxl = p.x - (float)tg.x0 - 0.5f;
-            myl = p.y - (float)tg.y0;
-            mzl = p.z - (float)tg.z0;
+            // delta = mu - p = (mu - tile centre) - p', p' = local index - 3.5
+            mxl = p.x - (float)tg.x0 - 4.0f;
+            myl = p.y - (float)tg.y0 - 4.0f;
+            mzl = p.z - (float)tg.z0 - 4.0f;
         }
     }
     __syncthreads();
@@ -307,18 +315,32 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
     const float Dn = -0.5f * kLog2e * cd, En = -kLog2e * ce, Fn = -0.5f * kLog2e * cf;
     const float shift = gt.shift, half = live ? gt.half : -1.f;
 
+    // Moments of h = a * G about the Gaussian's centre: S[..] = sum h * delta^k,
+    // delta = mu - p.  Per voxel: h, h*dx, h*dx^2 by FMAs against the lane's
+    // hoisted dx_u and dx_u^2; rows fold in dy, planes in dz.  Taking moments
+    // about the Gaussian (not the tile) keeps every sum well-conditioned: h is
+    // large only where |delta| is small.
     float S0 = 0.f, Sx = 0.f, Sy = 0.f, Sz = 0.f;
     float Sxx = 0.f, Sxy = 0.f, Sxz = 0.f, Syy = 0.f, Syz = 0.f, Szz = 0.f;
     float dIa[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) dIa[c] = 0.f;
+    float dxu[GSV_TILE], dxu2[GSV_TILE];
+#pragma unroll
+    for (int u = 0; u < GSV_TILE; ++u) {
+        dxu[u] = mxl - ((float)u - 3.5f);
+        dxu2[u] = dxu[u] * dxu[u];
+    }
 
     const int ny = min(GSV_TILE, H - tg.y0), nz = any_live ? min(GSV_TILE, D - tg.z0) : 0;
     for (int lz = 0; lz < nz; ++lz) {
-        const float dz = mzl - ((float)lz + 0.5f);
+        const float dz = mzl - ((float)lz - 3.5f);
         const float Cdz = Cn * dz, Edz = En * dz;
         const float R0z = fmaf(Fn * dz, dz, -shift);
-        for (int ly = 0; ly < ny; ++ly) {
+        float Q0 = 0.f, Qx = 0.f, Qxx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
+#pragma unroll
+        for (int ly = 0; ly < GSV_TILE; ++ly) {
+            if (ly >= ny) break;
             const int row = lz * GSV_TILE + ly;
             float gv[GSV_TILE * C];
 #pragma unroll
@@ -326,14 +348,13 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
                 const float4 t4 = s_g[row][q];
                 gv[4 * q] = t4.x; gv[4 * q + 1] = t4.y; gv[4 * q + 2] = t4.z; gv[4 * q + 3] = t4.w;
             }
-            const float dy = myl - ((float)ly + 0.5f);
+            const float dy = myl - ((float)ly - 3.5f);
             const float R1 = fmaf(Bn, dy, Cdz);
             const float R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
             float W0 = 0.f, W1 = 0.f, W2 = 0.f;
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
-                const float dx = mxl - (float)u;
-                const float s = fmaf(dx, fmaf(dx, A2, R1), R0);
+                const float s = fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
                 const float a = (fabsf(s) <= half) ? __builtin_amdgcn_exp2f(s) : 0.f;
                 float h;
                 if (C == 1) {
@@ -348,22 +369,26 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
                     h = a * G;
                 }
                 W0 += h;
-                const float t = h * dx;
-                W1 += t;
-                W2 = fmaf(t, dx, W2);
+                W1 = fmaf(h, dxu[u], W1);
+                W2 = fmaf(h, dxu2[u], W2);
             }
-            S0 += W0;
-            Sx += W1;
-            Sxx += W2;
-            Sxy = fmaf(W1, dy, Sxy);
-            Sxz = fmaf(W1, dz, Sxz);
-            const float t0 = W0 * dy, t1 = W0 * dz;
-            Sy += t0;
-            Syy = fmaf(t0, dy, Syy);
-            Syz = fmaf(t0, dz, Syz);
-            Sz += t1;
-            Szz = fmaf(t1, dz, Szz);
+            Q0 += W0;
+            Qx += W1;
+            Qxx += W2;
+            Qy = fmaf(W0, dy, Qy);
+            Qxy = fmaf(W1, dy, Qxy);
+            Qyy = fmaf(W0, dy * dy, Qyy);
         }
+        S0 += Q0;
+        Sx += Qx;
+        Sxx += Qxx;
+        Sy += Qy;
+        Sxy += Qxy;
+        Syy += Qyy;
+        Sz = fmaf(Q0, dz, Sz);
+        Sxz = fmaf(Qx, dz, Sxz);
+        Syz = fmaf(Qy, dz, Syz);
+        Szz = fmaf(Q0, dz * dz, Szz);
     }
     // sigma-gradient weight per unit of h: alpha = scale * a
     const float w = live ? ((C == 1) ? gt.scale * I[0] : gt.scale) : 0.f;
