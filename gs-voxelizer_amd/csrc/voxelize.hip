@@ -13,6 +13,15 @@
 //    Writing s = sigma2 - t2/2, h = -t2/2 makes that |s| <= h, and the factor
 //    2^(t2/2) is folded into the intensities (forward) or the final gradient
 //    scale (backward).
+//  * Gate-free evaluation.  v_exp_f32 returns exactly 0 for every result below
+//    2^-126 (it produces no denormals) and exactly 2^-126 at -126.  With
+//    off = -(t2 + 126), rounded once, exp2(sigma2 + off) is therefore nonzero
+//    iff sigma2 >= t2 (up to that rounding), and 2^-off restores the
+//    magnitude.  For a finite positive-definite conic sigma2 <= 0 holds
+//    everywhere (up to rounding), so both gates cost no instruction at all.
+//    Gaussians outside that domain (indefinite or non-finite conic, mean
+//    beyond 2^60 * 1e-6, intensities far above the mean) take the exact
+//    |s| <= h path.
 //  * Along a voxel row (fixed y, z) the quadratic form is
 //    s(dx) = R0 + dx*(R1 + A2*dx): two FMAs per voxel once R0, R1 are set up.
 //  * Forward: one 64-lane wave per tile, lane = one x-row of 8 voxels.  Per
@@ -40,11 +49,16 @@ constexpr float kLog2e = 1.44269504088896341f;
 constexpr float kLn2 = 0.693147180559945309f;
 constexpr float kLog2MinContrib = -19.9315685693241741f;  // log2(1e-6)
 
+constexpr float kExpFlush = 126.0f;     // v_exp_f32 results below 2^-126 are 0
+constexpr float kDeadOffset = -1000.0f;  // exponent offset that zeroes a lane
+
 struct Gate {
-    float shift;  // s = sigma2 - shift
-    float half;   // contributes iff |s| <= half
-    float scale;  // 2^shift
-    float t2;     // log2(1e-6 / mean), or 0 when unbounded
+    float shift;   // exact path: s = sigma2 - shift
+    float half;    // exact path: contributes iff |s| <= half
+    float scale;   // exact path: 2^shift
+    float off;     // gate-free path: a = exp2(sigma2 + off)
+    float fscale;  // gate-free path: 2^-off
+    float t2;      // log2(1e-6 / mean), or 0 when unbounded
     bool live;
     bool bounded;
 };
@@ -52,6 +66,8 @@ struct Gate {
 // Gate constants from the mean intensity (voxelize.cu:138-148).
 __device__ __forceinline__ Gate make_gate(float mean) {
     Gate g;
+    g.off = kDeadOffset;
+    g.fscale = 0.f;
     if (mean > 0.f && mean <= FLT_MAX) {
         const float t2 = kLog2MinContrib - __log2f(mean);
         g.t2 = t2;
@@ -60,6 +76,10 @@ __device__ __forceinline__ Gate make_gate(float mean) {
         g.scale = exp2f(g.shift);
         g.live = t2 <= 0.f;  // mean < 1e-6: alpha <= 1 can never reach the threshold
         g.bounded = true;
+        if (g.live && t2 >= -60.f) {
+            g.off = -(t2 + kExpFlush);
+            g.fscale = exp2f(-g.off);  // of the rounded offset, so the two cancel
+        }
     } else if (mean > 0.f || mean != mean) {
         // +inf or NaN mean: the reference's `alpha * mean < 1e-6` never holds,
         // every finite sigma <= 0 contributes I * alpha.
@@ -75,6 +95,21 @@ __device__ __forceinline__ Gate make_gate(float mean) {
         g.bounded = false;
     }
     return g;
+}
+
+// Whether a live Gaussian may use the gate-free evaluation: bounded gate with
+// t2 >= -60, intensities whose weights I * 2^-off stay below 2^120, a finite
+// centre and a finite positive-definite conic (Sylvester's criterion), so that
+// sigma2 <= 0 up to rounding and every product in the kernels stays finite.
+__device__ __forceinline__ bool gate_free_ok(const Gate &g, float max_abs_i, float mx, float my,
+                                             float mz, float a, float b, float c, float d, float e,
+                                             float f) {
+    if (!g.live || !g.bounded || !(g.fscale > 0.f)) return false;
+    if (!(max_abs_i * g.fscale <= 0x1p120f)) return false;
+    if (!__builtin_isfinite(mx + my + mz) || !__builtin_isfinite(a + b + c + d + e + f))
+        return false;
+    const float det = a * (d * f - e * e) - b * (b * f - c * e) + c * (b * e - c * d);
+    return a > 0.f && a * d - b * b > 0.f && det > 0.f;
 }
 
 // Conservative test: can the ellipsoid {d^T Q d <= K^2}, K^2 = 2 ln(mean*1e6),
@@ -136,17 +171,18 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
 
     for (int b0 = range.x; b0 < range.y; b0 += kWave) {
         const int idx = b0 + lane;
-        bool live = false;
+        bool live = false, fast = false;
         if (idx < range.y) {
             const int g = ids[idx];
             if ((unsigned)g < (unsigned)n) {
                 const float4 p = pos_radii[g];
                 const float2 c01 = conics[3 * g], c23 = conics[3 * g + 1], c45 = conics[3 * g + 2];
-                float I[C], mean = 0.f;
+                float I[C], mean = 0.f, max_abs = 0.f;
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
                     I[c] = intens[(size_t)g * C + c];
                     mean += I[c];
+                    max_abs = fmaxf(max_abs, fabsf(I[c]));
                 }
                 mean /= (float)C;
                 const Gate gt = make_gate(mean);
@@ -155,6 +191,8 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                     live = may_touch(p.x, p.y, p.z, c01.x, c01.y, c23.x, c23.y, c45.x, c45.y, gt.t2,
                                      tg.xlo, tg.xhi, tg.ylo, tg.yhi, tg.zlo, tg.zhi);
                 if (live) {
+                    fast = gate_free_ok(gt, max_abs, p.x, p.y, p.z, c01.x, c01.y, c23.x, c23.y,
+                                        c45.x, c45.y);
                     // centred offsets: delta = c - p', p' = local index - 3.5
                     const float cx = p.x - (float)tg.x0 - 4.0f;
                     const float A2 = -0.5f * kLog2e * c01.x;
@@ -162,15 +200,19 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                                                  p.z - (float)tg.z0 - 4.0f, A2);
                     s_rec[lane][1] = make_float4(-kLog2e * c01.y, -kLog2e * c23.x,
                                                  -0.5f * kLog2e * c23.y, -kLog2e * c45.x);
-                    s_rec[lane][2] = make_float4(-0.5f * kLog2e * c45.y, gt.shift, gt.half, A2 * cx);
+                    // gate-free: no shift inside the row constants, offset added per row
+                    s_rec[lane][2] = make_float4(-0.5f * kLog2e * c45.y, fast ? 0.f : gt.shift,
+                                                 fast ? gt.off : gt.half, A2 * cx);
+                    const float wscale = fast ? gt.fscale : gt.scale;
                     float iw[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int c = 0; c < C; ++c) iw[c] = I[c] * gt.scale;
+                    for (int c = 0; c < C; ++c) iw[c] = I[c] * wscale;
                     s_rec[lane][3] = make_float4(iw[0], iw[1], iw[2], iw[3]);
                 }
             }
         }
         uint64_t mask = __ballot(live);
+        const uint64_t fast_mask = __ballot(fast);
         __syncthreads();
         while (mask) {
             const int j = __builtin_ctzll(mask);
@@ -184,13 +226,25 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
             // around the row centre as T0 + u' * (A2 * u' - T1)
             const float T1 = R1 + 2.0f * r2.w;
             const float T0 = fmaf(r0.x, R1 + r2.w, R0);
+            if ((fast_mask >> j) & 1ull) {
+                // the offset enters once per row, after the small terms are summed
+                const float T0f = T0 + r2.z;
 #pragma unroll
-            for (int u = 0; u < GSV_TILE; ++u) {
-                const float uc = (float)u - 3.5f;
-                const float s = fmaf(uc, fmaf(uc, r0.w, -T1), T0);
-                const float a = (fabsf(s) <= r2.z) ? __builtin_amdgcn_exp2f(s) : 0.f;
+                for (int u = 0; u < GSV_TILE; ++u) {
+                    const float uc = (float)u - 3.5f;
+                    const float a = __builtin_amdgcn_exp2f(fmaf(uc, fmaf(uc, r0.w, -T1), T0f));
 #pragma unroll
-                for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
+                    for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < GSV_TILE; ++u) {
+                    const float uc = (float)u - 3.5f;
+                    const float s = fmaf(uc, fmaf(uc, r0.w, -T1), T0);
+                    const float a = (fabsf(s) <= r2.z) ? __builtin_amdgcn_exp2f(s) : 0.f;
+#pragma unroll
+                    for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
+                }
             }
         }
         __syncthreads();
@@ -232,6 +286,105 @@ __global__ __launch_bounds__(256) void k_bucket_fill(const int *__restrict__ cou
 }
 
 template <int C>
+struct Moments {
+    float S0, Sx, Sy, Sz, Sxx, Sxy, Sxz, Syy, Syz, Szz;
+    float dI[C];
+};
+
+// Moments of h = a * G about the Gaussian's centre for one lane's pair:
+// S[..] = sum h * delta^k, delta = mu - p, G = sum_c I_c g_c (g_c alone for
+// C == 1; I folds into the final scale).  Per voxel: h, h*dx, h*dx^2 by FMAs
+// against the lane's hoisted dx_u and dx_u^2; rows fold in dy, planes in dz.
+// Taking moments about the Gaussian (not the tile) keeps every sum
+// well-conditioned: h is large only where |delta| is small.
+//   kGateFree: a = exp2(sigma2 + bound), zero below the threshold by the
+//              hardware flush (bound = the gate-free offset, shift unused);
+//   otherwise: a = exp2(s) if |s| <= bound, s = sigma2 - shift.
+template <int C, bool kGateFree>
+__device__ __forceinline__ void pair_moments(const float4 (*s_g)[2 * C], int ny, int nz,
+                                             float mxl, float myl, float mzl, float A2, float Bn,
+                                             float Cn, float Dn, float En, float Fn, float shift,
+                                             float bound, const float (&I)[C], Moments<C> &M) {
+    M.S0 = M.Sx = M.Sy = M.Sz = 0.f;
+    M.Sxx = M.Sxy = M.Sxz = M.Syy = M.Syz = M.Szz = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) M.dI[c] = 0.f;
+    float dxu[GSV_TILE], dxu2[GSV_TILE];
+#pragma unroll
+    for (int u = 0; u < GSV_TILE; ++u) {
+        dxu[u] = mxl - ((float)u - 3.5f);
+        dxu2[u] = dxu[u] * dxu[u];
+    }
+    for (int lz = 0; lz < nz; ++lz) {
+        const float dz = mzl - ((float)lz - 3.5f);
+        const float Cdz = Cn * dz, Edz = En * dz;
+        const float R0z = kGateFree ? (Fn * dz) * dz : fmaf(Fn * dz, dz, -shift);
+        float Q0 = 0.f, Qx = 0.f, Qxx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
+#pragma unroll
+        for (int ly = 0; ly < GSV_TILE; ++ly) {
+            if (ly >= ny) break;
+            const int row = lz * GSV_TILE + ly;
+            float gv[GSV_TILE * C];
+#pragma unroll
+            for (int q = 0; q < 2 * C; ++q) {
+                const float4 t4 = s_g[row][q];
+                gv[4 * q] = t4.x; gv[4 * q + 1] = t4.y; gv[4 * q + 2] = t4.z; gv[4 * q + 3] = t4.w;
+            }
+            const float dy = myl - ((float)ly - 3.5f);
+            const float R1 = fmaf(Bn, dy, Cdz);
+            float R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
+            if (kGateFree) R0 += bound;  // the offset enters after the small terms
+            float W0 = 0.f, W1 = 0.f, W2 = 0.f;
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u) {
+                const float s = fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
+                float a;
+                if (kGateFree)
+                    a = __builtin_amdgcn_exp2f(s);
+                else
+                    a = (fabsf(s) <= bound) ? __builtin_amdgcn_exp2f(s) : 0.f;
+                float h;
+                if (C == 1) {
+                    h = a * gv[u];
+                } else {
+                    float G = 0.f;
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        G = fmaf(I[c], gv[u * C + c], G);
+                        M.dI[c] = fmaf(a, gv[u * C + c], M.dI[c]);
+                    }
+                    h = a * G;
+                }
+                W0 += h;
+                W1 = fmaf(h, dxu[u], W1);
+                W2 = fmaf(h, dxu2[u], W2);
+            }
+            Q0 += W0;
+            Qx += W1;
+            Qxx += W2;
+            Qy = fmaf(W0, dy, Qy);
+            Qxy = fmaf(W1, dy, Qxy);
+            Qyy = fmaf(W0, dy * dy, Qyy);
+        }
+        M.S0 += Q0;
+        M.Sx += Qx;
+        M.Sxx += Qxx;
+        M.Sy += Qy;
+        M.Sxy += Qxy;
+        M.Syy += Qyy;
+        M.Sz = fmaf(Q0, dz, M.Sz);
+        M.Sxz = fmaf(Qx, dz, M.Sxz);
+        M.Syz = fmaf(Qy, dz, M.Syz);
+        M.Szz = fmaf(Q0, dz * dz, M.Szz);
+    }
+}
+
+// vol_grad of a tile is staged scaled by 2^m so that its largest magnitude
+// lies in [2^89, 2^90): with the gate-free a >= 2^-126, every h = a * G is then
+// a normal number whatever the loss scale.  The epilogue divides 2^m out.
+constexpr int kGradScaleExp = 90;
+
+template <int C>
 __global__ __launch_bounds__(kWave) void k_vox_bwd(
     int D, int H, int W, int Tx, int Ty, int n, int n_isect, const int *__restrict__ ids,
     const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
@@ -254,6 +407,48 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
     range.y = min(range.y, n_isect);  // never index past the id array
     const TileGeom tg = tile_geom(tile, Tx, Ty, D, H, W);
 
+    // this lane's Gaussian
+    const int idx = range.x + chunk * kBucket + lane;
+    bool live = false, fast = false;
+    int g = 0;
+    float mxl = 0.f, myl = 0.f, mzl = 0.f;
+    float ca = 0.f, cb = 0.f, cc = 0.f, cd = 0.f, ce = 0.f, cf = 0.f;
+    float I[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) I[c] = 0.f;
+    Gate gt = make_gate(0.f);
+    if (idx < range.y) {
+        g = ids[idx];
+        if ((unsigned)g < (unsigned)n) {
+            const float4 p = pos_radii[g];
+            const float2 c01 = conics[3 * g], c23 = conics[3 * g + 1], c45 = conics[3 * g + 2];
+            ca = c01.x; cb = c01.y; cc = c23.x; cd = c23.y; ce = c45.x; cf = c45.y;
+            float mean = 0.f, max_abs = 0.f;
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                I[c] = intens[(size_t)g * C + c];
+                mean += I[c];
+                max_abs = fmaxf(max_abs, fabsf(I[c]));
+            }
+            mean /= (float)C;
+            gt = make_gate(mean);
+            live = gt.live;
+            if (live && gt.bounded)
+                live = may_touch(p.x, p.y, p.z, ca, cb, cc, cd, ce, cf, gt.t2, tg.xlo, tg.xhi,
+                                 tg.ylo, tg.yhi, tg.zlo, tg.zhi);
+            if (live) {
+                fast = gate_free_ok(gt, max_abs, p.x, p.y, p.z, ca, cb, cc, cd, ce, cf);
+                // delta = mu - p = (mu - tile centre) - p', p' = local index - 3.5
+                mxl = p.x - (float)tg.x0 - 4.0f;
+                myl = p.y - (float)tg.y0 - 4.0f;
+                mzl = p.z - (float)tg.z0 - 4.0f;
+            }
+        }
+    }
+    // One wave-uniform choice: gate-free unless a live lane needs the exact gate.
+    const bool wave_fast = __all(!live || fast);
+
+    int gexp = 0;  // vol_grad is staged as g * 2^gexp
     {   // stage the tile's vol_grad, lane = row; outside voxels are zero
         const int y = tg.y0 + (lane & 7), z = tg.z0 + (lane >> 3);
         float v[GSV_TILE * C];
@@ -268,146 +463,62 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
 #pragma unroll
                     for (int c = 0; c < C; ++c) v[u * C + c] = src[u * C + c];
         }
+        if (wave_fast) {
+            float mx = 0.f;
+#pragma unroll
+            for (int i = 0; i < GSV_TILE * C; ++i) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+            for (int o = kWave / 2; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+            if (mx > 0.f && mx <= FLT_MAX) {
+                int e;
+                (void)frexpf(mx, &e);
+                gexp = kGradScaleExp - e;
+            }
+#pragma unroll
+            for (int i = 0; i < GSV_TILE * C; ++i) v[i] = ldexpf(v[i], gexp);
+        }
 #pragma unroll
         for (int q = 0; q < 2 * C; ++q)
             s_g[lane][q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-    }
-
-    // this lane's Gaussian
-    const int idx = range.x + chunk * kBucket + lane;
-    bool live = false;
-    int g = 0;
-    float mxl = 0.f, myl = 0.f, mzl = 0.f;
-    float ca = 0.f, cb = 0.f, cc = 0.f, cd = 0.f, ce = 0.f, cf = 0.f;
-    float I[C];
-#pragma unroll
-    for (int c = 0; c < C; ++c) I[c] = 0.f;
-    Gate gt = make_gate(0.f);
-    if (idx < range.y) {
-        g = ids[idx];
-        if ((unsigned)g < (unsigned)n) {
-            const float4 p = pos_radii[g];
-            const float2 c01 = conics[3 * g], c23 = conics[3 * g + 1], c45 = conics[3 * g + 2];
-            ca = c01.x; cb = c01.y; cc = c23.x; cd = c23.y; ce = c45.x; cf = c45.y;
-            float mean = 0.f;
-#pragma unroll
-            for (int c = 0; c < C; ++c) {
-                I[c] = intens[(size_t)g * C + c];
-                mean += I[c];
-            }
-            mean /= (float)C;
-            gt = make_gate(mean);
-            live = gt.live;
-            if (live && gt.bounded)
-                live = may_touch(p.x, p.y, p.z, ca, cb, cc, cd, ce, cf, gt.t2, tg.xlo, tg.xhi,
-                                 tg.ylo, tg.yhi, tg.zlo, tg.zhi);
-            // delta = mu - p = (mu - tile centre) - p', p' = local index - 3.5
-            mxl = p.x - (float)tg.x0 - 4.0f;
-            myl = p.y - (float)tg.y0 - 4.0f;
-            mzl = p.z - (float)tg.z0 - 4.0f;
-        }
     }
     __syncthreads();
     const bool any_live = __any(live);
     if (!any_live && partial == nullptr) return;
 
-    const float A2 = -0.5f * kLog2e * ca, Bn = -kLog2e * cb, Cn = -kLog2e * cc;
-    const float Dn = -0.5f * kLog2e * cd, En = -kLog2e * ce, Fn = -0.5f * kLog2e * cf;
-    const float shift = gt.shift, half = live ? gt.half : -1.f;
-
-    // Moments of h = a * G about the Gaussian's centre: S[..] = sum h * delta^k,
-    // delta = mu - p.  Per voxel: h, h*dx, h*dx^2 by FMAs against the lane's
-    // hoisted dx_u and dx_u^2; rows fold in dy, planes in dz.  Taking moments
-    // about the Gaussian (not the tile) keeps every sum well-conditioned: h is
-    // large only where |delta| is small.
-    float S0 = 0.f, Sx = 0.f, Sy = 0.f, Sz = 0.f;
-    float Sxx = 0.f, Sxy = 0.f, Sxz = 0.f, Syy = 0.f, Syz = 0.f, Szz = 0.f;
-    float dIa[C];
-#pragma unroll
-    for (int c = 0; c < C; ++c) dIa[c] = 0.f;
-    float dxu[GSV_TILE], dxu2[GSV_TILE];
-#pragma unroll
-    for (int u = 0; u < GSV_TILE; ++u) {
-        dxu[u] = mxl - ((float)u - 3.5f);
-        dxu2[u] = dxu[u] * dxu[u];
-    }
-
+    // Dead lanes evaluate a zero form at the dead offset (a = 0 on both paths).
+    const float A2 = live ? -0.5f * kLog2e * ca : 0.f, Bn = live ? -kLog2e * cb : 0.f;
+    const float Cn = live ? -kLog2e * cc : 0.f, Dn = live ? -0.5f * kLog2e * cd : 0.f;
+    const float En = live ? -kLog2e * ce : 0.f, Fn = live ? -0.5f * kLog2e * cf : 0.f;
     const int ny = min(GSV_TILE, H - tg.y0), nz = any_live ? min(GSV_TILE, D - tg.z0) : 0;
-    for (int lz = 0; lz < nz; ++lz) {
-        const float dz = mzl - ((float)lz - 3.5f);
-        const float Cdz = Cn * dz, Edz = En * dz;
-        const float R0z = fmaf(Fn * dz, dz, -shift);
-        float Q0 = 0.f, Qx = 0.f, Qxx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
-#pragma unroll
-        for (int ly = 0; ly < GSV_TILE; ++ly) {
-            if (ly >= ny) break;
-            const int row = lz * GSV_TILE + ly;
-            float gv[GSV_TILE * C];
-#pragma unroll
-            for (int q = 0; q < 2 * C; ++q) {
-                const float4 t4 = s_g[row][q];
-                gv[4 * q] = t4.x; gv[4 * q + 1] = t4.y; gv[4 * q + 2] = t4.z; gv[4 * q + 3] = t4.w;
-            }
-            const float dy = myl - ((float)ly - 3.5f);
-            const float R1 = fmaf(Bn, dy, Cdz);
-            const float R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
-            float W0 = 0.f, W1 = 0.f, W2 = 0.f;
-#pragma unroll
-            for (int u = 0; u < GSV_TILE; ++u) {
-                const float s = fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
-                const float a = (fabsf(s) <= half) ? __builtin_amdgcn_exp2f(s) : 0.f;
-                float h;
-                if (C == 1) {
-                    h = a * gv[u];
-                } else {
-                    float G = 0.f;
-#pragma unroll
-                    for (int c = 0; c < C; ++c) {
-                        G = fmaf(I[c], gv[u * C + c], G);
-                        dIa[c] = fmaf(a, gv[u * C + c], dIa[c]);
-                    }
-                    h = a * G;
-                }
-                W0 += h;
-                W1 = fmaf(h, dxu[u], W1);
-                W2 = fmaf(h, dxu2[u], W2);
-            }
-            Q0 += W0;
-            Qx += W1;
-            Qxx += W2;
-            Qy = fmaf(W0, dy, Qy);
-            Qxy = fmaf(W1, dy, Qxy);
-            Qyy = fmaf(W0, dy * dy, Qyy);
-        }
-        S0 += Q0;
-        Sx += Qx;
-        Sxx += Qxx;
-        Sy += Qy;
-        Sxy += Qxy;
-        Syy += Qyy;
-        Sz = fmaf(Q0, dz, Sz);
-        Sxz = fmaf(Qx, dz, Sxz);
-        Syz = fmaf(Qy, dz, Syz);
-        Szz = fmaf(Q0, dz * dz, Szz);
+    Moments<C> M;
+    double wscale;  // turns a sum of h into a sum of alpha * g
+    if (wave_fast) {
+        pair_moments<C, true>(s_g, ny, nz, mxl, myl, mzl, A2, Bn, Cn, Dn, En, Fn, 0.f,
+                              live ? gt.off : kDeadOffset, I, M);
+        wscale = live ? ldexp((double)gt.fscale, -gexp) : 0.0;
+    } else {
+        pair_moments<C, false>(s_g, ny, nz, mxl, myl, mzl, A2, Bn, Cn, Dn, En, Fn, gt.shift,
+                               live ? gt.half : -1.f, I, M);
+        wscale = live ? (double)gt.scale : 0.0;
     }
-    // sigma-gradient weight per unit of h: alpha = scale * a
-    const float w = live ? ((C == 1) ? gt.scale * I[0] : gt.scale) : 0.f;
+    // sigma-gradient weight per unit of h (alpha = scale * a); binary64 keeps the
+    // 2^-gexp and 2^-off factors in range
+    const double w = (C == 1) ? wscale * (double)I[0] : wscale;
     float out[9 + C];
-    out[0] = -0.5f * w * Sxx;
-    out[1] = -w * Sxy;
-    out[2] = -w * Sxz;
-    out[3] = -0.5f * w * Syy;
-    out[4] = -w * Syz;
-    out[5] = -0.5f * w * Szz;
-    out[6] = -w * (ca * Sx + cb * Sy + cc * Sz);
-    out[7] = -w * (cb * Sx + cd * Sy + ce * Sz);
-    out[8] = -w * (cc * Sx + ce * Sy + cf * Sz);
-    const float sc = live ? gt.scale : 0.f;
+    out[0] = (float)(-0.5 * w * (double)M.Sxx);
+    out[1] = (float)(-w * (double)M.Sxy);
+    out[2] = (float)(-w * (double)M.Sxz);
+    out[3] = (float)(-0.5 * w * (double)M.Syy);
+    out[4] = (float)(-w * (double)M.Syz);
+    out[5] = (float)(-0.5 * w * (double)M.Szz);
+    out[6] = (float)(-w * ((double)ca * M.Sx + (double)cb * M.Sy + (double)cc * M.Sz));
+    out[7] = (float)(-w * ((double)cb * M.Sx + (double)cd * M.Sy + (double)ce * M.Sz));
+    out[8] = (float)(-w * ((double)cc * M.Sx + (double)ce * M.Sy + (double)cf * M.Sz));
     if (C == 1) {
-        out[9] = sc * S0;
+        out[9] = (float)(wscale * (double)M.S0);
     } else {
 #pragma unroll
-        for (int c = 0; c < C; ++c) out[9 + c] = sc * dIa[c];
+        for (int c = 0; c < C; ++c) out[9 + c] = (float)(wscale * (double)M.dI[c]);
     }
     if (partial != nullptr) {
         // Deterministic path: this pair's partial goes to its emission slot

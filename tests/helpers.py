@@ -1,5 +1,7 @@
 """Shared helpers for the parity tests: run the HIP path and the CPU oracle on
 the same seeded inputs and compare them."""
+import os
+
 import numpy as np
 import torch
 
@@ -57,6 +59,13 @@ def report_close(name, got, ref, rtol, atol, bound=None):
     bad = ~(err <= allow)  # NaN counts as bad unless both NaN
     both_nan = np.isnan(got) & np.isnan(ref)
     bad &= ~both_nan
+    log = os.environ.get("GSV_MARGIN_LOG")
+    if log and err.size:
+        # worst fraction of the allowance used, to watch how close parity runs
+        with np.errstate(divide="ignore", invalid="ignore"):
+            used = np.where(both_nan, 0.0, err / allow)
+        with open(log, "a") as f:
+            f.write(f"{name}\t{float(np.nanmax(used)):.4g}\n")
     if bad.any():
         idx = np.argsort(-(err - allow).ravel())[:5]
         worst = [(np.unravel_index(i, got.shape), got.ravel()[i], ref.ravel()[i]) for i in idx]

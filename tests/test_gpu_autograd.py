@@ -46,7 +46,11 @@ def test_api_matches_oracle_pipeline(device, case, per_gaussian):
     cfg = work.cfg
     ref_fwd = O.pipeline(work.pos3d.numpy(), work.scale3d.numpy(), work.quat.numpy(),
                          work.intensities.numpy(), cfg.vol, cfg.world, cfg.center)
-    report_close(f"{case}: volume", np32(vol), ref_fwd["volume"], 1e-4, 1e-6)
+    _, amb = O.voxelize_fwd(cfg.vol, ref_fwd["gaussian_ids_sorted"], ref_fwd["tile_bins"],
+                            ref_fwd["pos3d_radii"], ref_fwd["conics"], work.intensities.numpy(),
+                            with_amb=True)
+    # gate-ambiguous terms (alpha*mean within 1e-4 of the threshold) may differ
+    report_close(f"{case}: volume", np32(vol), ref_fwd["volume"], 1e-4, 1e-6, bound=amb)
     tgt = np.broadcast_to(target.cpu().numpy()[..., None], ref_fwd["volume"].shape)
     g = l1_vol_grad(np32(vol), tgt)  # same sign pattern the GPU loss saw
     ref = O.pipeline(work.pos3d.numpy(), work.scale3d.numpy(), work.quat.numpy(),

@@ -177,3 +177,67 @@ def test_backward_cfg3_full_size_identity(device):
     assert abs(lhs - rhs) <= 1e-5 * scale, (lhs, rhs, scale)
     assert torch.isfinite(dp).all() and torch.isfinite(dc).all() and torch.isfinite(di).all()
     assert float(dp[:, 3].abs().sum()) == 0.0
+
+
+def _mixed_gate_inputs(work, P):
+    """Gaussians outside the gate-free domain, interleaved in the same tiles
+    (and backward waves) with ordinary ones: indefinite conics, means beyond
+    2^60 * 1e-6, channels spread far beyond their mean, and means below 1e-6."""
+    rng = np.random.default_rng(12)
+    n = work.pos3d.shape[0]
+    pr, cn = P["rpr"].copy(), P["rcn"].copy()
+    inten = work.intensities.numpy().copy()
+    k = rng.permutation(n)
+    indef, huge, spread, dead = k[:60], k[60:80], k[80:120], k[120:140]
+    cn[indef, 5] = -0.05 * np.abs(cn[indef, 5])  # negative zz entry: indefinite form
+    inten[huge] *= np.float32(1e14)               # log2(1e-6 / mean) < -60
+    inten[spread, 0] = 3e7                        # mean ~0.5, |I| ~ 2^25 * mean
+    inten[spread, 1] = -3e7 + 4  # binary32 spacing at 3e7 is 2: mean 2 exactly
+    inten[dead] = 5e-7                            # alpha * mean < 1e-6 everywhere
+    return pr, cn, inten
+
+
+def test_mixed_gate_paths_match_oracle(device):
+    """Exact-gate Gaussians sharing tiles with gate-free ones, forward and both
+    backward reductions."""
+    import gs_voxelizer.cuda as _C
+    cfg = small_config(1, 1500, vol=(24, 32, 28), channels=2)
+    work = S.make_gaussians(cfg, seed=12)
+    P = _prepare(work, device)
+    pr, cn, inten = _mixed_gate_inputs(work, P)
+    dpr, dcn, dI = (torch.from_numpy(x).to(device) for x in (pr, cn, inten))
+    vol = _C.voxelize_forward(cfg.vol, P["ids"], P["bins"], dpr, dcn, dI)
+    ref, amb = O.voxelize_fwd(cfg.vol, P["rids"], P["rbins"], pr, cn, inten, with_amb=True)
+    # Signed channels of magnitude 3e7 cancel to ~1e4 here, so the forward gets
+    # the conditioning term the gradients have.  The oracle on |I| bounds the sum
+    # of |terms| from above: mean(|I|) >= mean(I) only lowers the threshold.
+    cond = O.voxelize_fwd(cfg.vol, P["rids"], P["rbins"], pr, cn, np.abs(inten))
+    report_close("mixed gates: volume", np32(vol), ref, RTOL, ATOL, bound=amb + 1e-5 * cond)
+    g = np.random.default_rng(3).standard_normal(cfg.vol + (2,)).astype(np.float32)
+    rg, absum, ramb = O.voxelize_bwd(cfg.vol, P["rids"], P["rbins"], pr, cn, inten, g,
+                                     diagnostics=True)
+    for mode in MODES:
+        extra = (P["tmin"], P["tmax"], P["cum"]) if mode == "pairs" else ()
+        got = _C.voxelize_backward_per_gaussian(cfg.vol, P["ids"], P["bins"], dpr, dcn, dI,
+                                                torch.from_numpy(g).to(device), *extra)
+        for nm, a, b, s, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, rg, absum,
+                                  ramb):
+            report_close(f"mixed gates {mode}: {nm}", np32(a), b, RTOL, ATOL, bound=1e-5 * s + m)
+
+
+@pytest.mark.parametrize("e", [-60, 60])
+def test_backward_power_of_two_gradient_scaling_is_exact(device, e):
+    """The gradients are linear in vol_grad.  Scaling vol_grad by 2^e must scale
+    every gradient by exactly 2^e, bit for bit: the kernel stages each tile's
+    vol_grad with its own power-of-two scale, so tiny loss gradients (where
+    alpha * g would otherwise be denormal) lose nothing."""
+    work = S.make_gaussians(small_config(2, 6000, vol=(64, 64, 64)), seed=4)
+    cfg = work.cfg
+    P = _prepare(work, device)
+    g = torch.randn(cfg.vol + (1,), generator=torch.Generator().manual_seed(7)).to(device)
+    base = [t.cpu() for t in _gpu_bwd(P, cfg, g, 1, "pairs")]
+    scaled = [t.cpu() for t in _gpu_bwd(P, cfg, torch.ldexp(g, torch.tensor(float(e))), 1,
+                                        "pairs")]
+    for x, y in zip(base, scaled):
+        assert torch.equal(torch.ldexp(x, torch.tensor(float(e))), y)
+    assert float(base[2].abs().sum()) > 0
