@@ -148,12 +148,17 @@ __device__ __forceinline__ TileGeom tile_geom(int64_t tile, int Tx, int Ty, int 
 
 // ---------------------------------------------------------------- forward --
 
+// float4 slots of one prepared Gaussian record: 13 + C floats (gate-free
+// layout) or 12 + C (exact layout).
+template <int C>
+constexpr int kRecF4 = (13 + C + 3) / 4;
+
 template <int C>
 __global__ __launch_bounds__(kWave) void k_vox_fwd(
     int D, int H, int W, int Tx, int Ty, int64_t T, int64_t per, int n, int n_isect,
     const int *__restrict__ ids, const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
     const float2 *__restrict__ conics, const float *__restrict__ intens, float *__restrict__ vol) {
-    __shared__ float4 s_rec[kWave][4];
+    __shared__ float4 s_rec[kWave][kRecF4<C>];
     const int64_t tile = xcd_remap(blockIdx.x, per);
     if (tile >= T) return;
     const int lane = threadIdx.x;
@@ -195,28 +200,75 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                                         c45.x, c45.y);
                     // centred offsets: delta = c - p', p' = local index - 3.5
                     const float cx = p.x - (float)tg.x0 - 4.0f;
+                    const float cy = p.y - (float)tg.y0 - 4.0f, cz = p.z - (float)tg.z0 - 4.0f;
                     const float A2 = -0.5f * kLog2e * c01.x;
-                    s_rec[lane][0] = make_float4(cx, p.y - (float)tg.y0 - 4.0f,
-                                                 p.z - (float)tg.z0 - 4.0f, A2);
-                    s_rec[lane][1] = make_float4(-kLog2e * c01.y, -kLog2e * c23.x,
-                                                 -0.5f * kLog2e * c23.y, -kLog2e * c45.x);
-                    // gate-free: no shift inside the row constants, offset added per row
-                    s_rec[lane][2] = make_float4(-0.5f * kLog2e * c45.y, fast ? 0.f : gt.shift,
-                                                 fast ? gt.off : gt.half, A2 * cx);
-                    const float wscale = fast ? gt.fscale : gt.scale;
-                    float iw[4] = {0.f, 0.f, 0.f, 0.f};
+                    const float4 q1 = make_float4(-kLog2e * c01.y, -kLog2e * c23.x,
+                                                  -0.5f * kLog2e * c23.y, -kLog2e * c45.x);
+                    const float F = -0.5f * kLog2e * c45.y;
+                    float rec[4 * kRecF4<C>];
+                    if (fast) {
+                        // (cx, cy, cz, A2 cx | B, C, D, E | F, Q0, Q1, Q2 | Q3, I*2^-off ...),
+                        // Q_k = A2 * uc_k^2 + off for the four |uc| = 0.5, 1.5, 2.5, 3.5
+                        rec[0] = cx; rec[1] = cy; rec[2] = cz; rec[3] = A2 * cx;
+                        rec[4] = q1.x; rec[5] = q1.y; rec[6] = q1.z; rec[7] = q1.w;
+                        rec[8] = F;
 #pragma unroll
-                    for (int c = 0; c < C; ++c) iw[c] = I[c] * wscale;
-                    s_rec[lane][3] = make_float4(iw[0], iw[1], iw[2], iw[3]);
+                        for (int k = 0; k < 4; ++k) {
+                            const float uc = 0.5f + (float)k;
+                            rec[9 + k] = fmaf(A2, uc * uc, gt.off);
+                        }
+#pragma unroll
+                        for (int c = 0; c < C; ++c) rec[13 + c] = I[c] * gt.fscale;
+                    } else {
+                        // (cx, cy, cz, A2 | B, C, D, E | F, shift, half, A2 cx | I*2^shift)
+                        rec[0] = cx; rec[1] = cy; rec[2] = cz; rec[3] = A2;
+                        rec[4] = q1.x; rec[5] = q1.y; rec[6] = q1.z; rec[7] = q1.w;
+                        rec[8] = F; rec[9] = gt.shift; rec[10] = gt.half; rec[11] = A2 * cx;
+#pragma unroll
+                        for (int c = 0; c < C; ++c) rec[12 + c] = I[c] * gt.scale;
+                    }
+#pragma unroll
+                    for (int q = 0; q < kRecF4<C>; ++q)
+                        s_rec[lane][q] = make_float4(rec[4 * q], rec[4 * q + 1], rec[4 * q + 2],
+                                                     rec[4 * q + 3]);
                 }
             }
         }
-        uint64_t mask = __ballot(live);
-        const uint64_t fast_mask = __ballot(fast);
+        const uint64_t live_mask = __ballot(live);
+        uint64_t fmask = __ballot(fast);  // fast implies live
+        uint64_t smask = live_mask & ~fmask;
         __syncthreads();
-        while (mask) {
-            const int j = __builtin_ctzll(mask);
-            mask &= mask - 1;
+        // Gate-free Gaussians first, then the exact-gate ones of the batch: two
+        // single-path loops keep the accumulators in place (no copies per trip).
+        while (fmask) {
+            const int j = __builtin_ctzll(fmask);
+            fmask &= fmask - 1;
+            const float4 r0 = s_rec[j][0], r1 = s_rec[j][1], r2 = s_rec[j][2], r3 = s_rec[j][3];
+            float iw[C];
+            iw[0] = r3.y;
+            if (C > 1) iw[1] = r3.z;
+            if (C > 2) iw[2] = r3.w;
+            if (C > 3) iw[3] = s_rec[j][kRecF4<C> - 1].x;
+            const float dy = r0.y - py, dz = r0.z - pz;
+            // X = R1 + A2 cx, T1 = R1 + 2 A2 cx, T0 = s at the row centre (no offset)
+            const float X = fmaf(r1.x, dy, fmaf(r1.y, dz, r0.w));
+            const float T1 = X + r0.w;
+            const float R0 = fmaf(fmaf(r1.z, dy, r1.w * dz), dy, (r2.x * dz) * dz);
+            const float T0 = fmaf(r0.x, X, R0);
+            // s(u) = T0 - T1 uc + A2 uc^2 + off; voxels u and 7-u share uc^2
+            const float V[4] = {T0 + r2.y, T0 + r2.z, T0 + r2.w, T0 + r3.x};
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u) {
+                const float uc = (float)u - 3.5f;
+                const int k = u < 4 ? 3 - u : u - 4;
+                const float a = __builtin_amdgcn_exp2f(fmaf(-uc, T1, V[k]));
+#pragma unroll
+                for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
+            }
+        }
+        while (smask) {
+            const int j = __builtin_ctzll(smask);
+            smask &= smask - 1;
             const float4 r0 = s_rec[j][0], r1 = s_rec[j][1], r2 = s_rec[j][2], r3 = s_rec[j][3];
             const float iw[4] = {r3.x, r3.y, r3.z, r3.w};
             const float dy = r0.y - py, dz = r0.z - pz;
@@ -226,25 +278,13 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
             // around the row centre as T0 + u' * (A2 * u' - T1)
             const float T1 = R1 + 2.0f * r2.w;
             const float T0 = fmaf(r0.x, R1 + r2.w, R0);
-            if ((fast_mask >> j) & 1ull) {
-                // the offset enters once per row, after the small terms are summed
-                const float T0f = T0 + r2.z;
 #pragma unroll
-                for (int u = 0; u < GSV_TILE; ++u) {
-                    const float uc = (float)u - 3.5f;
-                    const float a = __builtin_amdgcn_exp2f(fmaf(uc, fmaf(uc, r0.w, -T1), T0f));
+            for (int u = 0; u < GSV_TILE; ++u) {
+                const float uc = (float)u - 3.5f;
+                const float s = fmaf(uc, fmaf(uc, r0.w, -T1), T0);
+                const float a = (fabsf(s) <= r2.z) ? __builtin_amdgcn_exp2f(s) : 0.f;
 #pragma unroll
-                    for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
-                }
-            } else {
-#pragma unroll
-                for (int u = 0; u < GSV_TILE; ++u) {
-                    const float uc = (float)u - 3.5f;
-                    const float s = fmaf(uc, fmaf(uc, r0.w, -T1), T0);
-                    const float a = (fabsf(s) <= r2.z) ? __builtin_amdgcn_exp2f(s) : 0.f;
-#pragma unroll
-                    for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
-                }
+                for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
             }
         }
         __syncthreads();
