@@ -8,86 +8,239 @@
 // gaussian-major and every pass is stable, the result is the reference's exact
 // order: ascending tile, then ascending gaussian id.
 //
-// Data movement per pair: emission writes 8 B; each radix pass reads 4 B
-// (histogram) + 8 B and writes 8 B; the range pass reads 4 B.
+// Kernels (7 launches for two passes):
+//   k_emit_chunk     block b writes emission slots [4096 b, 4096 b + 4096) and
+//                    the first pass's digit histogram of that chunk; it also
+//                    zero-fills tile_bins;
+//   k_digit_scan     one block per digit: exclusive prefix of the per-chunk
+//                    counts over chunks, plus the digit total;
+//   k_radix_scatter  stable scatter of one 4096-key chunk; ranks come from wave
+//                    ballots within each wave's contiguous 1024 keys, so the
+//                    block synchronises a handful of times per chunk;
+//   k_radix_hist     per-chunk digit histogram for the later passes;
+//   k_tile_edges     [start, end) per tile, 16 sorted keys per thread.
+// Every kernel reads the live pair count from device memory when one is given
+// (capped by the capacity its grid was sized for), so the host need not know
+// the count before launching.
+//
+// Data movement per pair: emission writes 8 B; each pass reads 8 B and writes
+// 8 B (later passes read 4 B more for the histogram); the range pass reads 4 B.
 #include "gsv_device.h"
 
 namespace gsv {
 namespace {
 
-constexpr int kEmitThreads = 256;
+constexpr int kChunk = 4096;  // keys per emission chunk and per scatter block
+constexpr int kEmitThreads = 512;
+constexpr int kEmitItems = kChunk / kEmitThreads;  // 8 consecutive slots per thread
+constexpr int kWindow = 4096;                       // Gaussians cached by an emission block
 constexpr int kSortThreads = 256;
-constexpr int kSortItems = 16;
-constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 keys per block
+constexpr int kSortWaves = kSortThreads / kWave;
+constexpr int kWaveKeys = kChunk / kSortWaves;  // 1024 contiguous keys per wave
+constexpr int kRounds = kWaveKeys / kWave;      // 16
 constexpr int kRadixBits = 8;
 constexpr int kRadixBins = 1 << kRadixBits;
+constexpr int kEdgeItems = 16;
+constexpr int kInvalidKey = 0x7fffffff;  // slot beyond its Gaussian's box: sorts last, no tile
 static_assert(kRadixBins == kSortThreads, "one digit per thread in the block scans");
+static_assert(kEmitItems == 8, "two int4 stores per thread");
 
-// One block emits the pairs of 256 consecutive Gaussians.  Their output ranges
-// are contiguous ([cum[g-1], cum[g])), so the block walks its whole output range
-// with coalesced stores and finds each slot's Gaussian by binary search in LDS,
-// instead of one serial loop per Gaussian (which stalls on large Gaussians).
-__global__ __launch_bounds__(kEmitThreads) void k_emit(
-    int n, int64_t n_isect, const int *__restrict__ tile_min, const int *__restrict__ tile_max,
-    const int *__restrict__ cum, int Tx, int Ty, int *__restrict__ keys, int *__restrict__ vals) {
-    __shared__ int s_start[kEmitThreads];
-    __shared__ int s_cnt[kEmitThreads];
-    __shared__ int s_box[kEmitThreads][5];  // min x, y, z; extent x, y
-    const int t = threadIdx.x;
-    const int g0 = blockIdx.x * kEmitThreads;
-    const int g = g0 + t;
-    const int last = min(g0 + kEmitThreads, n) - 1;
-    int start = 0, cnt = 0;
-    if (g < n) {
-        start = g == 0 ? 0 : cum[g - 1];
-        const int mnx = tile_min[3 * g], mny = tile_min[3 * g + 1], mnz = tile_min[3 * g + 2];
-        const int ex = tile_max[3 * g] - mnx, ey = tile_max[3 * g + 1] - mny,
-                  ez = tile_max[3 * g + 2] - mnz;
-        const int64_t box = (ex > 0 && ey > 0 && ez > 0) ? (int64_t)ex * ey * ez : 0;
-        const int64_t avail = (int64_t)cum[g] - start;
-        cnt = (int)max<int64_t>(0, min(box, avail));
-        s_box[t][0] = mnx; s_box[t][1] = mny; s_box[t][2] = mnz;
-        s_box[t][3] = max(ex, 1); s_box[t][4] = max(ey, 1);
-    } else {
-        start = 0x7fffffff;  // sorts after every real start
-    }
-    s_start[t] = start;
-    s_cnt[t] = cnt;
-    __syncthreads();
-    const int64_t lo = max<int64_t>(0, s_start[0]);
-    const int64_t hi = min<int64_t>(n_isect, (int64_t)cum[last]);
-    for (int64_t p = lo + t; p < hi; p += kEmitThreads) {
-        // largest l with s_start[l] <= p
-        int l = 0;
-#pragma unroll
-        for (int step = kEmitThreads / 2; step > 0; step >>= 1)
-            if (s_start[l + step] <= p) l += step;
-        const int j = (int)(p - s_start[l]);
-        if (j < 0 || j >= s_cnt[l]) continue;
-        const int nx = s_box[l][3], ny = s_box[l][4];
-        const int dx = j % nx, r = j / nx;
-        const int dy = r % ny, dz = r / ny;
-        keys[p] = (s_box[l][2] + dz) * Ty * Tx + (s_box[l][1] + dy) * Tx + (s_box[l][0] + dx);
-        vals[p] = g0 + l;
-    }
+__device__ __forceinline__ int64_t live_count(int64_t cap, const int64_t *d_n) {
+    if (!d_n) return cap;
+    const int64_t v = *d_n;
+    return v < 0 ? 0 : (v < cap ? v : cap);
 }
 
-// Per-block digit histogram, stored digit-major: hist[d * nblocks + block].
+// Block b writes the emission slots [b*kChunk, (b+1)*kChunk) of the pairs:
+// Gaussian-major, and for each Gaussian its box tiles z -> y -> x with x
+// fastest (bin_and_sort_gaussians.cu:11-35).  Slot p belongs to the Gaussian g
+// with cum[g-1] <= p < cum[g].  The block finds the first such Gaussian with a
+// 512-way cooperative search of cum, caches the next kWindow entries of cum in
+// LDS, and gives each thread 8 consecutive slots: one search and one division
+// per thread, then stepping through the box.  The chunk's digit histogram for
+// the first radix pass is written digit-major: hist[d * nblocks + b].
+__global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
+    int n, int64_t cap, const int64_t *__restrict__ d_n, const int *__restrict__ tile_min,
+    const int *__restrict__ tile_max, const int *__restrict__ cum, int Tx, int Ty, int64_t T,
+    int *__restrict__ keys, int *__restrict__ vals, int *__restrict__ hist, int nblocks,
+    int2 *__restrict__ tile_bins) {
+    __shared__ int s_cum[kWindow];
+    __shared__ int s_hist[kRadixBins];
+    const int t = threadIdx.x;
+    for (int64_t i = (int64_t)blockIdx.x * kEmitThreads + t; i < T;
+         i += (int64_t)gridDim.x * kEmitThreads)
+        tile_bins[i] = make_int2(0, 0);
+    if (t < kRadixBins) s_hist[t] = 0;
+    const int64_t total = live_count(cap, d_n);
+    const int64_t base = (int64_t)blockIdx.x * kChunk;
+
+    // g_lo = min{g : cum[g] > base}, or n.  Invariant: cum[g] <= base for g < lo,
+    // and hi == n or cum[hi] > base.  Each round probes kEmitThreads points of
+    // [lo, hi) and keeps the interval between the last "<=" and the first ">".
+    int lo = 0, hi = n;
+    if (base < total) {
+        while (lo < hi) {
+            const int64_t span = hi - lo;
+            const int q = lo + (int)((span * t) / kEmitThreads);
+            const int c = __syncthreads_count(cum[q] <= base);
+            if (c == 0) { hi = lo; break; }
+            const int qa = lo + (int)((span * (c - 1)) / kEmitThreads);
+            const int qb = c < kEmitThreads ? lo + (int)((span * c) / kEmitThreads) : hi;
+            lo = qa + 1;
+            hi = qb > lo ? qb : lo;
+        }
+    }
+    const int g_lo = lo;
+    const int wlen = base < total ? min(kWindow, n - g_lo) : 0;
+    for (int i = t; i < wlen; i += kEmitThreads) s_cum[i] = cum[g_lo + i];
+    const int prev = g_lo > 0 ? cum[g_lo - 1] : 0;
+    __syncthreads();
+
+    const int64_t p0 = base + (int64_t)t * kEmitItems;
+    if (p0 < total) {
+        // cum at window index i (global beyond the window)
+        auto cum_at = [&](int i) -> int { return i < wlen ? s_cum[i] : cum[g_lo + i]; };
+        // l = min{i : cum_at(i) > p0}, searched in the window, then beyond it
+        int l;
+        if (wlen > 0 && (int64_t)s_cum[wlen - 1] > p0) {
+            int a = 0, b = wlen - 1;
+            while (a < b) {
+                const int m = (a + b) >> 1;
+                if ((int64_t)s_cum[m] > p0) b = m; else a = m + 1;
+            }
+            l = a;
+        } else {
+            int a = wlen, b = n - g_lo;  // answer in [wlen, n - g_lo]
+            while (a < b) {
+                const int m = (a + b) >> 1;
+                if ((int64_t)cum[g_lo + m] > p0) b = m; else a = m + 1;
+            }
+            l = a;
+        }
+        int key[kEmitItems], val[kEmitItems];
+        int g = g_lo + l;
+        int start = l == 0 ? prev : cum_at(l - 1);
+        int end = g < n ? cum_at(l) : start;
+        int mnx = 0, mny = 0, mnz = 0, ex = 0, ey = 0, ez = 0, dx = 0, dy = 0, dz = 0;
+        auto load_box = [&](int j) {
+            mnx = tile_min[3 * g]; mny = tile_min[3 * g + 1]; mnz = tile_min[3 * g + 2];
+            ex = tile_max[3 * g] - mnx; ey = tile_max[3 * g + 1] - mny; ez = tile_max[3 * g + 2] - mnz;
+            if (ex > 0 && ey > 0 && ez > 0) {
+                const unsigned r = (unsigned)j / (unsigned)ex;
+                dx = j - (int)r * ex;
+                dy = (int)(r % (unsigned)ey);
+                dz = (int)(r / (unsigned)ey);
+            }
+        };
+        if (g < n) load_box((int)(p0 - start));
+#pragma unroll
+        for (int k = 0; k < kEmitItems; ++k) {
+            const int64_t p = p0 + k;
+            if (p >= total || g >= n) {
+                key[k] = kInvalidKey;
+                val[k] = 0;
+                continue;
+            }
+            if (p >= end) {  // next non-empty Gaussian
+                do {
+                    ++l;
+                    ++g;
+                    start = end;
+                    end = g < n ? cum_at(l) : start;
+                } while (g < n && p >= end);
+                if (g >= n) { key[k] = kInvalidKey; val[k] = 0; continue; }
+                dx = dy = dz = 0;
+                load_box((int)(p - start));
+            }
+            val[k] = g;
+            // a slot past the box (cum inconsistent with the box) gets no tile
+            key[k] = (ex > 0 && ey > 0 && dz < ez)
+                         ? (mnz + dz) * Ty * Tx + (mny + dy) * Tx + (mnx + dx)
+                         : kInvalidKey;
+            if (++dx == ex) { dx = 0; if (++dy == ey) { dy = 0; ++dz; } }
+        }
+        // slots [p0, p0 + 8): two 16-byte stores when whole and aligned
+        if (p0 + kEmitItems <= total) {
+            int4 *k4 = reinterpret_cast<int4 *>(keys + p0);
+            int4 *v4 = reinterpret_cast<int4 *>(vals + p0);
+            k4[0] = make_int4(key[0], key[1], key[2], key[3]);
+            k4[1] = make_int4(key[4], key[5], key[6], key[7]);
+            v4[0] = make_int4(val[0], val[1], val[2], val[3]);
+            v4[1] = make_int4(val[4], val[5], val[6], val[7]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kEmitItems; ++k)
+                if (p0 + k < total) { keys[p0 + k] = key[k]; vals[p0 + k] = val[k]; }
+        }
+#pragma unroll
+        for (int k = 0; k < kEmitItems; ++k)
+            if (p0 + k < total) atomicAdd(&s_hist[key[k] & (kRadixBins - 1)], 1);
+    }
+    __syncthreads();
+    if (t < kRadixBins) hist[(int64_t)t * nblocks + blockIdx.x] = s_hist[t];
+}
+
+// Per-chunk digit histogram of a later pass, digit-major; chunks past the live
+// count write zeros.
 __global__ __launch_bounds__(kSortThreads) void k_radix_hist(const int *__restrict__ keys,
-                                                             int64_t n, int shift,
-                                                             int *__restrict__ hist, int nblocks) {
+                                                             int64_t cap,
+                                                             const int64_t *__restrict__ d_n,
+                                                             int shift, int *__restrict__ hist,
+                                                             int nblocks) {
     __shared__ int s_hist[kRadixBins];
     const int t = threadIdx.x;
     s_hist[t] = 0;
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    const int64_t n = live_count(cap, d_n);
+    const int64_t base = (int64_t)blockIdx.x * kChunk;
 #pragma unroll
-    for (int k = 0; k < kSortItems; ++k) {
-        const int64_t i = base + (int64_t)k * kSortThreads + t;
-        if (i < n) atomicAdd(&s_hist[(keys[i] >> shift) & (kRadixBins - 1)], 1);
+    for (int q = 0; q < kChunk / kSortThreads / 4; ++q) {
+        const int64_t i = base + 4 * ((int64_t)q * kSortThreads + t);
+        if (i + 4 <= n) {
+            const int4 k4 = *reinterpret_cast<const int4 *>(keys + i);
+            atomicAdd(&s_hist[(k4.x >> shift) & (kRadixBins - 1)], 1);
+            atomicAdd(&s_hist[(k4.y >> shift) & (kRadixBins - 1)], 1);
+            atomicAdd(&s_hist[(k4.z >> shift) & (kRadixBins - 1)], 1);
+            atomicAdd(&s_hist[(k4.w >> shift) & (kRadixBins - 1)], 1);
+        } else {
+            for (int64_t j = i; j < n && j < i + 4; ++j)
+                atomicAdd(&s_hist[(keys[j] >> shift) & (kRadixBins - 1)], 1);
+        }
     }
     __syncthreads();
     hist[(int64_t)t * nblocks + blockIdx.x] = s_hist[t];
+}
+
+// Block d turns hist[d][0..nblocks) into its exclusive prefix over chunks and
+// writes the digit total.
+__global__ __launch_bounds__(kSortThreads) void k_digit_scan(int *__restrict__ hist, int nblocks,
+                                                             int *__restrict__ totals) {
+    __shared__ int s_wtot[kSortWaves];
+    const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
+    int *row = hist + (int64_t)blockIdx.x * nblocks;
+    int carry = 0;
+    for (int s = 0; s < nblocks; s += kSortThreads) {
+        const int i = s + t;
+        const int v = i < nblocks ? row[i] : 0;
+        int inc = v;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int o = __shfl_up(inc, d, kWave);
+            if (lane >= d) inc += o;
+        }
+        if (lane == kWave - 1) s_wtot[wave] = inc;
+        __syncthreads();
+        int off = carry, sum = 0;
+#pragma unroll
+        for (int w = 0; w < kSortWaves; ++w) {
+            off += w < wave ? s_wtot[w] : 0;
+            sum += s_wtot[w];
+        }
+        if (i < nblocks) row[i] = off + inc - v;
+        carry += sum;
+        __syncthreads();
+    }
+    if (t == 0) totals[blockIdx.x] = carry;
 }
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
@@ -95,40 +248,62 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
     return lane == 0 ? 0ull : (~0ull >> (kWave - lane));
 }
 
-// Stable scatter of one 4096-key tile.  Ranks are computed in the tile's
-// original order (round, wave, lane) with wave ballots, staged sorted in LDS,
-// then written out so that consecutive lanes store consecutive addresses of the
-// same digit run.
+// Exclusive scan of one int per thread across the 256-thread block.
+__device__ __forceinline__ int block_excl_scan(int v, int *s_wtot) {
+    const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
+    int inc = v;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int o = __shfl_up(inc, d, kWave);
+        if (lane >= d) inc += o;
+    }
+    if (lane == kWave - 1) s_wtot[wave] = inc;
+    __syncthreads();
+    int off = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) off += w < wave ? s_wtot[w] : 0;
+    return off + inc - v;
+}
+
+// Stable scatter of one 4096-key chunk.  Wave w owns keys [w*1024, (w+1)*1024)
+// of the chunk and ranks them round by round (64 keys a round) against its own
+// running digit counts in LDS; after one barrier the per-wave counts become
+// offsets, keys are staged digit-sorted in LDS and written out so that
+// consecutive lanes store consecutive addresses of the same digit run.
 __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
     const int *__restrict__ kin, const int *__restrict__ vin, int *__restrict__ kout,
-    int *__restrict__ vout, int64_t n, int shift, const int *__restrict__ hist_scanned, int nblocks) {
-    __shared__ int s_keys[kSortTile];
-    __shared__ int s_vals[kSortTile];
-    __shared__ int s_wave_cnt[kSortThreads / kWave][kRadixBins];
-    __shared__ int s_running[kRadixBins];
-    __shared__ int s_tile_start[kRadixBins];
+    int *__restrict__ vout, int64_t cap, const int64_t *__restrict__ d_n, int shift,
+    const int *__restrict__ hist_scanned, const int *__restrict__ totals, int nblocks) {
+    __shared__ int s_keys[kChunk];
+    __shared__ int s_vals[kChunk];
+    __shared__ int s_wcnt[kSortWaves][kRadixBins];
+    __shared__ int s_start[kRadixBins];
     __shared__ int s_gbase[kRadixBins];
-    __shared__ int s_wtot[kSortThreads / kWave];
+    __shared__ int s_wtot[kSortWaves];
     const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    s_running[t] = 0;
-    s_gbase[t] = hist_scanned[(int64_t)t * nblocks + blockIdx.x];
+    const int64_t n = live_count(cap, d_n);
+    const int64_t base = (int64_t)blockIdx.x * kChunk;
+    if (base >= n) return;
 #pragma unroll
-    for (int w = 0; w < kSortThreads / kWave; ++w) s_wave_cnt[w][t] = 0;
-
-    int key[kSortItems], val[kSortItems], rank[kSortItems];
-#pragma unroll
-    for (int k = 0; k < kSortItems; ++k) {
-        const int64_t i = base + (int64_t)k * kSortThreads + t;
-        key[k] = i < n ? kin[i] : 0;
-        val[k] = i < n ? vin[i] : 0;
-        rank[k] = 0;
+    for (int w = 0; w < kSortWaves; ++w) s_wcnt[w][t] = 0;
+    {   // global start of this chunk's run of digit t
+        const int dbase = block_excl_scan(totals[t], s_wtot);
+        s_gbase[t] = dbase + hist_scanned[(int64_t)t * nblocks + blockIdx.x];
     }
     __syncthreads();
+
+    const int64_t wbase = base + (int64_t)wave * kWaveKeys;
+    int key[kRounds], val[kRounds], rank[kRounds];
+#pragma unroll
+    for (int k = 0; k < kRounds; ++k) {
+        const int64_t i = wbase + k * kWave + lane;
+        key[k] = i < n ? kin[i] : 0;
+        val[k] = i < n ? vin[i] : 0;
+    }
     const uint64_t lt = lanemask_lt();
 #pragma unroll
-    for (int k = 0; k < kSortItems; ++k) {
-        const bool valid = base + (int64_t)k * kSortThreads + t < n;
+    for (int k = 0; k < kRounds; ++k) {
+        const bool valid = wbase + k * kWave + lane < n;
         const int d = (key[k] >> shift) & (kRadixBins - 1);
         uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -138,98 +313,157 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
             peers &= bit ? m : ~m;
         }
         const int r = __popcll(peers & lt);
-        if (valid && r == 0) s_wave_cnt[wave][d] = __popcll(peers);
-        __syncthreads();
-        if (valid) {
-            int off = s_running[d];
-            for (int w = 0; w < wave; ++w) off += s_wave_cnt[w][d];
-            rank[k] = off + r;
-        }
-        __syncthreads();
-        int add = 0;
-#pragma unroll
-        for (int w = 0; w < kSortThreads / kWave; ++w) {
-            add += s_wave_cnt[w][t];
-            s_wave_cnt[w][t] = 0;
-        }
-        s_running[t] += add;
-        __syncthreads();
+        // one wave reads then updates its own counters: LDS keeps the order
+        const int off = s_wcnt[wave][d];
+        rank[k] = off + r;
+        if (valid && r == 0) s_wcnt[wave][d] = off + __popcll(peers);
     }
-    // exclusive scan of the tile's digit counts (one digit per thread)
-    {
-        const int c = s_running[t];
-        int v = c;
+    __syncthreads();
+    {   // per-digit wave offsets, then the chunk's digit starts
+        int c[kSortWaves], sum = 0;
 #pragma unroll
-        for (int dd = 1; dd < kWave; dd <<= 1) {
-            const int o = __shfl_up(v, dd, kWave);
-            if (lane >= dd) v += o;
+        for (int w = 0; w < kSortWaves; ++w) {
+            c[w] = s_wcnt[w][t];
+            s_wcnt[w][t] = sum;
+            sum += c[w];
         }
-        if (lane == kWave - 1) s_wtot[wave] = v;
-        __syncthreads();
-        int off = 0;
-        for (int w = 0; w < wave; ++w) off += s_wtot[w];
-        s_tile_start[t] = off + v - c;
+        __syncthreads();  // s_wtot is reused by the scan below
+        s_start[t] = block_excl_scan(sum, s_wtot);
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kSortItems; ++k) {
-        const bool valid = base + (int64_t)k * kSortThreads + t < n;
-        if (valid) {
+    for (int k = 0; k < kRounds; ++k) {
+        if (wbase + k * kWave + lane < n) {
             const int d = (key[k] >> shift) & (kRadixBins - 1);
-            const int pos = s_tile_start[d] + rank[k];
+            const int pos = s_start[d] + s_wcnt[wave][d] + rank[k];
             s_keys[pos] = key[k];
             s_vals[pos] = val[k];
         }
     }
     __syncthreads();
-    const int n_here = (int)min<int64_t>(kSortTile, n - base);
+    const int n_here = (int)min<int64_t>(kChunk, n - base);
 #pragma unroll
-    for (int k = 0; k < kSortItems; ++k) {
+    for (int k = 0; k < kChunk / kSortThreads; ++k) {
         const int p = k * kSortThreads + t;
         if (p < n_here) {
             const int kk = s_keys[p];
             const int d = (kk >> shift) & (kRadixBins - 1);
-            const int64_t dst = (int64_t)s_gbase[d] + (p - s_tile_start[d]);
+            const int64_t dst = (int64_t)s_gbase[d] + (p - s_start[d]);
             kout[dst] = kk;
             vout[dst] = s_vals[p];
         }
     }
 }
 
-// tile_bins[t] = [first, last+1) of tile t in the sorted keys; other tiles keep
-// the zeros written before (bin_and_sort_gaussians.cu:40-62).
-__global__ __launch_bounds__(256) void k_tile_edges(const int *__restrict__ keys, int64_t n,
+// tile_bins[t] = [first, last+1) of tile t in the sorted keys; tiles without
+// pairs keep the zeros k_emit_chunk wrote (bin_and_sort_gaussians.cu:40-62).
+__global__ __launch_bounds__(256) void k_tile_edges(const int *__restrict__ keys, int64_t cap,
+                                                    const int64_t *__restrict__ d_n,
                                                     int64_t n_tiles, int2 *__restrict__ bins) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const int k = keys[i];
-    if (k < 0 || k >= n_tiles) return;
-    if (i == 0 || keys[i - 1] != k) bins[k].x = (int)i;
-    if (i == n - 1 || keys[i + 1] != k) bins[k].y = (int)(i + 1);
+    const int64_t n = live_count(cap, d_n);
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kEdgeItems;
+    if (i0 >= n) return;
+    int k[kEdgeItems + 1];
+    if (i0 + kEdgeItems <= n) {
+        const int4 *k4 = reinterpret_cast<const int4 *>(keys + i0);
+#pragma unroll
+        for (int q = 0; q < kEdgeItems / 4; ++q) {
+            const int4 v = k4[q];
+            k[4 * q] = v.x; k[4 * q + 1] = v.y; k[4 * q + 2] = v.z; k[4 * q + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < kEdgeItems; ++q) k[q] = i0 + q < n ? keys[i0 + q] : kInvalidKey;
+    }
+    k[kEdgeItems] = i0 + kEdgeItems < n ? keys[i0 + kEdgeItems] : kInvalidKey;
+    int before = i0 > 0 ? keys[i0 - 1] : kInvalidKey;
+#pragma unroll
+    for (int q = 0; q < kEdgeItems; ++q) {
+        const int64_t i = i0 + q;
+        const int kk = k[q];
+        if (i < n && kk >= 0 && kk < n_tiles) {
+            if (before != kk) bins[kk].x = (int)i;
+            if (i == n - 1 || k[q + 1] != kk) bins[kk].y = (int)(i + 1);
+        }
+        before = kk;
+    }
 }
 
 struct BinLayout {
-    size_t keys_a, vals_a, keys_b, hist, scan, total;
+    size_t keys_a, vals_a, keys_b, hist, totals, total;
     int passes, nblocks;
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-BinLayout bin_layout(int64_t n_isect, int64_t n_tiles) {
+BinLayout bin_layout(int64_t cap, int64_t n_tiles) {
     BinLayout L{};
     int bits = 0;
     while (bits < 31 && ((int64_t)1 << bits) < n_tiles) ++bits;
     L.passes = (bits + kRadixBits - 1) / kRadixBits;
-    L.nblocks = (int)((n_isect + kSortTile - 1) / kSortTile);
-    const size_t arr = align256((size_t)n_isect * sizeof(int));
+    L.nblocks = (int)((cap + kChunk - 1) / kChunk);
+    const size_t arr = align256((size_t)cap * sizeof(int));
     size_t off = 0;
     L.keys_a = off; off += arr;
     L.vals_a = off; off += arr;
     L.keys_b = off; off += arr;
-    L.hist = off; off += align256((size_t)kRadixBins * L.nblocks * sizeof(int));
-    L.scan = off; off += scan_workspace_bytes((int64_t)kRadixBins * L.nblocks);
-    L.total = off; off += 256;
+    L.hist = off; off += align256((size_t)kRadixBins * imax64(L.nblocks, 1) * sizeof(int));
+    L.totals = off; off += align256(kRadixBins * sizeof(int));
+    L.total = off;
     return L;
+}
+
+int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *tile_min,
+                 const int32_t *tile_max, const int32_t *cum, int32_t D, int32_t H, int32_t W,
+                 void *workspace, size_t workspace_bytes, int32_t *ids_out, int32_t *tile_bins,
+                 hipStream_t s) {
+    if (n < 0 || D <= 0 || H <= 0 || W <= 0 || !tile_bins) return GSV_ERR_INVALID_ARGUMENT;
+    if (cap > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
+    const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
+    const int64_t T = (int64_t)Tx * Ty * Tz;
+    if (T > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
+    if (cap <= 0 || n == 0) return fill_zero_u32(tile_bins, 2 * T, s);
+    if (!tile_min || !tile_max || !cum || !ids_out || !workspace) return GSV_ERR_INVALID_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(ids_out) & 15) != 0) return GSV_ERR_INVALID_ARGUMENT;
+    const BinLayout L = bin_layout(cap, T);
+    if (workspace_bytes < L.total + 256) return GSV_ERR_WORKSPACE_TOO_SMALL;
+    char *ws = static_cast<char *>(workspace);
+    ws += (256 - (reinterpret_cast<uintptr_t>(ws) & 255)) & 255;  // 16-byte vector access
+    int *ka = reinterpret_cast<int *>(ws + L.keys_a);
+    int *va = reinterpret_cast<int *>(ws + L.vals_a);
+    int *kb = reinterpret_cast<int *>(ws + L.keys_b);
+    int *vb = ids_out;
+    int *hist = reinterpret_cast<int *>(ws + L.hist);
+    int *totals = reinterpret_cast<int *>(ws + L.totals);
+    // Emit into the pair of buffers that leaves the final pass in (kb, vb).
+    int *kin = (L.passes % 2 == 0) ? kb : ka;
+    int *vin = (L.passes % 2 == 0) ? vb : va;
+    hipLaunchKernelGGL(k_emit_chunk, dim3(L.nblocks), dim3(kEmitThreads), 0, s, n, cap, d_count,
+                       tile_min, tile_max, cum, Tx, Ty, T, kin, vin, hist, L.nblocks,
+                       reinterpret_cast<int2 *>(tile_bins));
+    if (int st = check_launch()) return st;
+    for (int p = 0; p < L.passes; ++p) {
+        int *kout = (kin == ka) ? kb : ka;
+        int *vout = (vin == va) ? vb : va;
+        const int shift = p * kRadixBits;
+        if (p > 0) {
+            hipLaunchKernelGGL(k_radix_hist, dim3(L.nblocks), dim3(kSortThreads), 0, s, kin, cap,
+                               d_count, shift, hist, L.nblocks);
+            if (int st = check_launch()) return st;
+        }
+        hipLaunchKernelGGL(k_digit_scan, dim3(kRadixBins), dim3(kSortThreads), 0, s, hist,
+                           L.nblocks, totals);
+        if (int st = check_launch()) return st;
+        hipLaunchKernelGGL(k_radix_scatter, dim3(L.nblocks), dim3(kSortThreads), 0, s, kin, vin,
+                           kout, vout, cap, d_count, shift, hist, totals, L.nblocks);
+        if (int st = check_launch()) return st;
+        kin = kout;
+        vin = vout;
+    }
+    const int64_t threads = (cap + kEdgeItems - 1) / kEdgeItems;
+    hipLaunchKernelGGL(k_tile_edges, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, kin,
+                       cap, d_count, T, reinterpret_cast<int2 *>(tile_bins));
+    return check_launch();
 }
 
 }  // namespace
@@ -251,48 +485,20 @@ extern "C" int gsv_bin_and_sort(int32_t n, int64_t num_intersects, const int32_t
                                 const int32_t *tile_max, const int32_t *cum_tiles_hit, int32_t D,
                                 int32_t H, int32_t W, void *workspace, size_t workspace_bytes,
                                 int32_t *gaussian_ids_sorted, int32_t *tile_bins, void *stream) {
-    if (n < 0 || D <= 0 || H <= 0 || W <= 0 || !tile_bins) return GSV_ERR_INVALID_ARGUMENT;
-    if (num_intersects > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
-    const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
-    const int64_t T = (int64_t)Tx * Ty * Tz;
-    if (T > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
-    hipStream_t s = as_stream(stream);
-    if (int st = fill_zero_u32(tile_bins, 2 * T, s)) return st;
-    if (num_intersects <= 0 || n == 0) return GSV_OK;
-    if (!tile_min || !tile_max || !cum_tiles_hit || !gaussian_ids_sorted || !workspace)
-        return GSV_ERR_INVALID_ARGUMENT;
-    const int64_t I = num_intersects;
-    const BinLayout L = bin_layout(I, T);
-    if (workspace_bytes < L.total + 256) return GSV_ERR_WORKSPACE_TOO_SMALL;
-    char *ws = static_cast<char *>(workspace);
-    int *ka = reinterpret_cast<int *>(ws + L.keys_a);
-    int *va = reinterpret_cast<int *>(ws + L.vals_a);
-    int *kb = reinterpret_cast<int *>(ws + L.keys_b);
-    int *vb = gaussian_ids_sorted;
-    int *hist = reinterpret_cast<int *>(ws + L.hist);
-    // Emit into the pair of buffers that leaves the final pass in (kb, vb).
-    int *kin = (L.passes % 2 == 0) ? kb : ka;
-    int *vin = (L.passes % 2 == 0) ? vb : va;
-    hipLaunchKernelGGL(k_emit, dim3((n + kEmitThreads - 1) / kEmitThreads), dim3(kEmitThreads), 0,
-                       s, n, I, tile_min, tile_max, cum_tiles_hit, Tx, Ty, kin, vin);
-    if (int st = check_launch()) return st;
-    for (int p = 0; p < L.passes; ++p) {
-        int *kout = (kin == ka) ? kb : ka;
-        int *vout = (vin == va) ? vb : va;
-        const int shift = p * kRadixBits;
-        hipLaunchKernelGGL(k_radix_hist, dim3(L.nblocks), dim3(kSortThreads), 0, s, kin, I, shift,
-                           hist, L.nblocks);
-        if (int st = check_launch()) return st;
-        if (int st = scan_i32(hist, hist, (int64_t)kRadixBins * L.nblocks, false, nullptr,
-                              ws + L.scan, scan_workspace_bytes((int64_t)kRadixBins * L.nblocks), s))
-            return st;
-        hipLaunchKernelGGL(k_radix_scatter, dim3(L.nblocks), dim3(kSortThreads), 0, s, kin, vin,
-                           kout, vout, I, shift, hist, L.nblocks);
-        if (int st = check_launch()) return st;
-        kin = kout;
-        vin = vout;
-    }
-    hipLaunchKernelGGL(k_tile_edges, dim3((unsigned)((I + 255) / 256)), dim3(256), 0, s, kin, I, T,
-                       reinterpret_cast<int2 *>(tile_bins));
-    return check_launch();
+    return bin_and_sort(n, num_intersects, nullptr, tile_min, tile_max, cum_tiles_hit, D, H, W,
+                        workspace, workspace_bytes, gaussian_ids_sorted, tile_bins,
+                        as_stream(stream));
+}
+
+extern "C" int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity,
+                                             const int64_t *num_intersects_dev,
+                                             const int32_t *tile_min, const int32_t *tile_max,
+                                             const int32_t *cum_tiles_hit, int32_t D, int32_t H,
+                                             int32_t W, void *workspace, size_t workspace_bytes,
+                                             int32_t *gaussian_ids_sorted, int32_t *tile_bins,
+                                             void *stream) {
+    if (!num_intersects_dev) return GSV_ERR_INVALID_ARGUMENT;
+    return bin_and_sort(n, capacity, num_intersects_dev, tile_min, tile_max, cum_tiles_hit, D, H,
+                        W, workspace, workspace_bytes, gaussian_ids_sorted, tile_bins,
+                        as_stream(stream));
 }

@@ -164,6 +164,38 @@ def bin_and_sort_gaussians(num_gaussians: int, num_intersects: int, tile_min, ti
     return ids, tile_bins
 
 
+def bin_and_sort_gaussians_device_count(num_gaussians: int, capacity: int, num_intersects_dev,
+                                        tile_min, tile_max, cum_tiles_hit, vol_size):
+    """Binning without the host read of the pair count (voxelize.py:87-88).
+
+    num_intersects_dev is a (1,) int64 device tensor, e.g. the total returned by
+    cumsum_tiles_hit.  Returns (gaussian_ids_sorted (capacity,), tile_bins (T,2)):
+    the first min(count, capacity) ids are sorted, and the result is complete only
+    when count <= capacity, which the caller checks once the count is on the host.
+    """
+    for t, w in ((tile_min, "tile_min"), (tile_max, "tile_max"), (cum_tiles_hit, "cum_tiles_hit"),
+                 (num_intersects_dev, "num_intersects_dev")):
+        _check_input(t, w)
+    for t, w in ((tile_min, "tile_min"), (tile_max, "tile_max"), (cum_tiles_hit, "cum_tiles_hit")):
+        _check_dtype(t, w, torch.int32)
+    _check_dtype(num_intersects_dev, "num_intersects_dev", torch.int64)
+    Tx, Ty, Tz = _tiles(vol_size)
+    D, H, W = (int(v) for v in vol_size)
+    dev = tile_min.device
+    n, cap = int(num_gaussians), max(int(capacity), 0)
+    i32 = dict(device=dev, dtype=torch.int32)
+    tile_bins = torch.empty((Tx * Ty * Tz, 2), **i32)
+    ids = torch.empty((cap,), **i32)
+    nbytes = ctypes.c_size_t(0)
+    _call("bin_workspace_bytes", n, cap, D, H, W, ctypes.byref(nbytes))
+    ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        _call("bin_and_sort_device_count", n, cap, _ptr(num_intersects_dev), _ptr(tile_min),
+              _ptr(tile_max), _ptr(cum_tiles_hit), D, H, W, _ptr(ws), nbytes.value, _ptr(ids),
+              _ptr(tile_bins), _stream(dev))
+    return ids, tile_bins
+
+
 def _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities):
     for t, w in ((gaussian_ids_sorted, "gaussian_ids_sorted"), (tile_bins, "tile_bins"),
                  (pos3d, "pos3d"), (conics, "conics"), (intensities, "intensities")):

@@ -108,6 +108,24 @@ int gsv_bin_and_sort(int32_t n, int64_t num_intersects, const int32_t *tile_min,
                      int32_t *gaussian_ids_sorted, int32_t *tile_bins, void *stream);
 
 /*
+ * Binning with the pair count left on the device.  Replaces the same reference
+ * path as gsv_bin_and_sort, minus the host read of the count
+ * (voxelize.py:87-88, `cum_tiles_hit[-1].item()`).  The kernels read the live
+ * count I = *num_intersects_dev (an int64, e.g. the total written by
+ * gsv_cumsum_tiles_hit) and sort min(I, capacity) pairs.  Grids, the workspace
+ * (gsv_bin_workspace_bytes with num_intersects = capacity) and
+ * gaussian_ids_sorted (capacity entries, 16-byte aligned) are sized by
+ * capacity.  When I > capacity the output is incomplete: the caller compares
+ * I with capacity once the count reaches the host, and runs again with a
+ * larger capacity.
+ */
+int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity, const int64_t *num_intersects_dev,
+                                  const int32_t *tile_min, const int32_t *tile_max,
+                                  const int32_t *cum_tiles_hit, int32_t D, int32_t H, int32_t W,
+                                  void *workspace, size_t workspace_bytes,
+                                  int32_t *gaussian_ids_sorted, int32_t *tile_bins, void *stream);
+
+/*
  * Forward voxelization.  Replaces voxelize_forward_torch (bindings.cu:362-457;
  * kernel voxelize.cu:39-164).  volume (D,H,W,channels) float32 is fully written.
  * n = number of Gaussians (rows of pos3d_radii / conics / intensities).

@@ -63,3 +63,93 @@ def test_binning_empty(device):
     torch.cuda.synchronize()
     assert ids.numel() == 0
     assert bins.shape == (2 * 2 * 3, 2) and int(bins.abs().sum()) == 0
+
+
+def _emission(tmin, tmax, Tx, Ty):
+    """Keys and Gaussian ids in emission order: Gaussian-major, each box's tiles
+    z -> y -> x (bin_and_sort_gaussians.cu:11-35)."""
+    keys, vals = [], []
+    for g in range(tmin.shape[0]):
+        (x0, y0, z0), (x1, y1, z1) = tmin[g], tmax[g]
+        if x1 <= x0 or y1 <= y0 or z1 <= z0:
+            continue
+        z, y, x = np.meshgrid(np.arange(z0, z1), np.arange(y0, y1), np.arange(x0, x1),
+                              indexing="ij")
+        keys.append(((z * Ty + y) * Tx + x).ravel())
+        vals.append(np.full(keys[-1].size, g))
+    if not keys:
+        return np.zeros(0, np.int64), np.zeros(0, np.int64)
+    return np.concatenate(keys), np.concatenate(vals)
+
+
+def _device_count_bin(device, n, tmin, tmax, nt, vol, capacity):
+    import gs_voxelizer.cuda as _C
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    cum, total = _C.cumsum_tiles_hit(t(nt))
+    ids, bins = _C.bin_and_sort_gaussians_device_count(n, capacity, total, t(tmin), t(tmax), cum,
+                                                       vol)
+    torch.cuda.synchronize()
+    return int(total.item()), np32(ids), np32(bins)
+
+
+@pytest.mark.parametrize("name,work", [c for c in _bin_cases() if c[0] in
+                                       ("cfg1", "few_tiles", "three_passes", "clustered_heavy")],
+                         ids=lambda v: v if isinstance(v, str) else "")
+def test_device_count_binning_matches_host_count(device, name, work):
+    """The count read on the device, capacity above it: same bits as the oracle."""
+    cfg = work.cfg
+    n = work.pos3d.shape[0]
+    _, _, rtmin, rtmax, rnt = oracle_project(work)
+    rcum = O.cumsum(rnt)
+    rI = int(rcum[-1])
+    rids, rbins = O.bin_and_sort(n, rI, rtmin, rtmax, rcum, cfg.vol)
+    I, ids, bins = _device_count_bin(device, n, rtmin, rtmax, rnt, cfg.vol, rI + 5000)
+    assert I == rI
+    np.testing.assert_array_equal(bins, rbins)
+    np.testing.assert_array_equal(ids[:rI], rids)
+
+
+def test_device_count_binning_over_capacity_sorts_the_prefix(device):
+    """Capacity below the count: exactly the first `capacity` emitted pairs are
+    sorted (stable by tile), and the call neither fails nor writes past it."""
+    work = S.make_gaussians(small_config(1, 3000, vol=(40, 48, 56)), seed=3)
+    cfg = work.cfg
+    n = work.pos3d.shape[0]
+    _, _, rtmin, rtmax, rnt = oracle_project(work)
+    Tx, Ty, Tz = O.tile_grid(cfg.vol)
+    keys, vals = _emission(rtmin, rtmax, Tx, Ty)
+    cap = keys.size // 2 + 17
+    order = np.argsort(keys[:cap], kind="stable")
+    I, ids, bins = _device_count_bin(device, n, rtmin, rtmax, rnt, cfg.vol, cap)
+    assert I == keys.size and ids.shape == (cap,)
+    np.testing.assert_array_equal(ids, vals[:cap][order])
+    counts = np.bincount(keys[:cap], minlength=Tx * Ty * Tz)
+    np.testing.assert_array_equal(bins[:, 1] - bins[:, 0], counts)
+
+
+def test_binning_long_runs_of_empty_gaussians(device):
+    """Runs of 5000 Gaussians without tiles between large boxes: chunks whose
+    Gaussians lie beyond the emission block's cached window of cum."""
+    import gs_voxelizer.cuda as _C
+    vol = (160, 160, 160)
+    Tx, Ty, Tz = O.tile_grid(vol)
+    n = 20000
+    rng = np.random.default_rng(11)
+    tmin = np.zeros((n, 3), np.int32)
+    tmax = np.zeros((n, 3), np.int32)
+    for g in range(0, n, 5000):
+        lo = rng.integers(0, 6, 3)
+        tmin[g] = lo
+        tmax[g] = lo + rng.integers(8, 14, 3)
+    nt = np.prod(np.maximum(tmax - tmin, 0), axis=1).astype(np.int32)
+    cum = O.cumsum(nt)
+    rI = int(cum[-1])
+    rids, rbins = O.bin_and_sort(n, rI, tmin, tmax, cum, vol)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    ids, bins = _C.bin_and_sort_gaussians(n, rI, t(tmin), t(tmax), t(cum), vol)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(np32(bins), rbins)
+    np.testing.assert_array_equal(np32(ids), rids)
+    I2, ids2, bins2 = _device_count_bin(device, n, tmin, tmax, nt, vol, rI)
+    np.testing.assert_array_equal(bins2, rbins)
+    np.testing.assert_array_equal(ids2, rids)
