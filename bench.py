@@ -139,20 +139,15 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    timer = KernelTimer(_C, ["optim_to_render_forward", "cumsum_tiles_hit", "bin_and_sort_gaussians",
-                             "voxelize_forward", "voxelize_backward_per_gaussian",
-                             "optim_to_render_backward"])
-    timer.install()
-    timer.active = True
-    _C._L.gsv_kernel_timing_enable(1)   # HIP events around the hot kernels, on their stream
+    # Timed region: the steps alone, plus the library's pooled HIP events around
+    # the hot kernels on their launch stream (no per-call Python instrumentation).
+    _C._L.gsv_kernel_timing_enable(1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    timer.active = False
-    timer.uninstall()
     ms = (t1 - t0) * 1e3 / args.steps
     kern = {}
     for slot, name in ((0, "k_vox_fwd"), (1, "k_vox_bwd"), (2, "k_pair_reduce")):
@@ -160,6 +155,20 @@ def main():
         _C._L.gsv_kernel_timing_collect(slot, ctypes.byref(tot), ctypes.byref(cnt))
         kern[name] = (tot.value / cnt.value) if cnt.value else None
     _C._L.gsv_kernel_timing_enable(0)
+
+    # Per-stage times from a separate, untimed pass: torch events around each
+    # native call of the drop-in API (host gaps included in neither figure).
+    timer = KernelTimer(_C, ["optim_to_render_forward", "cumsum_tiles_hit",
+                             "bin_and_sort_gaussians", "bin_and_sort_gaussians_device_count",
+                             "voxelize_forward", "voxelize_backward_per_gaussian",
+                             "optim_to_render_backward"])
+    timer.install()
+    timer.active = True
+    for _ in range(min(args.steps, 5)):
+        step()
+    torch.cuda.synchronize()
+    timer.active = False
+    timer.uninstall()
 
     C = cfg.channels
     fwd_ms = kern["k_vox_fwd"]          # kernel alone

@@ -50,7 +50,8 @@ def build(verbose=False):
     log = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
                     if not any(k in l for k in noise))
     if res.returncode != 0:
-        os.unlink(tmp)
+        if os.path.exists(tmp):  # hipcc may already have removed it
+            os.unlink(tmp)
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{log}")
     if verbose and log.strip():
         print(log, flush=True)

@@ -33,7 +33,7 @@ namespace {
 constexpr int kChunk = 4096;  // keys per emission chunk and per scatter block
 constexpr int kEmitThreads = 512;
 constexpr int kEmitItems = kChunk / kEmitThreads;  // 8 consecutive slots per thread
-constexpr int kWindow = 4096;                       // Gaussians cached by an emission block
+constexpr int kWindow = 1024;                       // Gaussians cached by an emission block
 constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / kWave;
 constexpr int kWaveKeys = kChunk / kSortWaves;  // 1024 contiguous keys per wave
@@ -55,16 +55,19 @@ __device__ __forceinline__ int64_t live_count(int64_t cap, const int64_t *d_n) {
 // Gaussian-major, and for each Gaussian its box tiles z -> y -> x with x
 // fastest (bin_and_sort_gaussians.cu:11-35).  Slot p belongs to the Gaussian g
 // with cum[g-1] <= p < cum[g].  The block finds the first such Gaussian with a
-// 512-way cooperative search of cum, caches the next kWindow entries of cum in
-// LDS, and gives each thread 8 consecutive slots: one search and one division
-// per thread, then stepping through the box.  The chunk's digit histogram for
-// the first radix pass is written digit-major: hist[d * nblocks + b].
+// 512-way cooperative search of cum, caches cum and the tile boxes of the
+// Gaussians that follow in LDS (in rounds of 512 until they cover the chunk,
+// at most kWindow; beyond that it reads global memory), and gives each thread
+// 8 consecutive slots: one search and one division per thread, then stepping
+// through the box.  The chunk's digit histogram for the first radix pass is
+// written digit-major: hist[d * nblocks + b].
 __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
     int n, int64_t cap, const int64_t *__restrict__ d_n, const int *__restrict__ tile_min,
     const int *__restrict__ tile_max, const int *__restrict__ cum, int Tx, int Ty, int64_t T,
     int *__restrict__ keys, int *__restrict__ vals, int *__restrict__ hist, int nblocks,
     int2 *__restrict__ tile_bins) {
     __shared__ int s_cum[kWindow];
+    __shared__ int s_box[kWindow][6];  // min x, y, z; extent x, y, z
     __shared__ int s_hist[kRadixBins];
     const int t = threadIdx.x;
     for (int64_t i = (int64_t)blockIdx.x * kEmitThreads + t; i < T;
@@ -91,15 +94,50 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
         }
     }
     const int g_lo = lo;
-    const int wlen = base < total ? min(kWindow, n - g_lo) : 0;
-    for (int i = t; i < wlen; i += kEmitThreads) s_cum[i] = cum[g_lo + i];
+    const int avail = base < total ? min(kWindow, n - g_lo) : 0;
+    const int64_t chunk_last = min<int64_t>(base + kChunk, total) - 1;
+    int wlen = 0;
+    for (int r = 0; r * kEmitThreads < avail; ++r) {  // uniform: avail and LDS reads agree
+        const int i = r * kEmitThreads + t;
+        if (i < avail) {
+            const int g = g_lo + i;
+            s_cum[i] = cum[g];
+            const int mnx = tile_min[3 * g], mny = tile_min[3 * g + 1], mnz = tile_min[3 * g + 2];
+            s_box[i][0] = mnx; s_box[i][1] = mny; s_box[i][2] = mnz;
+            s_box[i][3] = tile_max[3 * g] - mnx;
+            s_box[i][4] = tile_max[3 * g + 1] - mny;
+            s_box[i][5] = tile_max[3 * g + 2] - mnz;
+        }
+        wlen = min((r + 1) * kEmitThreads, avail);
+        __syncthreads();
+        if ((int64_t)s_cum[wlen - 1] > chunk_last) break;
+    }
     const int prev = g_lo > 0 ? cum[g_lo - 1] : 0;
     __syncthreads();
 
     const int64_t p0 = base + (int64_t)t * kEmitItems;
     if (p0 < total) {
-        // cum at window index i (global beyond the window)
+        // cum and box at window index i (global memory beyond the window)
         auto cum_at = [&](int i) -> int { return i < wlen ? s_cum[i] : cum[g_lo + i]; };
+        int mnx = 0, mny = 0, mnz = 0, ex = 0, ey = 0, ez = 0, dx = 0, dy = 0, dz = 0;
+        auto load_box = [&](int i, int j) {
+            if (i < wlen) {
+                mnx = s_box[i][0]; mny = s_box[i][1]; mnz = s_box[i][2];
+                ex = s_box[i][3]; ey = s_box[i][4]; ez = s_box[i][5];
+            } else {
+                const int g = g_lo + i;
+                mnx = tile_min[3 * g]; mny = tile_min[3 * g + 1]; mnz = tile_min[3 * g + 2];
+                ex = tile_max[3 * g] - mnx; ey = tile_max[3 * g + 1] - mny;
+                ez = tile_max[3 * g + 2] - mnz;
+            }
+            dx = dy = dz = 0;
+            if (ex > 0 && ey > 0 && ez > 0) {
+                const unsigned r = (unsigned)j / (unsigned)ex;
+                dx = j - (int)r * ex;
+                dy = (int)(r % (unsigned)ey);
+                dz = (int)(r / (unsigned)ey);
+            }
+        };
         // l = min{i : cum_at(i) > p0}, searched in the window, then beyond it
         int l;
         if (wlen > 0 && (int64_t)s_cum[wlen - 1] > p0) {
@@ -121,18 +159,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
         int g = g_lo + l;
         int start = l == 0 ? prev : cum_at(l - 1);
         int end = g < n ? cum_at(l) : start;
-        int mnx = 0, mny = 0, mnz = 0, ex = 0, ey = 0, ez = 0, dx = 0, dy = 0, dz = 0;
-        auto load_box = [&](int j) {
-            mnx = tile_min[3 * g]; mny = tile_min[3 * g + 1]; mnz = tile_min[3 * g + 2];
-            ex = tile_max[3 * g] - mnx; ey = tile_max[3 * g + 1] - mny; ez = tile_max[3 * g + 2] - mnz;
-            if (ex > 0 && ey > 0 && ez > 0) {
-                const unsigned r = (unsigned)j / (unsigned)ex;
-                dx = j - (int)r * ex;
-                dy = (int)(r % (unsigned)ey);
-                dz = (int)(r / (unsigned)ey);
-            }
-        };
-        if (g < n) load_box((int)(p0 - start));
+        if (g < n) load_box(l, (int)(p0 - start));
 #pragma unroll
         for (int k = 0; k < kEmitItems; ++k) {
             const int64_t p = p0 + k;
@@ -149,8 +176,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
                     end = g < n ? cum_at(l) : start;
                 } while (g < n && p >= end);
                 if (g >= n) { key[k] = kInvalidKey; val[k] = 0; continue; }
-                dx = dy = dz = 0;
-                load_box((int)(p - start));
+                load_box(l, (int)(p - start));
             }
             val[k] = g;
             // a slot past the box (cum inconsistent with the box) gets no tile
@@ -159,7 +185,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
                          : kInvalidKey;
             if (++dx == ex) { dx = 0; if (++dy == ey) { dy = 0; ++dz; } }
         }
-        // slots [p0, p0 + 8): two 16-byte stores when whole and aligned
+        // slots [p0, p0 + 8): two 16-byte stores when whole
         if (p0 + kEmitItems <= total) {
             int4 *k4 = reinterpret_cast<int4 *>(keys + p0);
             int4 *v4 = reinterpret_cast<int4 *>(vals + p0);

@@ -1,0 +1,175 @@
+// gsv_scan.h — int32 exclusive/inclusive prefix sums for gfx950 whose element
+// loads and result stores are functors, so a producer's arithmetic (e.g.
+// buckets per tile) and a consumer's scatter (e.g. bucket -> tile) ride along
+// with the scan instead of needing launches of their own.
+//
+// Blocks of 256 threads x 8 items (2048 elements).  Two launches when there
+// are at most 1024 blocks: block sums, then an apply pass in which every block
+// adds up its predecessors' sums itself (<= 4 loads per thread).  Above that a
+// third launch scans the block sums in one workgroup first.  Every pass is
+// HBM-bound: 4 B read per element twice, plus the stores.
+#pragma once
+
+#include "gsv_device.h"
+
+namespace gsv {
+// unnamed: each translation unit that scans gets its own copies of the kernels
+namespace {
+namespace scan_detail {
+
+constexpr int kThreads = 256;
+constexpr int kItems = 8;
+constexpr int kTile = kThreads * kItems;
+constexpr int64_t kDirectBlocks = 1024;
+
+// Inclusive scan of one int per lane across a 64-wide wave.
+__device__ __forceinline__ int wave_inclusive(int v) {
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int o = __shfl_up(v, d, kWave);
+        if (lane >= d) v += o;
+    }
+    return v;
+}
+
+// Exclusive scan of one int per thread over the block; *total gets the sum.
+__device__ __forceinline__ int block_exclusive(int v, int *lds_waves, int *total) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int inc = wave_inclusive(v);
+    if (lane == kWave - 1) lds_waves[wave] = inc;
+    __syncthreads();
+    int off = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) {
+        const int t = lds_waves[w];
+        off += (w < wave) ? t : 0;
+        sum += t;
+    }
+    *total = sum;
+    return off + inc - v;
+}
+
+template <class Load>
+__global__ __launch_bounds__(kThreads) void k_block_sums(Load ld, int64_t n, int32_t *part) {
+    __shared__ int lds_waves[kThreads / kWave];
+    const int64_t base = (int64_t)blockIdx.x * kTile + (int64_t)threadIdx.x * kItems;
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < kItems; ++k)
+        if (base + k < n) s += ld(base + k);
+    int total;
+    (void)block_exclusive(s, lds_waves, &total);
+    if (threadIdx.x == 0) part[blockIdx.x] = total;
+}
+
+// Exclusive scan of part[0..nb) in place by one workgroup; writes the total.
+__global__ __launch_bounds__(kThreads) void k_scan_block_sums(int32_t *part, int64_t nb,
+                                                              int64_t *total_out) {
+    __shared__ int lds_waves[kThreads / kWave];
+    int64_t carry = 0;
+    for (int64_t start = 0; start < nb; start += kThreads) {
+        const int64_t i = start + threadIdx.x;
+        const int v = i < nb ? part[i] : 0;
+        int total;
+        const int ex = block_exclusive(v, lds_waves, &total);
+        if (i < nb) part[i] = (int32_t)(carry + ex);
+        carry += total;
+        __syncthreads();  // lds_waves reused by the next chunk
+    }
+    if (total_out && threadIdx.x == 0) *total_out = carry;
+}
+
+// st(i, exclusive prefix of element i, element i) for every i < n.  direct:
+// part holds raw block sums and each block adds its predecessors' (the last
+// block then writes the total); otherwise part is already scanned.
+template <class Load, class Store>
+__global__ __launch_bounds__(kThreads) void k_apply(Load ld, Store st, int64_t n,
+                                                    const int32_t *part, int direct,
+                                                    int64_t *total_out) {
+    __shared__ int lds_waves[kThreads / kWave];
+    __shared__ long long lds_pre[kThreads / kWave];
+    const int b = blockIdx.x;
+    long long prefix;
+    if (direct) {
+        long long s = 0;
+        for (int j = threadIdx.x; j < b; j += kThreads) s += part[j];
+#pragma unroll
+        for (int o = kWave / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+        if ((threadIdx.x & (kWave - 1)) == 0) lds_pre[threadIdx.x / kWave] = s;
+        __syncthreads();
+        prefix = 0;
+#pragma unroll
+        for (int w = 0; w < kThreads / kWave; ++w) prefix += lds_pre[w];
+    } else {
+        prefix = part[b];
+    }
+    const int64_t base = (int64_t)b * kTile + (int64_t)threadIdx.x * kItems;
+    int v[kItems];
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+        v[k] = (base + k < n) ? ld(base + k) : 0;
+        s += v[k];
+    }
+    int total;
+    int run = (int)(block_exclusive(s, lds_waves, &total) + prefix);
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+        if (base + k < n) st(base + k, run, v[k]);
+        run += v[k];
+    }
+    if (direct && total_out && b == (int)gridDim.x - 1 && threadIdx.x == 0)
+        *total_out = prefix + total;
+}
+
+}  // namespace scan_detail
+}  // namespace
+
+// Workspace of scan_run for n elements (the block sums).
+inline size_t scan_workspace_bytes(int64_t n) {
+    const int64_t nb = (n + scan_detail::kTile - 1) / scan_detail::kTile;
+    return (size_t)((nb + 64) * sizeof(int32_t) + 255) / 256 * 256;
+}
+
+// Prefix sum of ld(0..n) handed to st; *total_out (optional, device int64)
+// receives the sum.  Launches on `stream`; no host synchronisation.
+template <class Load, class Store>
+int scan_run(Load ld, Store st, int64_t n, int64_t *total_out, void *ws, size_t ws_bytes,
+             hipStream_t stream) {
+    using namespace scan_detail;
+    if (n < 0) return GSV_ERR_INVALID_ARGUMENT;
+    if (ws_bytes < scan_workspace_bytes(n) || !ws) return GSV_ERR_WORKSPACE_TOO_SMALL;
+    const int64_t nb = (n + kTile - 1) / kTile;
+    int32_t *part = static_cast<int32_t *>(ws);
+    if (nb == 0) {
+        hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(kThreads), 0, stream, part, nb,
+                           total_out);
+        return check_launch();
+    }
+    hipLaunchKernelGGL(k_block_sums<Load>, dim3((unsigned)nb), dim3(kThreads), 0, stream, ld, n,
+                       part);
+    if (int st_ = check_launch()) return st_;
+    const int direct = nb <= kDirectBlocks ? 1 : 0;
+    if (!direct) {
+        hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(kThreads), 0, stream, part, nb,
+                           total_out);
+        if (int st_ = check_launch()) return st_;
+    }
+    hipLaunchKernelGGL((k_apply<Load, Store>), dim3((unsigned)nb), dim3(kThreads), 0, stream, ld,
+                       st, n, part, direct, total_out);
+    return check_launch();
+}
+
+struct LoadI32 {
+    const int32_t *p;
+    __device__ int operator()(int64_t i) const { return p[i]; }
+};
+
+struct StoreI32 {
+    int32_t *out;
+    int inclusive;
+    __device__ void operator()(int64_t i, int excl, int v) const { out[i] = inclusive ? excl + v : excl; }
+};
+
+}  // namespace gsv

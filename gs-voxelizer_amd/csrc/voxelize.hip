@@ -41,6 +41,7 @@
 #include <float.h>
 
 #include "gsv_device.h"
+#include "gsv_scan.h"
 
 namespace gsv {
 namespace {
@@ -305,25 +306,28 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
 
 constexpr int kBucket = kWave;  // (tile, Gaussian) pairs per wave
 
-__global__ __launch_bounds__(256) void k_bucket_counts(const int2 *__restrict__ bins, int64_t T,
-                                                       int *__restrict__ counts) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= T) return;
-    const int2 r = bins[t];
-    const int m = max(0, r.y - r.x);
-    counts[t] = (m + kBucket - 1) / kBucket;
-}
+// Buckets per tile, read by the bucket scan: ceil(pairs / 64).
+struct BucketCountLoad {
+    const int2 *bins;
+    __device__ int operator()(int64_t t) const {
+        const int2 r = bins[t];
+        const int m = max(0, r.y - r.x);
+        return (m + kBucket - 1) / kBucket;
+    }
+};
 
-__global__ __launch_bounds__(256) void k_bucket_fill(const int *__restrict__ counts,
-                                                     const int *__restrict__ offs, int64_t T,
-                                                     int64_t cap, int *__restrict__ bucket_tile) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= T) return;
-    const int c = counts[t];
-    const int64_t o = offs[t];
-    for (int k = 0; k < c; ++k)
-        if (o + k < cap) bucket_tile[o + k] = (int)t;
-}
+// Written by the bucket scan: the tile's first bucket, and bucket -> tile for
+// each of its buckets (capped at the launch's bucket capacity).
+struct BucketFillStore {
+    int *offs;
+    int *bucket_tile;
+    int64_t cap;
+    __device__ void operator()(int64_t t, int first, int count) const {
+        offs[t] = first;
+        for (int k = 0; k < count; ++k)
+            if ((int64_t)first + k < cap) bucket_tile[first + k] = (int)t;
+    }
+};
 
 template <int C>
 struct Moments {
@@ -590,26 +594,54 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
     }
 }
 
-// Deterministic reduction of the per-pair partials: Gaussian g sums its slots
-// [cum[g-1], cum[g]) in emission order and writes every output element.
+// Deterministic reduction of the per-pair partials: one 16-lane DPP row per
+// Gaussian g.  Lane r of the row sums slots cum[g-1] + r, + r + 16, ... of
+// [cum[g-1], cum[g]) (a row's loads cover 16 consecutive slots), then a fixed
+// row_shr 1, 2, 4, 8 scan adds the 16 lane sums; all in binary64, lane 15
+// writes every output element.  DPP keeps the cross-lane sums on the VALU (an
+// xor-shuffle butterfly goes through the LDS crossbar, 2 ops per double).
+constexpr int kRowLanes = 16;
+constexpr int kReduceThreads = 256;
+
+template <int kCtrl>
+__device__ __forceinline__ double row_shr(double x) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(x), kCtrl, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(x), kCtrl, 0xf, 0xf, true);
+    return __hiloint2double(hi, lo);
+}
+
+// Inclusive scan within each 16-lane row; lane 15 ends with the row total.
+__device__ __forceinline__ double row_total(double x) {
+    x += row_shr<0x111>(x);
+    x += row_shr<0x112>(x);
+    x += row_shr<0x114>(x);
+    x += row_shr<0x118>(x);
+    return x;
+}
+
 template <int C>
-__global__ __launch_bounds__(256) void k_pair_reduce(int n, int n_isect, const int *__restrict__ cum,
-                                                     const float *__restrict__ partial,
-                                                     float *__restrict__ dpos,
-                                                     float *__restrict__ dconic,
-                                                     float *__restrict__ dint) {
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= n) return;
-    const int64_t b = g == 0 ? 0 : max(0, cum[g - 1]);
-    const int64_t e = min<int64_t>(cum[g], n_isect);
-    double acc[9 + C];  // this pass is memory-bound; binary64 costs nothing here
-#pragma unroll
-    for (int q = 0; q < 9 + C; ++q) acc[q] = 0.0;
-    for (int64_t k = b; k < e; ++k) {
-        const float *src = partial + k * (9 + C);
-#pragma unroll
-        for (int q = 0; q < 9 + C; ++q) acc[q] += (double)src[q];
+__global__ __launch_bounds__(kReduceThreads) void k_pair_reduce(
+    int n, int n_isect, const int *__restrict__ cum, const float *__restrict__ partial,
+    float *__restrict__ dpos, float *__restrict__ dconic, float *__restrict__ dint) {
+    constexpr int F = 9 + C;
+    const int r = threadIdx.x & (kRowLanes - 1);
+    const int g = (int)(((int64_t)blockIdx.x * kReduceThreads + threadIdx.x) / kRowLanes);
+    int64_t b = 0, e = 0;
+    if (g < n) {  // rows past n reduce zeros; every lane stays for the DPP steps
+        b = g == 0 ? 0 : max(0, cum[g - 1]);
+        e = min<int64_t>(cum[g], n_isect);
     }
+    double acc[F];
+#pragma unroll
+    for (int q = 0; q < F; ++q) acc[q] = 0.0;
+    for (int64_t k = b + r; k < e; k += kRowLanes) {
+        const float *src = partial + k * F;
+#pragma unroll
+        for (int q = 0; q < F; ++q) acc[q] += (double)src[q];
+    }
+#pragma unroll
+    for (int q = 0; q < F; ++q) acc[q] = row_total(acc[q]);
+    if (r != kRowLanes - 1 || g >= n) return;
     float2 *dc = reinterpret_cast<float2 *>(dconic + 6 * (size_t)g);
     dc[0] = make_float2((float)acc[0], (float)acc[1]);
     dc[1] = make_float2((float)acc[2], (float)acc[3]);
@@ -620,7 +652,7 @@ __global__ __launch_bounds__(256) void k_pair_reduce(int n, int n_isect, const i
 }
 
 struct BwdLayout {
-    size_t counts, offs, scan, total, btile, partial, end;
+    size_t offs, scan, total, btile, partial, end;
     int64_t cap;
 };
 
@@ -630,7 +662,6 @@ BwdLayout bwd_layout(int64_t T, int64_t n_isect, int channels, bool pairs) {
     BwdLayout L{};
     L.cap = imin64(T, n_isect) + (n_isect + kBucket - 1) / kBucket;
     size_t off = 0;
-    L.counts = off; off += align256((size_t)T * 4);
     L.offs = off; off += align256((size_t)T * 4);
     L.scan = off; off += scan_workspace_bytes(T);
     L.total = off; off += 256;
@@ -727,19 +758,16 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
     const BwdLayout L = bwd_layout(T, num_intersects, channels, pairs);
     if (!workspace || workspace_bytes < L.end) return GSV_ERR_WORKSPACE_TOO_SMALL;
     char *ws = static_cast<char *>(workspace);
-    int *counts = reinterpret_cast<int *>(ws + L.counts);
     int *offs = reinterpret_cast<int *>(ws + L.offs);
     int64_t *total = reinterpret_cast<int64_t *>(ws + L.total);
     int *btile = reinterpret_cast<int *>(ws + L.btile);
     float *partial = pairs ? reinterpret_cast<float *>(ws + L.partial) : nullptr;
-    const unsigned tb = (unsigned)((T + 255) / 256);
-    hipLaunchKernelGGL(k_bucket_counts, dim3(tb), dim3(256), 0, s,
-                       reinterpret_cast<const int2 *>(tile_bins), T, counts);
-    if (int st = check_launch()) return st;
-    if (int st = scan_i32(counts, offs, T, false, total, ws + L.scan, scan_workspace_bytes(T), s))
+    // buckets per tile -> offsets, bucket -> tile map and the bucket total, in
+    // the scan's two launches
+    if (int st = scan_run(BucketCountLoad{reinterpret_cast<const int2 *>(tile_bins)},
+                          BucketFillStore{offs, btile, L.cap}, T, total, ws + L.scan,
+                          scan_workspace_bytes(T), s))
         return st;
-    hipLaunchKernelGGL(k_bucket_fill, dim3(tb), dim3(256), 0, s, counts, offs, T, L.cap, btile);
-    if (int st = check_launch()) return st;
     const dim3 grid((unsigned)(L.cap + kXcds)), block(kWave);
     const int ni = (int)num_intersects;
 #define GSV_VB(CH)                                                                                  \
@@ -755,7 +783,10 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
     if (int st = check_launch()) return st;                                                         \
     if (pairs) {                                                                                    \
         KernelTimer timer(kTimedPairReduce, s);                                                     \
-        hipLaunchKernelGGL(k_pair_reduce<CH>, dim3((n + 255) / 256), dim3(256), 0, s, n, ni,        \
+        hipLaunchKernelGGL(k_pair_reduce<CH>,                                                      \
+                           dim3((unsigned)(((int64_t)n * kRowLanes + kReduceThreads - 1) /          \
+                                           kReduceThreads)),                                        \
+                           dim3(kReduceThreads), 0, s, n, ni,        \
                            cum_tiles_hit, partial, dpos3d_radii, dconics, dintensities);            \
     }
     switch (channels) {

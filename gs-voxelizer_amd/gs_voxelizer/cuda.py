@@ -131,7 +131,7 @@ def cumsum_tiles_hit(num_tiles_hit):
     n = num_tiles_hit.numel()
     dev = num_tiles_hit.device
     cum = torch.empty((n,), device=dev, dtype=torch.int32)
-    total = torch.zeros((1,), device=dev, dtype=torch.int64)
+    total = torch.empty((1,), device=dev, dtype=torch.int64)  # written by the scan
     nbytes = ctypes.c_size_t(0)
     _call("scan_workspace_bytes", n, ctypes.byref(nbytes))
     ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)

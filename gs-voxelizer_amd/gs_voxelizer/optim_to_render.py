@@ -70,6 +70,9 @@ class _OptimToRender(Function):
         ctx.vol_center_pos = vol_center_pos
         ctx.save_for_backward(pos3d, scale3d, quat, pos3d_radii)
         ctx.mark_non_differentiable(tile_min, tile_max, num_tiles_hit)
+        # gradients of unused outputs arrive as None (handled in backward) rather
+        # than as zero tensors the engine would fill, one launch each
+        ctx.set_materialize_grads(False)
         if pos3d_radii_buffer is not None:
             buf = pos3d_radii_buffer
             if not buf.is_contiguous():

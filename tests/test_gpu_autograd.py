@@ -107,3 +107,26 @@ def test_api_channel_limit_and_device_checks(device):
     with pytest.raises(RuntimeError, match="CUDA tensor"):
         _C.optim_to_render_forward(10, w.pos3d.cpu(), w.scale3d, w.quat, w.intensities,
                                    (8, 8, 8), (1.0, 1.0, 1.0), (0.5, 0.5, 0.5))
+
+
+def test_speculative_capacity_matches_host_count(device, monkeypatch):
+    """Forwards after the first launch binning at a recorded capacity without
+    reading the count on the host.  Through a capacity overflow (a larger scene),
+    a speculative hit and a shrink (a much smaller scene), volumes and gradients
+    equal those of the reference's host-read path bit for bit."""
+    scenes = [S.make_gaussians(small_config(1, 800), seed=21),
+              S.make_gaussians(small_config(1, 6000), seed=22),   # more pairs: overflow
+              S.make_gaussians(small_config(1, 6000), seed=22),   # same again: speculative hit
+              S.make_gaussians(small_config(1, 40), seed=23)]     # far fewer: shrink
+    voxelize._capacity.clear()
+    spec = []
+    for work in scenes:
+        spec.append(_run_api(work, device, target=torch.zeros(work.cfg.vol, device=device)))
+    caps = dict(voxelize._capacity)
+    monkeypatch.setenv("GSV_SYNC_COUNT", "1")
+    for work, (vol_s, grads_s, _) in zip(scenes, spec):
+        vol, grads, _ = _run_api(work, device, target=torch.zeros(work.cfg.vol, device=device))
+        assert torch.equal(vol, vol_s)
+        for a, b in zip(grads, grads_s):
+            assert torch.equal(a, b)
+    assert len(caps) == 1 and 0 < next(iter(caps.values())) < 40 * 400
