@@ -1,13 +1,17 @@
 #!/usr/bin/env python3
 """Benchmark: one full differentiable voxelization iteration on one MI355X.
 
-A step is the reference's training iteration through the drop-in API
-(README.md:28-83 of PaPieta/gs-voxelizer): optim_to_render -> voxelize_gaussians
--> L1 loss against the phantom -> loss.backward() (voxelize backward +
-projection backward), on the headline workload of BASELINE.json: 256^3 volume,
-200,000 Gaussians, 1 channel, synthetic seeded inputs already resident in HBM.
+A step is the reference's training iteration (README.md:28-83 of
+PaPieta/gs-voxelizer): optim_to_render -> voxelization -> L1 loss against the
+phantom -> loss.backward() (voxelize backward + projection backward), on the
+headline workload of BASELINE.json: 256^3 volume, 200,000 Gaussians, 1 channel,
+synthetic seeded inputs already resident in HBM.
 
-Prints one JSON line.  `value` is ms per iteration (lower is better).  The
+Prints one JSON line.  `value` is ms per iteration (lower is better) of the
+step with the voxelization fused with the L1 loss (voxelize_gaussians_l1_loss:
+the same loss, gradients identical bit for bit); `dropin_ms_per_step` is the
+same step through the unchanged drop-in API (voxelize_gaussians, then torch's
+l1_loss).  The
 `roofline` object reports the dominant kernel (voxelize backward), timed with
 HIP events recorded on the stream it is launched on, against the FP32 vector
 peak; `cpu_baseline` times the CPU oracle (a binary32 C restatement of the
@@ -107,17 +111,37 @@ def main():
     leaves = [t.clone().requires_grad_() for t in (w.pos3d, w.scale3d, w.quat, w.intensities)]
     tgt = target[..., None].expand(cfg.vol + (cfg.channels,))
 
-    def step():
-        for t in leaves:
-            t.grad = None
-        pos3d, scale3d, quat, inten = leaves
-        pr, cn, tmin, tmax, nt = optim_to_render.optim_to_render(
-            pos3d, scale3d, quat, inten, cfg.vol, cfg.world, cfg.center)
-        vol = voxelize.voxelize_gaussians(pr, cn, inten, cfg.vol, tmin, tmax, nt,
-                                          use_per_gaussian_backward=True)
-        loss = F.l1_loss(vol, tgt)
-        loss.backward()
-        return vol
+    # the L1 target as the fused op takes it: (D, H, W) for one channel
+    tgt_fused = target if cfg.channels == 1 else tgt.contiguous()
+
+    def make_step(fused):
+        def step():
+            for t in leaves:
+                t.grad = None
+            pos3d, scale3d, quat, inten = leaves
+            pr, cn, tmin, tmax, nt = optim_to_render.optim_to_render(
+                pos3d, scale3d, quat, inten, cfg.vol, cfg.world, cfg.center)
+            if fused:
+                loss, vol = voxelize.voxelize_gaussians_l1_loss(
+                    pr, cn, inten, cfg.vol, tmin, tmax, nt, tgt_fused,
+                    use_per_gaussian_backward=True)
+            else:
+                vol = voxelize.voxelize_gaussians(pr, cn, inten, cfg.vol, tmin, tmax, nt,
+                                                  use_per_gaussian_backward=True)
+                loss = F.l1_loss(vol, tgt)
+            loss.backward()
+            return vol
+        return step
+
+    step_fused, step_dropin = make_step(True), make_step(False)
+
+    def timed(step, steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
 
     # workload statistics (intersections, evaluations) from one untimed pass
     with torch.no_grad():
@@ -136,25 +160,22 @@ def main():
         del pr, cn, tmin, tmax, nt, cum, ids, bins
 
     for _ in range(args.warmup):
-        step()
+        step_fused()
+        step_dropin()
     torch.cuda.synchronize()
 
     # Timed region: the steps alone, plus the library's pooled HIP events around
     # the hot kernels on their launch stream (no per-call Python instrumentation).
+    # `value` is the fused step; the unchanged drop-in step is timed after it.
     _C._L.gsv_kernel_timing_enable(1)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms = (t1 - t0) * 1e3 / args.steps
+    ms = timed(step_fused, args.steps)
     kern = {}
     for slot, name in ((0, "k_vox_fwd"), (1, "k_vox_bwd"), (2, "k_pair_reduce")):
         tot, cnt = ctypes.c_double(0), ctypes.c_int32(0)
         _C._L.gsv_kernel_timing_collect(slot, ctypes.byref(tot), ctypes.byref(cnt))
         kern[name] = (tot.value / cnt.value) if cnt.value else None
     _C._L.gsv_kernel_timing_enable(0)
+    ms_dropin = timed(step_dropin, args.steps)
 
     # Per-stage times from a separate, untimed pass: torch events around each
     # native call of the drop-in API (host gaps included in neither figure).
@@ -165,7 +186,7 @@ def main():
     timer.install()
     timer.active = True
     for _ in range(min(args.steps, 5)):
-        step()
+        step_dropin()
     torch.cuda.synchronize()
     timer.active = False
     timer.uninstall()
@@ -202,7 +223,10 @@ def main():
         "config": {"workload": cfg.name, "volume_zyx": list(cfg.vol), "gaussians": cfg.n,
                    "channels": C, "intersections": n_isect, "evals": evals,
                    "loss": f"l1 vs {cfg.phantom} phantom", "seed": args.seed,
-                   "step": "optim_to_render + voxelize_gaussians + l1 + backward"},
+                   "step": "optim_to_render + voxelize_gaussians_l1_loss (voxelization fused "
+                           "with torch's l1_loss; identical gradients) + backward",
+                   "dropin_step": "optim_to_render + voxelize_gaussians + torch l1_loss + backward"},
+        "dropin_ms_per_step": round(ms_dropin, 4),
         "evals_per_s": round(2 * evals / (ms * 1e-3), 1),
         "fwd_evals_per_s": round(evals / (fwd_ms * 1e-3), 1),
         "bwd_evals_per_s": round(evals / (bwd_ms * 1e-3), 1),

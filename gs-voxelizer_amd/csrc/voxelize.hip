@@ -149,6 +149,11 @@ __device__ __forceinline__ TileGeom tile_geom(int64_t tile, int Tx, int Ty, int 
 
 // ---------------------------------------------------------------- forward --
 
+// Fused L1: the forward stores sgn(volume - target) per element as one byte
+// (kSgnNaN for an unordered difference) for the backward, which then reads 1
+// byte per element instead of the volume and the target.
+constexpr int8_t kSgnNaN = 2;
+
 // float4 slots of one prepared Gaussian record: 13 + C floats (gate-free
 // layout) or 12 + C (exact layout).
 template <int C>
@@ -158,7 +163,8 @@ template <int C>
 __global__ __launch_bounds__(kWave) void k_vox_fwd(
     int D, int H, int W, int Tx, int Ty, int64_t T, int64_t per, int n, int n_isect,
     const int *__restrict__ ids, const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
-    const float2 *__restrict__ conics, const float *__restrict__ intens, float *__restrict__ vol) {
+    const float2 *__restrict__ conics, const float *__restrict__ intens, float *__restrict__ vol,
+    const float *__restrict__ target, float *__restrict__ tile_loss, int8_t *__restrict__ sgn) {
     __shared__ float4 s_rec[kWave][kRecF4<C>];
     const int64_t tile = xcd_remap(blockIdx.x, per);
     if (tile >= T) return;
@@ -245,7 +251,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
             const int j = __builtin_ctzll(fmask);
             fmask &= fmask - 1;
             const float4 r0 = s_rec[j][0], r1 = s_rec[j][1], r2 = s_rec[j][2], r3 = s_rec[j][3];
-            float iw[C];
+            float iw[4];  // entries >= C are unused
             iw[0] = r3.y;
             if (C > 1) iw[1] = r3.z;
             if (C > 2) iw[2] = r3.w;
@@ -291,14 +297,56 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
         __syncthreads();
     }
     const int y = tg.y0 + (lane & 7), z = tg.z0 + (lane >> 3);
+    float lsum = 0.f;  // fused L1: sum of |volume - target| over the lane's row
     if (y < H && z < D) {
-        float *o = vol + (((int64_t)z * H + y) * W + tg.x0) * C;
+        const int64_t off = (((int64_t)z * H + y) * W + tg.x0) * C;
+        float *o = vol + off;
         const int nx = min(GSV_TILE, W - tg.x0);
 #pragma unroll
         for (int u = 0; u < GSV_TILE; ++u)
             if (u < nx)
 #pragma unroll
                 for (int c = 0; c < C; ++c) o[u * C + c] = acc[u][c];
+        if (target != nullptr) {
+            const float *tt = target + off;
+            int8_t *sg = sgn + off;
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u)
+                if (u < nx)
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        const float d = acc[u][c] - tt[u * C + c];
+                        lsum += fabsf(d);
+                        sg[u * C + c] = d > 0.f ? 1 : (d < 0.f ? -1 : (d == 0.f ? 0 : kSgnNaN));
+                    }
+        }
+    }
+    if (target != nullptr) {  // fixed-order wave sum, one partial per tile
+#pragma unroll
+        for (int o = kWave / 2; o >= 1; o >>= 1) lsum += __shfl_xor(lsum, o, kWave);
+        if (lane == 0) tile_loss[tile] = lsum;
+    }
+}
+
+// loss = (sum over tiles of the partials) / numel, summed in a fixed order in
+// binary64 by one workgroup.
+constexpr int kFinishThreads = 1024;
+
+__global__ __launch_bounds__(kFinishThreads) void k_loss_finish(const float *__restrict__ tile_loss,
+                                                                int64_t T, double numel,
+                                                                float *__restrict__ loss) {
+    __shared__ double s_w[kFinishThreads / kWave];
+    double acc = 0.0;
+#pragma unroll 8
+    for (int64_t i = threadIdx.x; i < T; i += kFinishThreads) acc += (double)tile_loss[i];
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, kWave);
+    if ((threadIdx.x & (kWave - 1)) == 0) s_w[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < kFinishThreads / kWave; ++w) t += s_w[w];
+        *loss = (float)(t / numel);
     }
 }
 
@@ -433,7 +481,9 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
     int D, int H, int W, int Tx, int Ty, int n, int n_isect, const int *__restrict__ ids,
     const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
     const float2 *__restrict__ conics, const float *__restrict__ intens,
-    const float *__restrict__ vol_grad, const int *__restrict__ bucket_tile,
+    const float *__restrict__ vol_grad, const int8_t *__restrict__ l1_sgn,
+    const float *__restrict__ l1_grad, float l1_numel,
+    const int *__restrict__ bucket_tile,
     const int *__restrict__ bucket_off, const int64_t *__restrict__ total_buckets, int64_t cap,
     float *__restrict__ dpos, float *__restrict__ dconic, float *__restrict__ dint,
     const int *__restrict__ tile_min, const int *__restrict__ tile_max,
@@ -499,13 +549,33 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
 #pragma unroll
         for (int i = 0; i < GSV_TILE * C; ++i) v[i] = 0.f;
         if (y < H && z < D) {
-            const float *src = vol_grad + (((int64_t)z * H + y) * W + tg.x0) * C;
+            const int64_t off = (((int64_t)z * H + y) * W + tg.x0) * C;
             const int nx = min(GSV_TILE, W - tg.x0);
+            if (l1_sgn != nullptr) {
+                // fused L1 (torch's l1_loss, mean): dL/dv = sgn(v - t) * (dL / numel),
+                // plus the volume's own incoming gradient when it has one.  The
+                // division is a multiply by the binary32 reciprocal, as torch's
+                // division by a host scalar does, so the bits agree.
+                const float sc = *l1_grad * (1.0f / l1_numel);
+                const int8_t *sg = l1_sgn + off;
 #pragma unroll
-            for (int u = 0; u < GSV_TILE; ++u)
-                if (u < nx)
+                for (int u = 0; u < GSV_TILE; ++u)
+                    if (u < nx)
 #pragma unroll
-                    for (int c = 0; c < C; ++c) v[u * C + c] = src[u * C + c];
+                        for (int c = 0; c < C; ++c) {
+                            const int8_t q = sg[u * C + c];
+                            float gv = q == kSgnNaN ? __builtin_nanf("") : sc * (float)q;
+                            if (vol_grad != nullptr) gv += vol_grad[off + u * C + c];
+                            v[u * C + c] = gv;
+                        }
+            } else {
+                const float *src = vol_grad + off;
+#pragma unroll
+                for (int u = 0; u < GSV_TILE; ++u)
+                    if (u < nx)
+#pragma unroll
+                        for (int c = 0; c < C; ++c) v[u * C + c] = src[u * C + c];
+            }
         }
         if (wave_fast) {
             float mx = 0.f;
@@ -677,13 +747,16 @@ bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 }  // namespace
 }  // namespace gsv
 
-using namespace gsv;
+namespace gsv {
+namespace {
 
-extern "C" int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
-                                int64_t num_intersects, const int32_t *gaussian_ids_sorted,
-                                const int32_t *tile_bins, const float *pos3d_radii,
-                                const float *conics, const float *intensities, float *volume,
-                                void *stream) {
+// Forward; with `target`, also the L1 loss mean|volume - target| into *loss
+// (tile_loss: T floats of scratch) and sgn(volume - target) into sgn.
+int voxelize_fwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                      int64_t num_intersects, const int32_t *ids, const int32_t *tile_bins,
+                      const float *pos3d_radii, const float *conics, const float *intensities,
+                      float *volume, const float *target, float *tile_loss, int8_t *sgn,
+                      float *loss, hipStream_t s) {
     if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
     if (n < 0 || D <= 0 || H <= 0 || W <= 0 || !volume || !tile_bins) return GSV_ERR_INVALID_ARGUMENT;
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
@@ -691,48 +764,50 @@ extern "C" int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channel
     const int64_t vox = (int64_t)D * H * W;
     if (vox * channels > ((int64_t)1 << 40) || T > INT32_MAX || num_intersects > INT32_MAX)
         return GSV_ERR_SIZE_OVERFLOW;
-    hipStream_t s = as_stream(stream);
-    if (num_intersects <= 0 || n == 0) return fill_zero_u32(volume, vox * channels, s);
-    if (!gaussian_ids_sorted || !pos3d_radii || !conics || !intensities) return GSV_ERR_INVALID_ARGUMENT;
-    if (!aligned(pos3d_radii, 16) || !aligned(conics, 8)) return GSV_ERR_INVALID_ARGUMENT;
+    const bool empty = num_intersects <= 0 || n == 0;
+    if (empty && !target) return fill_zero_u32(volume, vox * channels, s);
+    if (!empty && (!ids || !pos3d_radii || !conics || !intensities)) return GSV_ERR_INVALID_ARGUMENT;
+    if (!empty && (!aligned(pos3d_radii, 16) || !aligned(conics, 8))) return GSV_ERR_INVALID_ARGUMENT;
+    // an empty list still runs the kernel for the loss: every tile range is empty
+    const int ni = empty ? 0 : (int)num_intersects;
     const int64_t per = xcd_per(T);
     const dim3 grid((unsigned)(kXcds * per)), block(kWave);
-    KernelTimer timer(kTimedVoxFwd, s);
+    {
+        KernelTimer timer(kTimedVoxFwd, s);
 #define GSV_VF(CH)                                                                                 \
-    hipLaunchKernelGGL(k_vox_fwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, T, per, n,               \
-                       (int)num_intersects,                                                         \
-                       gaussian_ids_sorted, reinterpret_cast<const int2 *>(tile_bins),             \
+    hipLaunchKernelGGL(k_vox_fwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, T, per, n, ni, ids,      \
+                       reinterpret_cast<const int2 *>(tile_bins),                                  \
                        reinterpret_cast<const float4 *>(pos3d_radii),                              \
-                       reinterpret_cast<const float2 *>(conics), intensities, volume)
-    switch (channels) {
-        case 1: GSV_VF(1); break;
-        case 2: GSV_VF(2); break;
-        case 3: GSV_VF(3); break;
-        default: GSV_VF(4); break;
-    }
+                       reinterpret_cast<const float2 *>(conics), intensities, volume, target,      \
+                       tile_loss, sgn)
+        switch (channels) {
+            case 1: GSV_VF(1); break;
+            case 2: GSV_VF(2); break;
+            case 3: GSV_VF(3); break;
+            default: GSV_VF(4); break;
+        }
 #undef GSV_VF
-    return check_launch();
-}
-
-extern "C" int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W,
-                                                int32_t channels, int64_t num_intersects,
-                                                int32_t deterministic, size_t *bytes) {
-    if (!bytes || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
-    if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
-    const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
-    *bytes = bwd_layout(T, num_intersects > 0 ? num_intersects : 0, channels, deterministic != 0).end;
+    }
+    if (int st = check_launch()) return st;
+    if (target) {
+        hipLaunchKernelGGL(k_loss_finish, dim3(1), dim3(kFinishThreads), 0, s, tile_loss, T,
+                           (double)vox * channels, loss);
+        return check_launch();
+    }
     return GSV_OK;
 }
 
-extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
-                                int64_t num_intersects, const int32_t *gaussian_ids_sorted,
-                                const int32_t *tile_bins, const float *pos3d_radii,
-                                const float *conics, const float *intensities,
-                                const float *vol_grad, const int32_t *tile_min,
-                                const int32_t *tile_max, const int32_t *cum_tiles_hit,
-                                float *dpos3d_radii, float *dconics, float *dintensities,
-                                int32_t variant, void *workspace, size_t workspace_bytes,
-                                void *stream) {
+// Backward from vol_grad, or (l1_sgn set) from the fused L1 loss: dL/dv =
+// sgn(volume - target) * (*l1_grad / numel) + vol_grad (vol_grad optional),
+// l1_sgn being the signs gsv_voxelize_fwd_l1 stored.
+int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                      int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                      const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
+                      const float *intensities, const float *vol_grad, const int8_t *l1_sgn,
+                      const float *l1_grad, const int32_t *tile_min,
+                      const int32_t *tile_max, const int32_t *cum_tiles_hit, float *dpos3d_radii,
+                      float *dconics, float *dintensities, int32_t variant, void *workspace,
+                      size_t workspace_bytes, hipStream_t s) {
     if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
     if (n < 0 || D <= 0 || H <= 0 || W <= 0 || (variant != 0 && variant != 1))
         return GSV_ERR_INVALID_ARGUMENT;
@@ -740,14 +815,15 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
     if (!dpos3d_radii || !dconics || !dintensities) return GSV_ERR_INVALID_ARGUMENT;
     const bool pairs = tile_min && tile_max && cum_tiles_hit;
     if (!pairs && (tile_min || tile_max || cum_tiles_hit)) return GSV_ERR_INVALID_ARGUMENT;
-    hipStream_t s = as_stream(stream);
     if (num_intersects <= 0 || !pairs) {
         if (int st = fill_zero_u32(dpos3d_radii, 4 * (int64_t)n, s)) return st;
         if (int st = fill_zero_u32(dconics, 6 * (int64_t)n, s)) return st;
         if (int st = fill_zero_u32(dintensities, (int64_t)channels * n, s)) return st;
     }
     if (num_intersects <= 0) return GSV_OK;
-    if (!gaussian_ids_sorted || !tile_bins || !pos3d_radii || !conics || !intensities || !vol_grad)
+    const bool l1 = l1_sgn != nullptr;
+    if (!gaussian_ids_sorted || !tile_bins || !pos3d_radii || !conics || !intensities ||
+        (!l1 && !vol_grad) || (l1 && !l1_grad))
         return GSV_ERR_INVALID_ARGUMENT;
     if (!aligned(pos3d_radii, 16) || !aligned(conics, 8) || !aligned(dpos3d_radii, 16) ||
         !aligned(dconics, 8))
@@ -770,15 +846,16 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
         return st;
     const dim3 grid((unsigned)(L.cap + kXcds)), block(kWave);
     const int ni = (int)num_intersects;
+    const float numel = (float)((int64_t)D * H * W * channels);
 #define GSV_VB(CH)                                                                                  \
     {                                                                                               \
         KernelTimer timer(kTimedVoxBwd, s);                                                         \
         hipLaunchKernelGGL(k_vox_bwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, n, ni,                \
                            gaussian_ids_sorted, reinterpret_cast<const int2 *>(tile_bins),          \
                            reinterpret_cast<const float4 *>(pos3d_radii),                           \
-                           reinterpret_cast<const float2 *>(conics), intensities, vol_grad, btile,  \
-                           offs, total, L.cap, dpos3d_radii, dconics, dintensities, tile_min,       \
-                           tile_max, cum_tiles_hit, partial);                                       \
+                           reinterpret_cast<const float2 *>(conics), intensities, vol_grad, l1_sgn, \
+                           l1_grad, numel, btile, offs, total, L.cap, dpos3d_radii,                \
+                           dconics, dintensities, tile_min, tile_max, cum_tiles_hit, partial);      \
     }                                                                                               \
     if (int st = check_launch()) return st;                                                         \
     if (pairs) {                                                                                    \
@@ -786,7 +863,7 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
         hipLaunchKernelGGL(k_pair_reduce<CH>,                                                      \
                            dim3((unsigned)(((int64_t)n * kRowLanes + kReduceThreads - 1) /          \
                                            kReduceThreads)),                                        \
-                           dim3(kReduceThreads), 0, s, n, ni,        \
+                           dim3(kReduceThreads), 0, s, n, ni,                                       \
                            cum_tiles_hit, partial, dpos3d_radii, dconics, dintensities);            \
     }
     switch (channels) {
@@ -797,4 +874,84 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
     }
 #undef GSV_VB
     return check_launch();
+}
+
+}  // namespace
+}  // namespace gsv
+
+using namespace gsv;
+
+extern "C" int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                                int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                                const int32_t *tile_bins, const float *pos3d_radii,
+                                const float *conics, const float *intensities, float *volume,
+                                void *stream) {
+    return voxelize_fwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
+                             pos3d_radii, conics, intensities, volume, nullptr, nullptr, nullptr,
+                             nullptr, as_stream(stream));
+}
+
+extern "C" int gsv_voxelize_fwd_l1_workspace_bytes(int32_t D, int32_t H, int32_t W,
+                                                   size_t *bytes) {
+    if (!bytes || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
+    const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
+    *bytes = align256((size_t)T * sizeof(float));
+    return GSV_OK;
+}
+
+extern "C" int gsv_voxelize_fwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                                   int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                                   const int32_t *tile_bins, const float *pos3d_radii,
+                                   const float *conics, const float *intensities,
+                                   const float *target, float *volume, int8_t *sign, float *loss,
+                                   void *workspace, size_t workspace_bytes, void *stream) {
+    if (!target || !loss || !sign) return GSV_ERR_INVALID_ARGUMENT;
+    size_t need = 0;
+    if (int st = gsv_voxelize_fwd_l1_workspace_bytes(D, H, W, &need)) return st;
+    if (!workspace || workspace_bytes < need) return GSV_ERR_WORKSPACE_TOO_SMALL;
+    return voxelize_fwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
+                             pos3d_radii, conics, intensities, volume, target,
+                             static_cast<float *>(workspace), sign, loss, as_stream(stream));
+}
+
+extern "C" int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W,
+                                                int32_t channels, int64_t num_intersects,
+                                                int32_t deterministic, size_t *bytes) {
+    if (!bytes || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
+    if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
+    const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
+    *bytes = bwd_layout(T, num_intersects > 0 ? num_intersects : 0, channels, deterministic != 0).end;
+    return GSV_OK;
+}
+
+extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                                int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                                const int32_t *tile_bins, const float *pos3d_radii,
+                                const float *conics, const float *intensities,
+                                const float *vol_grad, const int32_t *tile_min,
+                                const int32_t *tile_max, const int32_t *cum_tiles_hit,
+                                float *dpos3d_radii, float *dconics, float *dintensities,
+                                int32_t variant, void *workspace, size_t workspace_bytes,
+                                void *stream) {
+    return voxelize_bwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
+                             pos3d_radii, conics, intensities, vol_grad, nullptr, nullptr,
+                             tile_min, tile_max, cum_tiles_hit, dpos3d_radii, dconics,
+                             dintensities, variant, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                                   int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                                   const int32_t *tile_bins, const float *pos3d_radii,
+                                   const float *conics, const float *intensities,
+                                   const int8_t *sign, const float *grad_loss,
+                                   const float *vol_grad, const int32_t *tile_min,
+                                   const int32_t *tile_max, const int32_t *cum_tiles_hit,
+                                   float *dpos3d_radii, float *dconics, float *dintensities,
+                                   int32_t variant, void *workspace, size_t workspace_bytes,
+                                   void *stream) {
+    if (!sign || !grad_loss) return GSV_ERR_INVALID_ARGUMENT;
+    return voxelize_bwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
+                             pos3d_radii, conics, intensities, vol_grad, sign, grad_loss,
+                             tile_min, tile_max, cum_tiles_hit, dpos3d_radii, dconics,
+                             dintensities, variant, workspace, workspace_bytes, as_stream(stream));
 }

@@ -224,9 +224,53 @@ def voxelize_forward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, in
     return out
 
 
+def _l1_target(target, volume):
+    """The target laid out like the (D, H, W, C) volume (a (D, H, W) target serves C = 1)."""
+    _check_input(target, "target")
+    _check_dtype(target, "target", torch.float32)
+    if target.device != volume.device:
+        raise RuntimeError("target must be on the volume's device")
+    if target.shape == volume.shape:
+        return target
+    if target.dim() == 3 and volume.shape[-1] == 1 and tuple(target.shape) == tuple(volume.shape[:3]):
+        return target
+    raise RuntimeError(f"target shape {tuple(target.shape)} does not match the volume "
+                       f"{tuple(volume.shape)}")
+
+
+def voxelize_forward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
+                        target):
+    """voxelize_forward fused with torch.nn.functional.l1_loss(volume, target) (mean).
+    Returns (volume (D, H, W, C), loss (0-d device tensor), sign): sign is
+    sgn(volume - target) as int8 (2 where the difference is NaN), kept for
+    voxelize_backward_l1."""
+    _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
+    channels = _channels(intensities)
+    D, H, W = (int(v) for v in vol_size)
+    n = pos3d.size(0)
+    dev = pos3d.device
+    out = torch.empty((D, H, W, channels), device=dev, dtype=torch.float32)
+    target = _l1_target(target, out)
+    sign = torch.empty((D, H, W, channels), device=dev, dtype=torch.int8)
+    loss = torch.empty((), device=dev, dtype=torch.float32)
+    Tx, Ty, Tz = _tiles(vol_size)
+    if tile_bins.numel() < 2 * Tx * Ty * Tz:
+        raise RuntimeError("tile_bins does not cover the volume's tile grid")
+    nbytes = ctypes.c_size_t(0)
+    _call("voxelize_fwd_l1_workspace_bytes", D, H, W, ctypes.byref(nbytes))
+    ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        _call("voxelize_fwd_l1", D, H, W, channels, n, gaussian_ids_sorted.numel(),
+              _ptr(gaussian_ids_sorted), _ptr(tile_bins), _ptr(pos3d), _ptr(conics),
+              _ptr(intensities), _ptr(target), _ptr(out), _ptr(sign), _ptr(loss), _ptr(ws),
+              nbytes.value, _stream(dev))
+    return out, loss, sign
+
+
 def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                        intensities, vol_grad_in, tile_min=None, tile_max=None,
-                       cum_tiles_hit=None):
+                       cum_tiles_hit=None, l1=None):
+    """l1 = (sign, grad_loss): the fused L1 source, with vol_grad_in optional."""
     _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
     given = [t is not None for t in (tile_min, tile_max, cum_tiles_hit)]
     if any(given) and not all(given):
@@ -237,12 +281,21 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
                      (cum_tiles_hit, "cum_tiles_hit")):
             _check_input(t, w)
             _check_dtype(t, w, torch.int32)
-    _check_input(vol_grad_in, "vol_grad_in")
-    _check_dtype(vol_grad_in, "vol_grad_in", torch.float32)
     channels = _channels(intensities)
     D, H, W = (int(v) for v in vol_size)
-    if vol_grad_in.numel() != D * H * W * channels:
-        raise RuntimeError("vol_grad_in must have D*H*W*channels elements")
+    if vol_grad_in is not None or l1 is None:
+        _check_input(vol_grad_in, "vol_grad_in")
+        _check_dtype(vol_grad_in, "vol_grad_in", torch.float32)
+        if vol_grad_in.numel() != D * H * W * channels:
+            raise RuntimeError("vol_grad_in must have D*H*W*channels elements")
+    if l1 is not None:
+        sign, grad_loss = l1
+        _check_input(sign, "sign")
+        _check_dtype(sign, "sign", torch.int8)
+        _check_input(grad_loss, "grad_loss")
+        _check_dtype(grad_loss, "grad_loss", torch.float32)
+        if sign.numel() != D * H * W * channels or grad_loss.numel() != 1:
+            raise RuntimeError("sign must have D*H*W*channels elements and grad_loss one")
     n = pos3d.size(0)
     dev = pos3d.device
     I = gaussian_ids_sorted.numel()
@@ -260,12 +313,30 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
     null = ctypes.c_void_p(0)
     boxes = ((_ptr(tile_min), _ptr(tile_max), _ptr(cum_tiles_hit)) if deterministic
              else (null, null, null))
+    vg = _ptr(vol_grad_in) if vol_grad_in is not None else null
     with torch.cuda.device(dev):
-        _call("voxelize_bwd", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted), _ptr(tile_bins),
-              _ptr(pos3d), _ptr(conics), _ptr(intensities), _ptr(vol_grad_in), *boxes,
-              _ptr(dpos), _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value,
-              _stream(dev))
+        if l1 is None:
+            _call("voxelize_bwd", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted),
+                  _ptr(tile_bins), _ptr(pos3d), _ptr(conics), _ptr(intensities), vg, *boxes,
+                  _ptr(dpos), _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value,
+                  _stream(dev))
+        else:
+            _call("voxelize_bwd_l1", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted),
+                  _ptr(tile_bins), _ptr(pos3d), _ptr(conics), _ptr(intensities), _ptr(sign),
+                  _ptr(grad_loss), vg, *boxes, _ptr(dpos), _ptr(dconics), _ptr(dint), variant,
+                  _ptr(ws), nbytes.value, _stream(dev))
     return dpos, dconics, dint
+
+
+def voxelize_backward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
+                         sign, grad_loss, vol_grad_in=None, tile_min=None, tile_max=None,
+                         cum_tiles_hit=None, per_gaussian=True):
+    """Backward of voxelize_forward_l1: dL/dvolume = sign * grad_loss / numel (+
+    vol_grad_in, the volume's gradient from other uses, when given), never
+    materialised.  Returns (dpos3d_radii, dconics, dintensities)."""
+    return _voxelize_backward(1 if per_gaussian else 0, vol_size, gaussian_ids_sorted, tile_bins,
+                              pos3d, conics, intensities, vol_grad_in, tile_min, tile_max,
+                              cum_tiles_hit, l1=(sign, grad_loss))
 
 
 def voxelize_backward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,

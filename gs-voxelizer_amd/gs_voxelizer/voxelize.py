@@ -73,6 +73,45 @@ def voxelize_gaussians(
     )
 
 
+def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd):
+    """Prefix sum, binning and `fwd(gaussian_ids_sorted, tile_bins)` for a
+    non-empty Gaussian set.  Returns (num_intersects, ids, tile_bins, cum,
+    fwd's result); ids is None when there are no intersections."""
+    cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous())
+    dev = cum_tiles_hit.device
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    cap = _capacity.get(key) if _speculate() else None
+    if cap is not None:
+        # launch at the recorded capacity; the count travels meanwhile
+        host = torch.empty((1,), dtype=torch.int64, pin_memory=True)
+        host.copy_(total, non_blocking=True)
+        copied = torch.cuda.Event()
+        copied.record()
+        ids_cap, tile_bins = _C.bin_and_sort_gaussians_device_count(
+            num_gaussians, cap, total, tile_min, tile_max, cum_tiles_hit, vol_size_voxel)
+        result = fwd(ids_cap, tile_bins)
+        copied.synchronize()  # the queued kernels keep the GPU busy meanwhile
+        num_intersects = int(host[0])
+        if num_intersects <= cap:
+            if num_intersects < cap // 4:
+                _capacity[key] = _grow(num_intersects)
+            ids = ids_cap[:num_intersects] if num_intersects > 0 else None
+            return num_intersects, ids, tile_bins, cum_tiles_hit, result
+    else:
+        num_intersects = int(total.item())
+    if num_intersects > _INT32_MAX:
+        raise RuntimeError(
+            f"gs_voxelizer: {num_intersects} tile intersections overflow the int32 layout")
+    if _speculate():
+        _capacity[key] = _grow(num_intersects)
+    if num_intersects < 1:
+        return 0, None, None, cum_tiles_hit, None
+    # first call on the device, host read requested, or the capacity overflowed
+    ids, tile_bins = bin_and_sort_gaussians(num_gaussians, num_intersects, tile_min, tile_max,
+                                            cum_tiles_hit, vol_size_voxel)
+    return num_intersects, ids, tile_bins, cum_tiles_hit, fwd(ids, tile_bins)
+
+
 class _VoxelizeGaussians(Function):
     @staticmethod
     def forward(ctx, pos3d_radii, conics, intensities, vol_size_voxel, tile_min, tile_max,
@@ -84,55 +123,23 @@ class _VoxelizeGaussians(Function):
         ctx.use_per_gaussian_backward = use_per_gaussian_backward
         dev = pos3d_radii.device
         D, H, W = (int(v) for v in vol_size_voxel)
+        C = intensities.shape[-1]
         boxes = ()
-        if num_gaussians == 0:
-            out = torch.zeros(D, H, W, intensities.shape[-1], device=dev, dtype=pos3d_radii.dtype)
+        gaussian_ids_sorted = tile_bins = None
+        ctx.num_intersects = 0
+        if num_gaussians > 0:
+            fwd = lambda ids, bins: _C.voxelize_forward(vol_size_voxel, ids, bins, pos3d_radii,
+                                                        conics, intensities)
+            I, gaussian_ids_sorted, tile_bins, cum_tiles_hit, out = _bin_and_forward(
+                num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd)
+            ctx.num_intersects = I
+            # the backward reduces per-pair partials in duplication order (no atomics)
+            boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit)
+        if ctx.num_intersects < 1:
+            out = torch.zeros(D, H, W, C, device=dev, dtype=pos3d_radii.dtype)
             gaussian_ids_sorted = torch.zeros(0, 1, device=dev, dtype=torch.int32)
             tile_bins = torch.zeros(0, 3, device=dev, dtype=torch.int32)
-            ctx.num_intersects = 0
-        else:
-            cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous())
-            key = dev.index if dev.index is not None else torch.cuda.current_device()
-            cap = _capacity.get(key) if _speculate() else None
-            gaussian_ids_sorted = None
-            if cap is not None:
-                # launch at the recorded capacity; the count travels meanwhile
-                host = torch.empty((1,), dtype=torch.int64, pin_memory=True)
-                host.copy_(total, non_blocking=True)
-                copied = torch.cuda.Event()
-                copied.record()
-                ids_cap, tile_bins = _C.bin_and_sort_gaussians_device_count(
-                    num_gaussians, cap, total, tile_min, tile_max, cum_tiles_hit, vol_size_voxel)
-                out = _C.voxelize_forward(vol_size_voxel, ids_cap, tile_bins, pos3d_radii, conics,
-                                          intensities)
-                copied.synchronize()  # the queued kernels keep the GPU busy meanwhile
-                num_intersects = int(host[0])
-                if num_intersects <= cap:
-                    gaussian_ids_sorted = ids_cap[:num_intersects]
-                    if num_intersects < cap // 4:
-                        _capacity[key] = _grow(num_intersects)
-            else:
-                num_intersects = int(total.item())
-            if num_intersects > _INT32_MAX:
-                raise RuntimeError(
-                    f"gs_voxelizer: {num_intersects} tile intersections overflow the int32 layout")
-            ctx.num_intersects = num_intersects
-            if num_intersects < 1:
-                out = torch.zeros(D, H, W, intensities.shape[-1], device=dev)
-                gaussian_ids_sorted = torch.zeros(0, 1, device=dev, dtype=torch.int32)
-                tile_bins = torch.zeros(0, 3, device=dev, dtype=torch.int32)
-            else:
-                if gaussian_ids_sorted is None:  # first call, host read requested, or overflow
-                    gaussian_ids_sorted, tile_bins = bin_and_sort_gaussians(
-                        num_gaussians, num_intersects, tile_min, tile_max, cum_tiles_hit,
-                        vol_size_voxel)
-                    out = _C.voxelize_forward(vol_size_voxel, gaussian_ids_sorted, tile_bins,
-                                              pos3d_radii, conics, intensities)
-                    if _speculate():
-                        _capacity[key] = _grow(num_intersects)
-                # the backward reduces per-pair partials in duplication order (no atomics)
-                boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit)
-        ctx.n_boxes = len(boxes)
+            boxes = ()
         ctx.set_materialize_grads(False)  # an unused volume needs no zero-filled gradient
         ctx.save_for_backward(pos3d_radii, conics, intensities, gaussian_ids_sorted, tile_bins,
                               *boxes)
@@ -155,3 +162,90 @@ class _VoxelizeGaussians(Function):
                 vol_size_voxel, gaussian_ids_sorted, tile_bins, pos3d_radii, conics, intensities,
                 vol_grad.contiguous(), *boxes)
         return pos3d_grad, conics_grad, intensities_grad, None, None, None, None, None
+
+
+def voxelize_gaussians_l1_loss(
+    pos3d_radii: Tensor,
+    conics: Tensor,
+    intensities: Tensor,
+    vol_size_voxel: Tuple[int, int, int],
+    tile_min: Tensor,
+    tile_max: Tensor,
+    num_tiles_hit: Tensor,
+    target: Tensor,
+    use_per_gaussian_backward: bool = True,
+) -> Tuple[Tensor, Tensor]:
+    """voxelize_gaussians fused with the L1 loss of the reference's training loop.
+
+    Returns (loss, volume) with loss = torch.nn.functional.l1_loss(volume, target)
+    (mean over all elements).  The backward forms dL/dvolume = sgn(volume -
+    target) * grad / numel inside the voxelization backward instead of
+    materialising it (and the loss inside the forward kernel), which is the same
+    gradient, bit for bit, as the unfused sequence.  `target` has the volume's
+    (D, H, W, C) shape, or (D, H, W) for one channel.  The returned volume is
+    differentiable too; a gradient reaching it from other uses is added.
+    The loss equals torch's up to float summation order.
+    """
+    return _VoxelizeL1.apply(
+        pos3d_radii.contiguous(),
+        conics.contiguous(),
+        intensities.contiguous(),
+        vol_size_voxel,
+        tile_min,
+        tile_max,
+        num_tiles_hit,
+        target.contiguous(),
+        use_per_gaussian_backward,
+    )
+
+
+class _VoxelizeL1(Function):
+    @staticmethod
+    def forward(ctx, pos3d_radii, conics, intensities, vol_size_voxel, tile_min, tile_max,
+                num_tiles_hit, target, use_per_gaussian_backward=True):
+        if intensities.dim() == 1:
+            intensities = intensities.unsqueeze(-1)
+        num_gaussians = pos3d_radii.size(-2)
+        ctx.vol_size_voxel = vol_size_voxel
+        ctx.use_per_gaussian_backward = use_per_gaussian_backward
+        dev = pos3d_radii.device
+        D, H, W = (int(v) for v in vol_size_voxel)
+        C = intensities.shape[-1]
+        fwd = lambda ids, bins: _C.voxelize_forward_l1(vol_size_voxel, ids, bins, pos3d_radii,
+                                                       conics, intensities, target)
+        boxes = ()
+        ctx.num_intersects = 0
+        if num_gaussians > 0:
+            I, ids, tile_bins, cum_tiles_hit, res = _bin_and_forward(
+                num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd)
+            ctx.num_intersects = I
+            boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit)
+        if ctx.num_intersects < 1:
+            # no Gaussian touches the volume: it is zero, the loss mean(|target|)
+            empty_ids = torch.zeros(0, device=dev, dtype=torch.int32)
+            Tx, Ty, Tz = ((int(v) + 7) // 8 for v in (W, H, D))
+            bins = torch.zeros(Tx * Ty * Tz, 2, device=dev, dtype=torch.int32)
+            res = fwd(empty_ids, bins)
+            ids, tile_bins, boxes = empty_ids, bins, ()
+        volume, loss, sign = res
+        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(pos3d_radii, conics, intensities, ids, tile_bins, sign, *boxes)
+        return loss, volume
+
+    @staticmethod
+    def backward(ctx, grad_loss, grad_volume):
+        saved = ctx.saved_tensors
+        pos3d_radii, conics, intensities, ids, tile_bins, sign = saved[:6]
+        boxes = saved[6:]
+        if ctx.num_intersects < 1 or (grad_loss is None and grad_volume is None):
+            z = (torch.zeros_like(pos3d_radii), torch.zeros_like(conics),
+                 torch.zeros_like(intensities))
+        else:
+            if grad_loss is None:
+                grad_loss = torch.zeros((), device=sign.device, dtype=torch.float32)
+            z = _C.voxelize_backward_l1(
+                ctx.vol_size_voxel, ids, tile_bins, pos3d_radii, conics, intensities, sign,
+                grad_loss.contiguous(),
+                grad_volume.contiguous() if grad_volume is not None else None, *boxes,
+                per_gaussian=ctx.use_per_gaussian_backward)
+        return z[0], z[1], z[2], None, None, None, None, None, None

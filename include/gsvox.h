@@ -167,6 +167,41 @@ int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
                      size_t workspace_bytes, void *stream);
 
 /*
+ * Voxelization fused with an L1 loss.  These have no reference binding.  They
+ * fuse the voxelizer with the loss of the reference's training loop (README.md:77-82,
+ * torch.nn.functional.l1_loss with reduction "mean") so that dL/dvolume is
+ * never materialised.
+ *
+ * gsv_voxelize_fwd_l1: gsv_voxelize_fwd plus *loss (one float on the device)
+ * = mean over all D*H*W*channels elements of |volume - target|, target laid
+ * out like volume.  The loss is summed per tile in binary32 and over tiles in
+ * binary64 in a fixed order.  `sign` (int8, laid out like volume) receives
+ * sgn(volume - target): -1, 0, 1, or 2 where the difference is NaN.
+ * Workspace: gsv_voxelize_fwd_l1_workspace_bytes.
+ *
+ * gsv_voxelize_bwd_l1: gsv_voxelize_bwd with vol_grad replaced by
+ * sign * (*grad_loss * (1 / numel)), exactly what torch's l1_loss backward
+ * produces, plus vol_grad when it is not NULL (the volume's gradient from
+ * other uses).  grad_loss is one float on the device.  Same workspace and
+ * reduction modes as gsv_voxelize_bwd.
+ */
+int gsv_voxelize_fwd_l1_workspace_bytes(int32_t D, int32_t H, int32_t W, size_t *bytes);
+int gsv_voxelize_fwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                        int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                        const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
+                        const float *intensities, const float *target, float *volume,
+                        int8_t *sign, float *loss, void *workspace, size_t workspace_bytes,
+                        void *stream);
+int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
+                        int64_t num_intersects, const int32_t *gaussian_ids_sorted,
+                        const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
+                        const float *intensities, const int8_t *sign, const float *grad_loss,
+                        const float *vol_grad, const int32_t *tile_min, const int32_t *tile_max,
+                        const int32_t *cum_tiles_hit, float *dpos3d_radii, float *dconics,
+                        float *dintensities, int32_t variant, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/*
  * Kernel timing (no counterpart in the reference; for benchmarks and
  * profiling).  While enabled, each launch of the hot kernels is bracketed by
  * two HIP events recorded on its launch stream.  collect() waits for the
