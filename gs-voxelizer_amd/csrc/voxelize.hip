@@ -41,7 +41,6 @@
 #include <float.h>
 
 #include "gsv_device.h"
-#include "gsv_scan.h"
 
 namespace gsv {
 namespace {
@@ -352,30 +351,17 @@ __global__ __launch_bounds__(kFinishThreads) void k_loss_finish(const float *__r
 
 // --------------------------------------------------------------- backward --
 
-constexpr int kBucket = kWave;  // (tile, Gaussian) pairs per wave
-
-// Buckets per tile, read by the bucket scan: ceil(pairs / 64).
-struct BucketCountLoad {
-    const int2 *bins;
-    __device__ int operator()(int64_t t) const {
-        const int2 r = bins[t];
-        const int m = max(0, r.y - r.x);
-        return (m + kBucket - 1) / kBucket;
-    }
-};
-
-// Written by the bucket scan: the tile's first bucket, and bucket -> tile for
-// each of its buckets (capped at the launch's bucket capacity).
-struct BucketFillStore {
-    int *offs;
-    int *bucket_tile;
-    int64_t cap;
-    __device__ void operator()(int64_t t, int first, int count) const {
-        offs[t] = first;
-        for (int k = 0; k < count; ++k)
-            if ((int64_t)first + k < cap) bucket_tile[first + k] = (int)t;
-    }
-};
+// pair_tiles[p] = tile of sorted pair p: one wave per tile writes its range.
+// Also zeroes the count of backward waves left for k_vox_bwd_rest.
+__global__ __launch_bounds__(kWave) void k_pair_tiles(const int2 *__restrict__ bins, int n_isect,
+                                                      int *__restrict__ pair_tiles,
+                                                      int *__restrict__ rest_count) {
+    const int t = blockIdx.x;
+    if (t == 0 && threadIdx.x == 0) *rest_count = 0;
+    const int2 r = bins[t];
+    const int e = min(r.y, n_isect);
+    for (int q = max(r.x, 0) + (int)threadIdx.x; q < e; q += kWave) pair_tiles[q] = t;
+}
 
 template <int C>
 struct Moments {
@@ -383,7 +369,7 @@ struct Moments {
     float dI[C];
 };
 
-// Moments of h = a * G about the Gaussian's centre for one lane's pair:
+// Adds to M the moments of h = a * G about the Gaussian's centre for one lane's pair:
 // S[..] = sum h * delta^k, delta = mu - p, G = sum_c I_c g_c (g_c alone for
 // C == 1; I folds into the final scale).  Per voxel: h, h*dx, h*dx^2 by FMAs
 // against the lane's hoisted dx_u and dx_u^2; rows fold in dy, planes in dz.
@@ -393,14 +379,10 @@ struct Moments {
 //              hardware flush (bound = the gate-free offset, shift unused);
 //   otherwise: a = exp2(s) if |s| <= bound, s = sigma2 - shift.
 template <int C, bool kGateFree>
-__device__ __forceinline__ void pair_moments(const float4 (*s_g)[2 * C], int ny, int nz,
+__device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int nz,
                                              float mxl, float myl, float mzl, float A2, float Bn,
                                              float Cn, float Dn, float En, float Fn, float shift,
                                              float bound, const float (&I)[C], Moments<C> &M) {
-    M.S0 = M.Sx = M.Sy = M.Sz = 0.f;
-    M.Sxx = M.Sxy = M.Sxz = M.Syy = M.Syz = M.Szz = 0.f;
-#pragma unroll
-    for (int c = 0; c < C; ++c) M.dI[c] = 0.f;
     float dxu[GSV_TILE], dxu2[GSV_TILE];
 #pragma unroll
     for (int u = 0; u < GSV_TILE; ++u) {
@@ -419,7 +401,7 @@ __device__ __forceinline__ void pair_moments(const float4 (*s_g)[2 * C], int ny,
             float gv[GSV_TILE * C];
 #pragma unroll
             for (int q = 0; q < 2 * C; ++q) {
-                const float4 t4 = s_g[row][q];
+                const float4 t4 = s_rows[row * 2 * C + q];
                 gv[4 * q] = t4.x; gv[4 * q + 1] = t4.y; gv[4 * q + 2] = t4.z; gv[4 * q + 3] = t4.w;
             }
             const float dy = myl - ((float)ly - 3.5f);
@@ -471,116 +453,176 @@ __device__ __forceinline__ void pair_moments(const float4 (*s_g)[2 * C], int ny,
     }
 }
 
-// vol_grad of a tile is staged scaled by 2^m so that its largest magnitude
-// lies in [2^89, 2^90): with the gate-free a >= 2^-126, every h = a * G is then
-// a normal number whatever the loss scale.  The epilogue divides 2^m out.
+// vol_grad of a tile is staged scaled by a power of two so that its largest
+// magnitude lies in [2^89, 2^90): with the gate-free a >= 2^-126, every
+// h = a * G is then a normal number whatever the loss scale.  The epilogue
+// divides the factor out.
 constexpr int kGradScaleExp = 90;
 
+// Tiles staged at once by a backward wave: the LDS of K tiles (2 KB * C each)
+// must leave room for several waves per CU.
 template <int C>
-__global__ __launch_bounds__(kWave) void k_vox_bwd(
-    int D, int H, int W, int Tx, int Ty, int n, int n_isect, const int *__restrict__ ids,
-    const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
-    const float2 *__restrict__ conics, const float *__restrict__ intens,
-    const float *__restrict__ vol_grad, const int8_t *__restrict__ l1_sgn,
-    const float *__restrict__ l1_grad, float l1_numel,
-    const int *__restrict__ bucket_tile,
-    const int *__restrict__ bucket_off, const int64_t *__restrict__ total_buckets, int64_t cap,
-    float *__restrict__ dpos, float *__restrict__ dconic, float *__restrict__ dint,
-    const int *__restrict__ tile_min, const int *__restrict__ tile_max,
-    const int *__restrict__ cum, float *__restrict__ partial) {
-    __shared__ float4 s_g[kWave][2 * C];  // vol_grad of the tile: row (ly + 8*lz), 8*C floats
-    const int64_t total = min<int64_t>(*total_buckets, cap);
-    const int64_t per = xcd_per(total);
-    const int64_t bkt = xcd_remap(blockIdx.x, per);
-    if (bkt >= total || blockIdx.x >= kXcds * per) return;
-    const int lane = threadIdx.x;
-    const int tile = bucket_tile[bkt];
-    const int chunk = (int)(bkt - bucket_off[tile]);
-    int2 range = bins[tile];
-    range.x = max(range.x, 0);
-    range.y = min(range.y, n_isect);  // never index past the id array
-    const TileGeom tg = tile_geom(tile, Tx, Ty, D, H, W);
+constexpr int kStageTiles = 2;
 
-    // this lane's Gaussian
-    const int idx = range.x + chunk * kBucket + lane;
-    bool live = false, fast = false;
-    int g = 0;
-    float mxl = 0.f, myl = 0.f, mzl = 0.f;
-    float ca = 0.f, cb = 0.f, cc = 0.f, cd = 0.f, ce = 0.f, cf = 0.f;
+struct BwdArgs {
+    int D, H, W, Tx, Ty, n, n_isect;
+    int64_t T, per;
+    const int *ids, *pair_tiles;
+    const float4 *pos_radii;
+    const float2 *conics;
+    const float *intens, *vol_grad;
+    const int8_t *l1_sgn;
+    const float *l1_grad;
+    float l1_numel;
+    float *dpos, *dconic, *dint;
+    const int *tile_min, *tile_max, *cum;
+    float *partial;
+    int *rest_count, *rest_waves;  // waves spanning more than K tiles
+};
+
+// One backward wave's view: lane = one of 64 consecutive (tile, Gaussian)
+// pairs of the sorted list; `slot` numbers the runs of equal tiles.
+template <int C>
+struct BwdLane {
+    int tile, slot, g;
+    bool valid, live, fast;
+    float mxl, myl, mzl, ca, cb, cc, cd, ce, cf;
     float I[C];
-#pragma unroll
-    for (int c = 0; c < C; ++c) I[c] = 0.f;
-    Gate gt = make_gate(0.f);
-    if (idx < range.y) {
-        g = ids[idx];
-        if ((unsigned)g < (unsigned)n) {
-            const float4 p = pos_radii[g];
-            const float2 c01 = conics[3 * g], c23 = conics[3 * g + 1], c45 = conics[3 * g + 2];
-            ca = c01.x; cb = c01.y; cc = c23.x; cd = c23.y; ce = c45.x; cf = c45.y;
-            float mean = 0.f, max_abs = 0.f;
-#pragma unroll
-            for (int c = 0; c < C; ++c) {
-                I[c] = intens[(size_t)g * C + c];
-                mean += I[c];
-                max_abs = fmaxf(max_abs, fabsf(I[c]));
-            }
-            mean /= (float)C;
-            gt = make_gate(mean);
-            live = gt.live;
-            if (live && gt.bounded)
-                live = may_touch(p.x, p.y, p.z, ca, cb, cc, cd, ce, cf, gt.t2, tg.xlo, tg.xhi,
-                                 tg.ylo, tg.yhi, tg.zlo, tg.zhi);
-            if (live) {
-                fast = gate_free_ok(gt, max_abs, p.x, p.y, p.z, ca, cb, cc, cd, ce, cf);
-                // delta = mu - p = (mu - tile centre) - p', p' = local index - 3.5
-                mxl = p.x - (float)tg.x0 - 4.0f;
-                myl = p.y - (float)tg.y0 - 4.0f;
-                mzl = p.z - (float)tg.z0 - 4.0f;
-            }
-        }
-    }
-    // One wave-uniform choice: gate-free unless a live lane needs the exact gate.
-    const bool wave_fast = __all(!live || fast);
+    Gate gt;
+    TileGeom tg;
+};
 
-    int gexp = 0;  // vol_grad is staged as g * 2^gexp
-    {   // stage the tile's vol_grad, lane = row; outside voxels are zero
-        const int y = tg.y0 + (lane & 7), z = tg.z0 + (lane >> 3);
-        float v[GSV_TILE * C];
+// Which tiles the wave's pairs lie in (cheap: one coalesced load and ballots).
+template <int C>
+__device__ __forceinline__ bool bwd_slots(const BwdArgs &a, int64_t p0, BwdLane<C> &L,
+                                          uint64_t &starts, int &nslots) {
+    const int lane = threadIdx.x;
+    const int64_t p = p0 + lane;
+    int tile = p < a.n_isect ? a.pair_tiles[p] : -1;
+    if (tile < 0 || tile >= a.T) tile = -1;
+    L.tile = tile;
+    L.valid = tile >= 0;
+    const int prev_tile = __shfl_up(tile, 1, kWave);
+    starts = __ballot(L.valid && (lane == 0 || prev_tile != tile));
+    nslots = __popcll(starts);
+    const uint64_t upto = lane == kWave - 1 ? ~0ull : ((2ull << lane) - 1);
+    L.slot = L.valid ? __popcll(starts & upto) - 1 : -1;
+    return nslots > 0;
+}
+
+// The lane's Gaussian, its gate and its offsets from the tile centre.
+template <int C>
+__device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, int64_t p0, BwdLane<C> &L) {
+    L.live = L.fast = false;
+    L.g = 0;
+    L.mxl = L.myl = L.mzl = 0.f;
+    L.ca = L.cb = L.cc = L.cd = L.ce = L.cf = 0.f;
 #pragma unroll
-        for (int i = 0; i < GSV_TILE * C; ++i) v[i] = 0.f;
-        if (y < H && z < D) {
-            const int64_t off = (((int64_t)z * H + y) * W + tg.x0) * C;
-            const int nx = min(GSV_TILE, W - tg.x0);
-            if (l1_sgn != nullptr) {
-                // fused L1 (torch's l1_loss, mean): dL/dv = sgn(v - t) * (dL / numel),
-                // plus the volume's own incoming gradient when it has one.  The
-                // division is a multiply by the binary32 reciprocal, as torch's
-                // division by a host scalar does, so the bits agree.
-                const float sc = *l1_grad * (1.0f / l1_numel);
-                const int8_t *sg = l1_sgn + off;
+    for (int c = 0; c < C; ++c) L.I[c] = 0.f;
+    L.gt = make_gate(0.f);
+    L.tg = tile_geom(L.valid ? L.tile : 0, a.Tx, a.Ty, a.D, a.H, a.W);
+    if (!L.valid) return;
+    const int g = a.ids[p0 + threadIdx.x];
+    L.g = g;
+    if ((unsigned)g >= (unsigned)a.n) return;
+    const float4 pr = a.pos_radii[g];
+    const float2 c01 = a.conics[3 * g], c23 = a.conics[3 * g + 1], c45 = a.conics[3 * g + 2];
+    L.ca = c01.x; L.cb = c01.y; L.cc = c23.x; L.cd = c23.y; L.ce = c45.x; L.cf = c45.y;
+    float mean = 0.f, max_abs = 0.f;
 #pragma unroll
-                for (int u = 0; u < GSV_TILE; ++u)
-                    if (u < nx)
+    for (int c = 0; c < C; ++c) {
+        L.I[c] = a.intens[(size_t)g * C + c];
+        mean += L.I[c];
+        max_abs = fmaxf(max_abs, fabsf(L.I[c]));
+    }
+    mean /= (float)C;
+    L.gt = make_gate(mean);
+    L.live = L.gt.live;
+    const TileGeom &tg = L.tg;
+    if (L.live && L.gt.bounded)
+        L.live = may_touch(pr.x, pr.y, pr.z, L.ca, L.cb, L.cc, L.cd, L.ce, L.cf, L.gt.t2, tg.xlo,
+                           tg.xhi, tg.ylo, tg.yhi, tg.zlo, tg.zhi);
+    if (L.live) {
+        L.fast = gate_free_ok(L.gt, max_abs, pr.x, pr.y, pr.z, L.ca, L.cb, L.cc, L.cd, L.ce, L.cf);
+        // delta = mu - p = (mu - tile centre) - p', p' = local index - 3.5
+        L.mxl = pr.x - (float)tg.x0 - 4.0f;
+        L.myl = pr.y - (float)tg.y0 - 4.0f;
+        L.mzl = pr.z - (float)tg.z0 - 4.0f;
+    }
+}
+
+// One group of up to K tiles (slots g0 .. g0+K-1): stage them in LDS (lane =
+// row), accumulate each in-group lane's moments against its own tile's rows,
+// and write those lanes' gradients.  Lanes outside the group evaluate a zero
+// form at the dead offset and write nothing.
+template <int C, int K>
+__device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L, uint64_t starts,
+                                          int g0, bool wave_fast, bool any_live, float4 *s_g) {
+    constexpr int kRowF4 = 2 * C;              // float4 per staged row
+    constexpr int kSlot = kWave * kRowF4 + 1;  // +16 B: slots start on different banks
+    const int lane = threadIdx.x;
+    const bool mine = L.valid && L.slot >= g0 && L.slot < g0 + K;
+    const bool in_grp = mine && L.live;
+    Moments<C> M;
+    M.S0 = M.Sx = M.Sy = M.Sz = 0.f;
+    M.Sxx = M.Sxy = M.Sxz = M.Syy = M.Syz = M.Szz = 0.f;
 #pragma unroll
-                        for (int c = 0; c < C; ++c) {
-                            const int8_t q = sg[u * C + c];
-                            float gv = q == kSgnNaN ? __builtin_nanf("") : sc * (float)q;
-                            if (vol_grad != nullptr) gv += vol_grad[off + u * C + c];
-                            v[u * C + c] = gv;
-                        }
-            } else {
-                const float *src = vol_grad + off;
+    for (int c = 0; c < C; ++c) M.dI[c] = 0.f;
+    int gexp = 0;  // vol_grad of the group's tiles is staged as g * 2^gexp
+    if (any_live) {
+        uint64_t rest = starts;
+        for (int k = 0; k < g0; ++k) rest &= rest - 1;  // skip earlier groups' tiles
+        const int y_l = lane & 7, z_l = lane >> 3;
+        float mx = 0.f;
 #pragma unroll
-                for (int u = 0; u < GSV_TILE; ++u)
-                    if (u < nx)
+        for (int k = 0; k < K; ++k) {
+            float v[GSV_TILE * C];
 #pragma unroll
-                        for (int c = 0; c < C; ++c) v[u * C + c] = src[u * C + c];
+            for (int i = 0; i < GSV_TILE * C; ++i) v[i] = 0.f;
+            if (rest) {
+                const int first = __builtin_ctzll(rest);
+                rest &= rest - 1;
+                const int tk = __shfl(L.tile, first, kWave);
+                const TileGeom kg = tile_geom(tk, a.Tx, a.Ty, a.D, a.H, a.W);
+                const int y = kg.y0 + y_l, z = kg.z0 + z_l;
+                if (y < a.H && z < a.D) {
+                    const int64_t off = (((int64_t)z * a.H + y) * a.W + kg.x0) * C;
+                    const int nx = min(GSV_TILE, a.W - kg.x0);
+                    if (a.l1_sgn != nullptr) {
+                        // fused L1 (torch's l1_loss, mean): dL/dv = sgn(v - t) * (dL / numel),
+                        // plus the volume's own incoming gradient when it has one.  The
+                        // division is a multiply by the binary32 reciprocal, as torch's
+                        // division by a host scalar does, so the bits agree.
+                        const float sc = *a.l1_grad * (1.0f / a.l1_numel);
+                        const int8_t *sg = a.l1_sgn + off;
+#pragma unroll
+                        for (int u = 0; u < GSV_TILE; ++u)
+                            if (u < nx)
+#pragma unroll
+                                for (int c = 0; c < C; ++c) {
+                                    const int8_t q = sg[u * C + c];
+                                    float gv = q == kSgnNaN ? __builtin_nanf("") : sc * (float)q;
+                                    if (a.vol_grad != nullptr) gv += a.vol_grad[off + u * C + c];
+                                    v[u * C + c] = gv;
+                                }
+                    } else {
+                        const float *src = a.vol_grad + off;
+#pragma unroll
+                        for (int u = 0; u < GSV_TILE; ++u)
+                            if (u < nx)
+#pragma unroll
+                                for (int c = 0; c < C; ++c) v[u * C + c] = src[u * C + c];
+                    }
+                }
             }
-        }
-        if (wave_fast) {
-            float mx = 0.f;
 #pragma unroll
             for (int i = 0; i < GSV_TILE * C; ++i) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+            for (int q = 0; q < kRowF4; ++q)
+                s_g[k * kSlot + lane * kRowF4 + q] =
+                    make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        }
+        if (wave_fast) {  // one power-of-two scale for the group, applied in LDS
 #pragma unroll
             for (int o = kWave / 2; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
             if (mx > 0.f && mx <= FLT_MAX) {
@@ -588,36 +630,38 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
                 (void)frexpf(mx, &e);
                 gexp = kGradScaleExp - e;
             }
+            if (gexp != 0) {
 #pragma unroll
-            for (int i = 0; i < GSV_TILE * C; ++i) v[i] = ldexpf(v[i], gexp);
+                for (int k = 0; k < K; ++k)
+#pragma unroll
+                    for (int q = 0; q < kRowF4; ++q) {
+                        float4 &t4 = s_g[k * kSlot + lane * kRowF4 + q];
+                        t4 = make_float4(ldexpf(t4.x, gexp), ldexpf(t4.y, gexp),
+                                         ldexpf(t4.z, gexp), ldexpf(t4.w, gexp));
+                    }
+            }
         }
-#pragma unroll
-        for (int q = 0; q < 2 * C; ++q)
-            s_g[lane][q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        __syncthreads();
+        const int my = in_grp ? L.slot - g0 : 0;
+        // lanes outside the group evaluate a zero form at the dead offset (a = 0)
+        const float A2 = in_grp ? -0.5f * kLog2e * L.ca : 0.f, Bn = in_grp ? -kLog2e * L.cb : 0.f;
+        const float Cn = in_grp ? -kLog2e * L.cc : 0.f, Dn = in_grp ? -0.5f * kLog2e * L.cd : 0.f;
+        const float En = in_grp ? -kLog2e * L.ce : 0.f, Fn = in_grp ? -0.5f * kLog2e * L.cf : 0.f;
+        const float gx = in_grp ? L.mxl : 0.f, gy = in_grp ? L.myl : 0.f, gz = in_grp ? L.mzl : 0.f;
+        if (wave_fast)
+            pair_moments<C, true>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn, Cn, Dn,
+                                  En, Fn, 0.f, in_grp ? L.gt.off : kDeadOffset, L.I, M);
+        else
+            pair_moments<C, false>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn, Cn,
+                                   Dn, En, Fn, L.gt.shift, in_grp ? L.gt.half : -1.f, L.I, M);
+        __syncthreads();  // a later group restages the slots
     }
-    __syncthreads();
-    const bool any_live = __any(live);
-    if (!any_live && partial == nullptr) return;
-
-    // Dead lanes evaluate a zero form at the dead offset (a = 0 on both paths).
-    const float A2 = live ? -0.5f * kLog2e * ca : 0.f, Bn = live ? -kLog2e * cb : 0.f;
-    const float Cn = live ? -kLog2e * cc : 0.f, Dn = live ? -0.5f * kLog2e * cd : 0.f;
-    const float En = live ? -kLog2e * ce : 0.f, Fn = live ? -0.5f * kLog2e * cf : 0.f;
-    const int ny = min(GSV_TILE, H - tg.y0), nz = any_live ? min(GSV_TILE, D - tg.z0) : 0;
-    Moments<C> M;
-    double wscale;  // turns a sum of h into a sum of alpha * g
-    if (wave_fast) {
-        pair_moments<C, true>(s_g, ny, nz, mxl, myl, mzl, A2, Bn, Cn, Dn, En, Fn, 0.f,
-                              live ? gt.off : kDeadOffset, I, M);
-        wscale = live ? ldexp((double)gt.fscale, -gexp) : 0.0;
-    } else {
-        pair_moments<C, false>(s_g, ny, nz, mxl, myl, mzl, A2, Bn, Cn, Dn, En, Fn, gt.shift,
-                               live ? gt.half : -1.f, I, M);
-        wscale = live ? (double)gt.scale : 0.0;
-    }
+    if (!mine) return;
     // sigma-gradient weight per unit of h (alpha = scale * a); binary64 keeps the
     // 2^-gexp and 2^-off factors in range
-    const double w = (C == 1) ? wscale * (double)I[0] : wscale;
+    double wscale = 0.0;
+    if (L.live) wscale = wave_fast ? ldexp((double)L.gt.fscale, -gexp) : (double)L.gt.scale;
+    const double w = (C == 1) ? wscale * (double)L.I[0] : wscale;
     float out[9 + C];
     out[0] = (float)(-0.5 * w * (double)M.Sxx);
     out[1] = (float)(-w * (double)M.Sxy);
@@ -625,42 +669,92 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(
     out[3] = (float)(-0.5 * w * (double)M.Syy);
     out[4] = (float)(-w * (double)M.Syz);
     out[5] = (float)(-0.5 * w * (double)M.Szz);
-    out[6] = (float)(-w * ((double)ca * M.Sx + (double)cb * M.Sy + (double)cc * M.Sz));
-    out[7] = (float)(-w * ((double)cb * M.Sx + (double)cd * M.Sy + (double)ce * M.Sz));
-    out[8] = (float)(-w * ((double)cc * M.Sx + (double)ce * M.Sy + (double)cf * M.Sz));
+    out[6] = (float)(-w * ((double)L.ca * M.Sx + (double)L.cb * M.Sy + (double)L.cc * M.Sz));
+    out[7] = (float)(-w * ((double)L.cb * M.Sx + (double)L.cd * M.Sy + (double)L.ce * M.Sz));
+    out[8] = (float)(-w * ((double)L.cc * M.Sx + (double)L.ce * M.Sy + (double)L.cf * M.Sz));
     if (C == 1) {
         out[9] = (float)(wscale * (double)M.S0);
     } else {
 #pragma unroll
         for (int c = 0; c < C; ++c) out[9 + c] = (float)(wscale * (double)M.dI[c]);
     }
-    if (partial != nullptr) {
+    const int g = L.g;
+    if (a.partial != nullptr) {
         // Deterministic path: this pair's partial goes to its emission slot
         // e = cum[g-1] + ((tz-min.z)*ny + (ty-min.y))*nx + (tx-min.x), the order
         // the pairs were duplicated in (gaussian-major, tiles z->y->x), so each
         // Gaussian's partials are contiguous for the reduction pass.
-        if (idx < range.y && (unsigned)g < (unsigned)n) {
-            const int tx = tg.x0 / GSV_TILE, ty = tg.y0 / GSV_TILE, tz = tg.z0 / GSV_TILE;
-            const int mnx = tile_min[3 * g], mny = tile_min[3 * g + 1], mnz = tile_min[3 * g + 2];
-            const int nxb = tile_max[3 * g] - mnx, nyb = tile_max[3 * g + 1] - mny;
-            const int64_t base = g == 0 ? 0 : cum[g - 1];
+        if ((unsigned)g < (unsigned)a.n) {
+            const int tx = L.tg.x0 / GSV_TILE, ty = L.tg.y0 / GSV_TILE, tz = L.tg.z0 / GSV_TILE;
+            const int mnx = a.tile_min[3 * g], mny = a.tile_min[3 * g + 1];
+            const int mnz = a.tile_min[3 * g + 2];
+            const int nxb = a.tile_max[3 * g] - mnx, nyb = a.tile_max[3 * g + 1] - mny;
+            const int64_t base = g == 0 ? 0 : a.cum[g - 1];
             const int64_t e = base + ((int64_t)(tz - mnz) * nyb + (ty - mny)) * nxb + (tx - mnx);
-            if (e >= base && e < (int64_t)cum[g] && e < n_isect) {
-                float *dst = partial + e * (9 + C);
+            if (e >= base && e < (int64_t)a.cum[g] && e < a.n_isect) {
+                float *dst = a.partial + e * (9 + C);
 #pragma unroll
                 for (int q = 0; q < 9 + C; ++q) dst[q] = out[q];
             }
         }
-    } else if (live) {
-        float *dc = dconic + 6 * (size_t)g;
+    } else if (L.live) {
+        float *dc = a.dconic + 6 * (size_t)g;
 #pragma unroll
         for (int q = 0; q < 6; ++q) unsafeAtomicAdd(dc + q, out[q]);
-        float *dp = dpos + 4 * (size_t)g;
+        float *dp = a.dpos + 4 * (size_t)g;
 #pragma unroll
         for (int q = 0; q < 3; ++q) unsafeAtomicAdd(dp + q, out[6 + q]);
-        float *di = dint + (size_t)C * g;
+        float *di = a.dint + (size_t)C * g;
 #pragma unroll
         for (int c = 0; c < C; ++c) unsafeAtomicAdd(di + c, out[9 + c]);
+    }
+}
+
+// One wave per 64 consecutive (tile, Gaussian) pairs of the sorted list, lane
+// = pair, so no lane idles except in the last wave.  The wave stages the
+// first K tiles its pairs span (lane = row; each lane reads its own tile's
+// rows); a wave whose pairs span more tiles lists itself for k_vox_bwd_rest.
+template <int C, int K>
+__global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
+    __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
+    const int64_t wv = xcd_remap(blockIdx.x, a.per);
+    const int64_t p0 = wv * kWave;
+    if (p0 >= a.n_isect) return;
+    BwdLane<C> L;
+    uint64_t starts;
+    int nslots;
+    if (!bwd_slots(a, p0, L, starts, nslots)) return;
+    if (nslots > K && threadIdx.x == 0) a.rest_waves[atomicAdd(a.rest_count, 1)] = (int)wv;
+    bwd_gaussian(a, p0, L);
+    // one wave-uniform choice: gate-free unless a live lane needs the exact gate
+    const bool wave_fast = __all(!L.live || L.fast);
+    const bool any_live = __any(L.live);
+    if (!any_live && a.partial == nullptr) return;
+    bwd_group<C, K>(a, L, starts, 0, wave_fast, any_live, s_g);
+}
+
+// The pairs of the listed waves (those spanning more than K tiles), in groups
+// of K tiles after the first.  A fixed grid walks the list; every wave ends
+// when the list does.
+constexpr int kRestBlocks = 512;
+
+template <int C, int K>
+__global__ __launch_bounds__(kWave) void k_vox_bwd_rest(BwdArgs a) {
+    __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
+    const int count = *a.rest_count;
+    for (int i = blockIdx.x; i < count; i += gridDim.x) {
+        const int64_t p0 = (int64_t)a.rest_waves[i] * kWave;
+        if (p0 < 0 || p0 >= a.n_isect) continue;
+        BwdLane<C> L;
+        uint64_t starts;
+        int nslots;
+        if (!bwd_slots(a, p0, L, starts, nslots) || nslots <= K) continue;
+        bwd_gaussian(a, p0, L);
+        const bool wave_fast = __all(!L.live || L.fast);
+        const bool any_live = __any(L.live);
+        if (!any_live && a.partial == nullptr) continue;
+        for (int g0 = K; g0 < nslots; g0 += K)
+            bwd_group<C, K>(a, L, starts, g0, wave_fast, any_live, s_g);
     }
 }
 
@@ -722,20 +816,18 @@ __global__ __launch_bounds__(kReduceThreads) void k_pair_reduce(
 }
 
 struct BwdLayout {
-    size_t offs, scan, total, btile, partial, end;
-    int64_t cap;
+    size_t tiles, rest, partial, end;
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-BwdLayout bwd_layout(int64_t T, int64_t n_isect, int channels, bool pairs) {
+// pair -> tile map (n_isect ints), the count and list of backward waves left
+// for k_vox_bwd_rest, then the per-pair partials in pairs mode.
+BwdLayout bwd_layout(int64_t n_isect, int channels, bool pairs) {
     BwdLayout L{};
-    L.cap = imin64(T, n_isect) + (n_isect + kBucket - 1) / kBucket;
     size_t off = 0;
-    L.offs = off; off += align256((size_t)T * 4);
-    L.scan = off; off += scan_workspace_bytes(T);
-    L.total = off; off += 256;
-    L.btile = off; off += align256((size_t)imax64(L.cap, 1) * 4);
+    L.tiles = off; off += align256((size_t)imax64(n_isect, 1) * 4);
+    L.rest = off; off += align256(((size_t)(n_isect + kWave - 1) / kWave + 1) * 4);  // count, list
     L.partial = off;
     if (pairs) off += align256((size_t)n_isect * (9 + channels) * 4);
     L.end = off;
@@ -831,31 +923,40 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
     const int64_t T = (int64_t)Tx * Ty * Tz;
     if (T > INT32_MAX || num_intersects > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
-    const BwdLayout L = bwd_layout(T, num_intersects, channels, pairs);
+    const BwdLayout L = bwd_layout(num_intersects, channels, pairs);
     if (!workspace || workspace_bytes < L.end) return GSV_ERR_WORKSPACE_TOO_SMALL;
     char *ws = static_cast<char *>(workspace);
-    int *offs = reinterpret_cast<int *>(ws + L.offs);
-    int64_t *total = reinterpret_cast<int64_t *>(ws + L.total);
-    int *btile = reinterpret_cast<int *>(ws + L.btile);
+    int *pair_tiles = reinterpret_cast<int *>(ws + L.tiles);
+    int *rest = reinterpret_cast<int *>(ws + L.rest);
     float *partial = pairs ? reinterpret_cast<float *>(ws + L.partial) : nullptr;
-    // buckets per tile -> offsets, bucket -> tile map and the bucket total, in
-    // the scan's two launches
-    if (int st = scan_run(BucketCountLoad{reinterpret_cast<const int2 *>(tile_bins)},
-                          BucketFillStore{offs, btile, L.cap}, T, total, ws + L.scan,
-                          scan_workspace_bytes(T), s))
-        return st;
-    const dim3 grid((unsigned)(L.cap + kXcds)), block(kWave);
     const int ni = (int)num_intersects;
+    hipLaunchKernelGGL(k_pair_tiles, dim3((unsigned)T), dim3(kWave), 0, s,
+                       reinterpret_cast<const int2 *>(tile_bins), ni, pair_tiles, rest);
+    if (int st = check_launch()) return st;
+    const int64_t waves = (num_intersects + kWave - 1) / kWave;
+    const int64_t per = xcd_per(waves);
+    const dim3 grid((unsigned)(kXcds * per)), block(kWave);
     const float numel = (float)((int64_t)D * H * W * channels);
+    BwdArgs args;
+    args.D = D; args.H = H; args.W = W; args.Tx = Tx; args.Ty = Ty; args.n = n; args.n_isect = ni;
+    args.T = T; args.per = per;
+    args.ids = gaussian_ids_sorted; args.pair_tiles = pair_tiles;
+    args.pos_radii = reinterpret_cast<const float4 *>(pos3d_radii);
+    args.conics = reinterpret_cast<const float2 *>(conics);
+    args.intens = intensities; args.vol_grad = vol_grad;
+    args.l1_sgn = l1_sgn; args.l1_grad = l1_grad; args.l1_numel = numel;
+    args.dpos = dpos3d_radii; args.dconic = dconics; args.dint = dintensities;
+    args.tile_min = tile_min; args.tile_max = tile_max; args.cum = cum_tiles_hit;
+    args.partial = partial;
+    args.rest_count = rest;
+    args.rest_waves = rest + 1;
 #define GSV_VB(CH)                                                                                  \
     {                                                                                               \
         KernelTimer timer(kTimedVoxBwd, s);                                                         \
-        hipLaunchKernelGGL(k_vox_bwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, n, ni,                \
-                           gaussian_ids_sorted, reinterpret_cast<const int2 *>(tile_bins),          \
-                           reinterpret_cast<const float4 *>(pos3d_radii),                           \
-                           reinterpret_cast<const float2 *>(conics), intensities, vol_grad, l1_sgn, \
-                           l1_grad, numel, btile, offs, total, L.cap, dpos3d_radii,                \
-                           dconics, dintensities, tile_min, tile_max, cum_tiles_hit, partial);      \
+        hipLaunchKernelGGL((k_vox_bwd<CH, kStageTiles<CH>>), grid, block, 0, s, args);             \
+        if (int st = check_launch()) return st;                                                     \
+        hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTiles<CH>>), dim3(kRestBlocks), block, 0, s,  \
+                           args);                                                                   \
     }                                                                                               \
     if (int st = check_launch()) return st;                                                         \
     if (pairs) {                                                                                    \
@@ -919,8 +1020,7 @@ extern "C" int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W,
                                                 int32_t deterministic, size_t *bytes) {
     if (!bytes || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
     if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
-    const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
-    *bytes = bwd_layout(T, num_intersects > 0 ? num_intersects : 0, channels, deterministic != 0).end;
+    *bytes = bwd_layout(num_intersects > 0 ? num_intersects : 0, channels, deterministic != 0).end;
     return GSV_OK;
 }
 
