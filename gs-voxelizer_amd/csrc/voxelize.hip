@@ -462,7 +462,7 @@ constexpr int kGradScaleExp = 90;
 // Tiles staged at once by a backward wave: the LDS of K tiles (2 KB * C each)
 // must leave room for several waves per CU.
 template <int C>
-constexpr int kStageTiles = 2;
+constexpr int kStageTiles = C == 1 ? 3 : 2;
 
 struct BwdArgs {
     int D, H, W, Tx, Ty, n, n_isect;
