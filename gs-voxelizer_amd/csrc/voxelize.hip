@@ -136,9 +136,12 @@ struct TileGeom {
     float xlo, xhi, ylo, yhi, zlo, zhi;  // voxel-centre box of the tile's inside voxels
 };
 
-__device__ __forceinline__ TileGeom tile_geom(int64_t tile, int Tx, int Ty, int D, int H, int W) {
+// Tile counts are below 2^31 (checked on the host), so 32-bit division serves.
+__device__ __forceinline__ TileGeom tile_geom(int tile, int Tx, int Ty, int D, int H, int W) {
     TileGeom t;
-    const int tx = (int)(tile % Tx), ty = (int)((tile / Tx) % Ty), tz = (int)(tile / ((int64_t)Tx * Ty));
+    const unsigned q = (unsigned)tile / (unsigned)Tx;
+    const int tx = (int)((unsigned)tile - q * (unsigned)Tx);
+    const int ty = (int)(q % (unsigned)Ty), tz = (int)(q / (unsigned)Ty);
     t.x0 = tx * GSV_TILE; t.y0 = ty * GSV_TILE; t.z0 = tz * GSV_TILE;
     t.xlo = (float)t.x0 + 0.5f; t.xhi = (float)min(t.x0 + GSV_TILE - 1, W - 1) + 0.5f;
     t.ylo = (float)t.y0 + 0.5f; t.yhi = (float)min(t.y0 + GSV_TILE - 1, H - 1) + 0.5f;
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
     const int64_t tile = xcd_remap(blockIdx.x, per);
     if (tile >= T) return;
     const int lane = threadIdx.x;
-    const TileGeom tg = tile_geom(tile, Tx, Ty, D, H, W);
+    const TileGeom tg = tile_geom((int)tile, Tx, Ty, D, H, W);
     const float py = (float)(lane & 7) - 3.5f, pz = (float)(lane >> 3) - 3.5f;  // centred, tile-local
     int2 range = bins[tile];
     range.x = max(range.x, 0);
@@ -551,6 +554,88 @@ __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, int64_t p0, BwdLa
     }
 }
 
+// Exponent e such that m * 2^e lies in [2^(kGradScaleExp-1), 2^kGradScaleExp);
+// 0 for m = 0, infinite or NaN.
+__device__ __forceinline__ int grad_scale_exp(float m) {
+    if (!(m > 0.f && m <= FLT_MAX)) return 0;
+    int e;
+    (void)frexpf(m, &e);
+    return kGradScaleExp - e;
+}
+
+// Nonzero when some byte of w equals kSgnNaN (the zero-byte test on w ^ 0x02..).
+__device__ __forceinline__ uint32_t has_nan_byte(uint32_t w) {
+    const uint32_t x = w ^ (0x01010101u * (uint32_t)kSgnNaN);
+    return (x - 0x01010101u) & ~x & 0x80808080u;
+}
+
+// One staged row of the backward's source gradient: x = x0 .. x0+nx-1 of one
+// (y, z), C channels, at element offset `off`.  With the fused L1 sign bytes
+// the value is sc * sgn (NaN for kSgnNaN), plus vol_grad when that is given
+// too; otherwise it is vol_grad.  Full rows at a suitable alignment are read
+// with vector loads (one 8-byte load per 8 sign bytes, float4 for vol_grad).
+template <int C>
+__device__ __forceinline__ void load_grad_row(const BwdArgs &a, int64_t off, int nx, float sc,
+                                              float (&v)[GSV_TILE * C]) {
+    constexpr int kN = GSV_TILE * C;
+    if (a.l1_sgn != nullptr) {
+        const int8_t *sg = a.l1_sgn + off;
+        if (nx == GSV_TILE && ((uintptr_t)sg & 7) == 0) {
+            uint32_t w[kN / 4];
+#pragma unroll
+            for (int q = 0; q < kN / 8; ++q) {
+                const uint2 t = reinterpret_cast<const uint2 *>(sg)[q];
+                w[2 * q] = t.x;
+                w[2 * q + 1] = t.y;
+            }
+            uint32_t nan_bytes = 0;
+#pragma unroll
+            for (int q = 0; q < kN / 4; ++q) {
+                nan_bytes |= has_nan_byte(w[q]);
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    v[4 * q + b] = sc * (float)(int8_t)(w[q] >> (8 * b));
+            }
+            if (nan_bytes) {
+#pragma unroll
+                for (int i = 0; i < kN; ++i)
+                    if ((int8_t)(w[i / 4] >> (8 * (i % 4))) == kSgnNaN) v[i] = __builtin_nanf("");
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u)
+                if (u < nx)
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        const int8_t q = sg[u * C + c];
+                        v[u * C + c] = q == kSgnNaN ? __builtin_nanf("") : sc * (float)q;
+                    }
+        }
+        if (a.vol_grad != nullptr) {
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u)
+                if (u < nx)
+#pragma unroll
+                    for (int c = 0; c < C; ++c) v[u * C + c] += a.vol_grad[off + u * C + c];
+        }
+        return;
+    }
+    const float *src = a.vol_grad + off;
+    if (nx == GSV_TILE && ((uintptr_t)src & 15) == 0) {
+#pragma unroll
+        for (int q = 0; q < kN / 4; ++q) {
+            const float4 t = reinterpret_cast<const float4 *>(src)[q];
+            v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < GSV_TILE; ++u)
+            if (u < nx)
+#pragma unroll
+                for (int c = 0; c < C; ++c) v[u * C + c] = src[u * C + c];
+    }
+}
+
 // One group of up to K tiles (slots g0 .. g0+K-1): stage them in LDS (lane =
 // row), accumulate each in-group lane's moments against its own tile's rows,
 // and write those lanes' gradients.  Lanes outside the group evaluate a zero
@@ -573,6 +658,20 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
         uint64_t rest = starts;
         for (int k = 0; k < g0; ++k) rest &= rest - 1;  // skip earlier groups' tiles
         const int y_l = lane & 7, z_l = lane >> 3;
+        // fused L1 (torch's l1_loss, mean): dL/dv = sgn(v - t) * (dL / numel).  The
+        // division is a multiply by the binary32 reciprocal, as torch's division
+        // by a host scalar does, so the bits agree.  Without another incoming
+        // volume gradient every staged value is 0 or +-sc, so the group's scale
+        // follows from |sc| alone and is applied to sc up front (exactly).
+        const bool prescaled = a.l1_sgn != nullptr && a.vol_grad == nullptr;
+        float sc = 0.f;
+        if (a.l1_sgn != nullptr) {
+            sc = *a.l1_grad * (1.0f / a.l1_numel);
+            if (prescaled && wave_fast) {
+                gexp = grad_scale_exp(fabsf(sc));
+                sc = ldexpf(sc, gexp);
+            }
+        }
         float mx = 0.f;
 #pragma unroll
         for (int k = 0; k < K; ++k) {
@@ -582,54 +681,29 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
             if (rest) {
                 const int first = __builtin_ctzll(rest);
                 rest &= rest - 1;
-                const int tk = __shfl(L.tile, first, kWave);
-                const TileGeom kg = tile_geom(tk, a.Tx, a.Ty, a.D, a.H, a.W);
-                const int y = kg.y0 + y_l, z = kg.z0 + z_l;
+                // the tile's origin, read from the (valid) lane that starts its run
+                const int x0 = __builtin_amdgcn_readlane(L.tg.x0, first);
+                const int y = __builtin_amdgcn_readlane(L.tg.y0, first) + y_l;
+                const int z = __builtin_amdgcn_readlane(L.tg.z0, first) + z_l;
                 if (y < a.H && z < a.D) {
-                    const int64_t off = (((int64_t)z * a.H + y) * a.W + kg.x0) * C;
-                    const int nx = min(GSV_TILE, a.W - kg.x0);
-                    if (a.l1_sgn != nullptr) {
-                        // fused L1 (torch's l1_loss, mean): dL/dv = sgn(v - t) * (dL / numel),
-                        // plus the volume's own incoming gradient when it has one.  The
-                        // division is a multiply by the binary32 reciprocal, as torch's
-                        // division by a host scalar does, so the bits agree.
-                        const float sc = *a.l1_grad * (1.0f / a.l1_numel);
-                        const int8_t *sg = a.l1_sgn + off;
-#pragma unroll
-                        for (int u = 0; u < GSV_TILE; ++u)
-                            if (u < nx)
-#pragma unroll
-                                for (int c = 0; c < C; ++c) {
-                                    const int8_t q = sg[u * C + c];
-                                    float gv = q == kSgnNaN ? __builtin_nanf("") : sc * (float)q;
-                                    if (a.vol_grad != nullptr) gv += a.vol_grad[off + u * C + c];
-                                    v[u * C + c] = gv;
-                                }
-                    } else {
-                        const float *src = a.vol_grad + off;
-#pragma unroll
-                        for (int u = 0; u < GSV_TILE; ++u)
-                            if (u < nx)
-#pragma unroll
-                                for (int c = 0; c < C; ++c) v[u * C + c] = src[u * C + c];
-                    }
+                    const int64_t off = (((int64_t)z * a.H + y) * a.W + x0) * C;
+                    const int nx = min(GSV_TILE, a.W - x0);
+                    load_grad_row<C>(a, off, nx, sc, v);
                 }
             }
+            if (!prescaled) {
 #pragma unroll
-            for (int i = 0; i < GSV_TILE * C; ++i) mx = fmaxf(mx, fabsf(v[i]));
+                for (int i = 0; i < GSV_TILE * C; ++i) mx = fmaxf(mx, fabsf(v[i]));
+            }
 #pragma unroll
             for (int q = 0; q < kRowF4; ++q)
                 s_g[k * kSlot + lane * kRowF4 + q] =
                     make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
         }
-        if (wave_fast) {  // one power-of-two scale for the group, applied in LDS
+        if (wave_fast && !prescaled) {  // one power-of-two scale for the group, applied in LDS
 #pragma unroll
             for (int o = kWave / 2; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-            if (mx > 0.f && mx <= FLT_MAX) {
-                int e;
-                (void)frexpf(mx, &e);
-                gexp = kGradScaleExp - e;
-            }
+            gexp = grad_scale_exp(mx);
             if (gexp != 0) {
 #pragma unroll
                 for (int k = 0; k < K; ++k)
