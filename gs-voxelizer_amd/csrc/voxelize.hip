@@ -379,7 +379,12 @@ struct Moments {
 // Taking moments about the Gaussian (not the tile) keeps every sum
 // well-conditioned: h is large only where |delta| is small.
 //   kGateFree: a = exp2(sigma2 + bound), zero below the threshold by the
-//              hardware flush (bound = the gate-free offset, shift unused);
+//              hardware flush (bound = the gate-free offset, shift unused).
+//              For C == 1, along a row sigma2 + bound = S0 + P_k - p' S1 with
+//              p' = u - 3.5 = +-(k + 1/2): S0 and S1 are the form and its
+//              x-slope at the row centre, P_k = A2 p'^2 + bound is per lane, so
+//              the voxels u and 7 - u share S0 + P_k (more channels keep the
+//              plain form: the four P_k would cost them occupancy);
 //   otherwise: a = exp2(s) if |s| <= bound, s = sigma2 - shift.
 template <int C, bool kGateFree>
 __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int nz,
@@ -392,9 +397,19 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
         dxu[u] = mxl - ((float)u - 3.5f);
         dxu2[u] = dxu[u] * dxu[u];
     }
+    constexpr bool kSym = kGateFree && C == 1;
+    float P[4];
+    const float A2m = A2 * mxl, Bm = Bn * mxl, Cm = Cn * mxl;
+    if (kSym) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) P[k] = fmaf(A2, (0.5f + k) * (0.5f + k), bound);
+    }
     for (int lz = 0; lz < nz; ++lz) {
         const float dz = mzl - ((float)lz - 3.5f);
         const float Cdz = Cn * dz, Edz = En * dz;
+        // gate-free: S1 = Bn dy + K1, S0 = dy (Dn dy + L1) + K0
+        const float K1 = fmaf(2.0f, A2m, Cdz), L1 = Bm + Edz;
+        const float K0 = fmaf(dz, fmaf(Fn, dz, Cm), A2m * mxl);
         const float R0z = kGateFree ? (Fn * dz) * dz : fmaf(Fn * dz, dz, -shift);
         float Q0 = 0.f, Qx = 0.f, Qxx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
 #pragma unroll
@@ -408,13 +423,26 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                 gv[4 * q] = t4.x; gv[4 * q + 1] = t4.y; gv[4 * q + 2] = t4.z; gv[4 * q + 3] = t4.w;
             }
             const float dy = myl - ((float)ly - 3.5f);
-            const float R1 = fmaf(Bn, dy, Cdz);
-            float R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
-            if (kGateFree) R0 += bound;  // the offset enters after the small terms
+            float sv[GSV_TILE];  // kSym: the row's exponents
+            float R1 = 0.f, R0 = 0.f;
+            if (kSym) {
+                const float S1 = fmaf(Bn, dy, K1);
+                const float S0 = fmaf(dy, fmaf(Dn, dy, L1), K0);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float V = S0 + P[k];
+                    sv[4 + k] = fmaf(-(0.5f + k), S1, V);
+                    sv[3 - k] = fmaf(0.5f + k, S1, V);
+                }
+            } else {
+                R1 = fmaf(Bn, dy, Cdz);
+                R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
+                if (kGateFree) R0 += bound;  // the offset enters after the small terms
+            }
             float W0 = 0.f, W1 = 0.f, W2 = 0.f;
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
-                const float s = fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
+                const float s = kSym ? sv[u] : fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
                 float a;
                 if (kGateFree)
                     a = __builtin_amdgcn_exp2f(s);
