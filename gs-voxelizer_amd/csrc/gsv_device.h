@@ -32,6 +32,24 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t per) {
     return (b % kXcds) * per + b / kXcds;
 }
 __host__ __device__ inline int64_t xcd_per(int64_t count) { return (count + kXcds - 1) / kXcds; }
+
+// Tile order for per-tile launches: runs of 8 consecutive tiles (along x)
+// rotate over the XCDs, one run per XCD in each super-run S of 64 tiles, by
+// S + S/8 + S/64 (the higher terms keep rows whose super-run index is a
+// multiple of 8 from landing on the same XCDs).  Every XCD so gets an even
+// share of every region of the volume (clustered scenes and the volume's faces
+// included) while the tiles of a run share one L2.  Block b (dispatched to
+// XCD b % 8) takes the tile returned, which is below kRunSpan * ceil(T /
+// kRunSpan) = the grid size.
+constexpr int kRunSpan = 8 * kXcds;
+__device__ __forceinline__ int64_t xcd_runs(int64_t b) {
+    const int64_t k = b % kXcds, j = b / kXcds;
+    const int64_t S = j / 8, t = j % 8;
+    return S * kRunSpan + ((k + S + (S >> 3) + (S >> 6)) % kXcds) * 8 + t;
+}
+__host__ __device__ inline int64_t xcd_runs_grid(int64_t T) {
+    return (T + kRunSpan - 1) / kRunSpan * kRunSpan;
+}
 __host__ __device__ inline int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
 __host__ __device__ inline int64_t imax64(int64_t a, int64_t b) { return a > b ? a : b; }
 

@@ -163,12 +163,12 @@ constexpr int kRecF4 = (13 + C + 3) / 4;
 
 template <int C>
 __global__ __launch_bounds__(kWave) void k_vox_fwd(
-    int D, int H, int W, int Tx, int Ty, int64_t T, int64_t per, int n, int n_isect,
+    int D, int H, int W, int Tx, int Ty, int64_t T, int n, int n_isect,
     const int *__restrict__ ids, const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
     const float2 *__restrict__ conics, const float *__restrict__ intens, float *__restrict__ vol,
     const float *__restrict__ target, float *__restrict__ tile_loss, int8_t *__restrict__ sgn) {
     __shared__ float4 s_rec[kWave][kRecF4<C>];
-    const int64_t tile = xcd_remap(blockIdx.x, per);
+    const int64_t tile = xcd_runs(blockIdx.x);
     if (tile >= T) return;
     const int lane = threadIdx.x;
     const TileGeom tg = tile_geom((int)tile, Tx, Ty, D, H, W);
@@ -964,12 +964,11 @@ int voxelize_fwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     if (!empty && (!aligned(pos3d_radii, 16) || !aligned(conics, 8))) return GSV_ERR_INVALID_ARGUMENT;
     // an empty list still runs the kernel for the loss: every tile range is empty
     const int ni = empty ? 0 : (int)num_intersects;
-    const int64_t per = xcd_per(T);
-    const dim3 grid((unsigned)(kXcds * per)), block(kWave);
+    const dim3 grid((unsigned)xcd_runs_grid(T)), block(kWave);
     {
         KernelTimer timer(kTimedVoxFwd, s);
 #define GSV_VF(CH)                                                                                 \
-    hipLaunchKernelGGL(k_vox_fwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, T, per, n, ni, ids,      \
+    hipLaunchKernelGGL(k_vox_fwd<CH>, grid, block, 0, s, D, H, W, Tx, Ty, T, n, ni, ids,           \
                        reinterpret_cast<const int2 *>(tile_bins),                                  \
                        reinterpret_cast<const float4 *>(pos3d_radii),                              \
                        reinterpret_cast<const float2 *>(conics), intensities, volume, target,      \
