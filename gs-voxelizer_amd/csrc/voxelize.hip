@@ -173,6 +173,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
     const int lane = threadIdx.x;
     const TileGeom tg = tile_geom((int)tile, Tx, Ty, D, H, W);
     const float py = (float)(lane & 7) - 3.5f, pz = (float)(lane >> 3) - 3.5f;  // centred, tile-local
+    const float py2 = py * py, pyz = py * pz, pz2 = pz * pz;                      // exact
     int2 range = bins[tile];
     range.x = max(range.x, 0);
     range.y = min(range.y, n_isect);  // never index past the id array
@@ -216,10 +217,23 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                     const float F = -0.5f * kLog2e * c45.y;
                     float rec[4 * kRecF4<C>];
                     if (fast) {
-                        // (cx, cy, cz, A2 cx | B, C, D, E | F, Q0, Q1, Q2 | Q3, I*2^-off ...),
+                        // The form about the tile centre, in the lane's row offsets
+                        // (py, pz):  s(u) = T0 - T1 uc + A2 uc^2 + off with
+                        //   T1 = t1 - B py - C pz,
+                        //   T0 = t0 + ty py + tz pz + D py^2 + E py pz + F pz^2,
+                        // t0 = the form at the tile centre, ty/tz its y/z slopes there.
+                        // Formed in binary64 and rounded once.
+                        // (t1, -B, -C, t0 | ty, tz, D, E | F, Q0, Q1, Q2 | Q3, I*2^-off ...),
                         // Q_k = A2 * uc_k^2 + off for the four |uc| = 0.5, 1.5, 2.5, 3.5
-                        rec[0] = cx; rec[1] = cy; rec[2] = cz; rec[3] = A2 * cx;
-                        rec[4] = q1.x; rec[5] = q1.y; rec[6] = q1.z; rec[7] = q1.w;
+                        const double X = cx, Y = cy, Z = cz;
+                        const double a2 = A2, bb = q1.x, cc = q1.y, dd = q1.z, ee = q1.w, ff = F;
+                        rec[0] = (float)(2.0 * a2 * X + bb * Y + cc * Z);
+                        rec[1] = -q1.x; rec[2] = -q1.y;
+                        rec[3] = (float)(X * (a2 * X + bb * Y + cc * Z) + Y * (dd * Y + ee * Z) +
+                                         ff * Z * Z);
+                        rec[4] = (float)(-(bb * X + 2.0 * dd * Y + ee * Z));
+                        rec[5] = (float)(-(cc * X + ee * Y + 2.0 * ff * Z));
+                        rec[6] = q1.z; rec[7] = q1.w;
                         rec[8] = F;
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
@@ -258,12 +272,9 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
             if (C > 1) iw[1] = r3.z;
             if (C > 2) iw[2] = r3.w;
             if (C > 3) iw[3] = s_rec[j][kRecF4<C> - 1].x;
-            const float dy = r0.y - py, dz = r0.z - pz;
-            // X = R1 + A2 cx, T1 = R1 + 2 A2 cx, T0 = s at the row centre (no offset)
-            const float X = fmaf(r1.x, dy, fmaf(r1.y, dz, r0.w));
-            const float T1 = X + r0.w;
-            const float R0 = fmaf(fmaf(r1.z, dy, r1.w * dz), dy, (r2.x * dz) * dz);
-            const float T0 = fmaf(r0.x, X, R0);
+            const float T1 = fmaf(r0.y, py, fmaf(r0.z, pz, r0.x));
+            const float T0 =
+                fmaf(r2.x, pz2, fmaf(r1.w, pyz, fmaf(r1.z, py2, fmaf(r1.y, pz, fmaf(r1.x, py, r0.w)))));
             // s(u) = T0 - T1 uc + A2 uc^2 + off; voxels u and 7-u share uc^2
             const float V[4] = {T0 + r2.y, T0 + r2.z, T0 + r2.w, T0 + r3.x};
 #pragma unroll
