@@ -439,10 +439,13 @@ BinLayout bin_layout(int64_t cap, int64_t n_tiles) {
     return L;
 }
 
+// tiles_out (optional, 16-byte aligned, cap entries): the sorted keys, i.e. the
+// tile of each sorted pair, written by the last pass in place of a workspace
+// buffer.
 int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *tile_min,
                  const int32_t *tile_max, const int32_t *cum, int32_t D, int32_t H, int32_t W,
                  void *workspace, size_t workspace_bytes, int32_t *ids_out, int32_t *tile_bins,
-                 hipStream_t s) {
+                 int32_t *tiles_out, hipStream_t s) {
     if (n < 0 || D <= 0 || H <= 0 || W <= 0 || !tile_bins) return GSV_ERR_INVALID_ARGUMENT;
     if (cap > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
@@ -451,13 +454,14 @@ int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *
     if (cap <= 0 || n == 0) return fill_zero_u32(tile_bins, 2 * T, s);
     if (!tile_min || !tile_max || !cum || !ids_out || !workspace) return GSV_ERR_INVALID_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(ids_out) & 15) != 0) return GSV_ERR_INVALID_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(tiles_out) & 15) != 0) return GSV_ERR_INVALID_ARGUMENT;
     const BinLayout L = bin_layout(cap, T);
     if (workspace_bytes < L.total + 256) return GSV_ERR_WORKSPACE_TOO_SMALL;
     char *ws = static_cast<char *>(workspace);
     ws += (256 - (reinterpret_cast<uintptr_t>(ws) & 255)) & 255;  // 16-byte vector access
     int *ka = reinterpret_cast<int *>(ws + L.keys_a);
     int *va = reinterpret_cast<int *>(ws + L.vals_a);
-    int *kb = reinterpret_cast<int *>(ws + L.keys_b);
+    int *kb = tiles_out ? tiles_out : reinterpret_cast<int *>(ws + L.keys_b);
     int *vb = ids_out;
     int *hist = reinterpret_cast<int *>(ws + L.hist);
     int *totals = reinterpret_cast<int *>(ws + L.totals);
@@ -510,9 +514,10 @@ extern "C" int gsv_bin_workspace_bytes(int32_t n, int64_t num_intersects, int32_
 extern "C" int gsv_bin_and_sort(int32_t n, int64_t num_intersects, const int32_t *tile_min,
                                 const int32_t *tile_max, const int32_t *cum_tiles_hit, int32_t D,
                                 int32_t H, int32_t W, void *workspace, size_t workspace_bytes,
-                                int32_t *gaussian_ids_sorted, int32_t *tile_bins, void *stream) {
+                                int32_t *gaussian_ids_sorted, int32_t *tile_bins,
+                                int32_t *tiles_sorted, void *stream) {
     return bin_and_sort(n, num_intersects, nullptr, tile_min, tile_max, cum_tiles_hit, D, H, W,
-                        workspace, workspace_bytes, gaussian_ids_sorted, tile_bins,
+                        workspace, workspace_bytes, gaussian_ids_sorted, tile_bins, tiles_sorted,
                         as_stream(stream));
 }
 
@@ -522,9 +527,9 @@ extern "C" int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity,
                                              const int32_t *cum_tiles_hit, int32_t D, int32_t H,
                                              int32_t W, void *workspace, size_t workspace_bytes,
                                              int32_t *gaussian_ids_sorted, int32_t *tile_bins,
-                                             void *stream) {
+                                             int32_t *tiles_sorted, void *stream) {
     if (!num_intersects_dev) return GSV_ERR_INVALID_ARGUMENT;
     return bin_and_sort(n, capacity, num_intersects_dev, tile_min, tile_max, cum_tiles_hit, D, H,
                         W, workspace, workspace_bytes, gaussian_ids_sorted, tile_bins,
-                        as_stream(stream));
+                        tiles_sorted, as_stream(stream));
 }

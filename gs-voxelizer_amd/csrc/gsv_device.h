@@ -71,6 +71,6 @@ int fill_zero_u32(void *ptr, int64_t n_words, hipStream_t stream);
 // Exclusive / inclusive int32 scan of a device array (scan.hip; the functor
 // form and scan_workspace_bytes are in gsv_scan.h).
 int scan_i32(const int32_t *in, int32_t *out, int64_t n, bool inclusive, int64_t *total_out,
-             void *ws, size_t ws_bytes, hipStream_t stream);
+             int64_t *total_host, void *ws, size_t ws_bytes, hipStream_t stream);
 
 }  // namespace gsv

@@ -63,9 +63,20 @@ __global__ __launch_bounds__(kThreads) void k_block_sums(Load ld, int64_t n, int
     if (threadIdx.x == 0) part[blockIdx.x] = total;
 }
 
+// Writes the total to the device int64 and, when given, to pinned host memory
+// (system-scope fence, so the host sees it once the kernel has completed).
+__device__ __forceinline__ void put_total(int64_t v, int64_t *total_out, int64_t *total_host) {
+    if (total_out) *total_out = v;
+    if (total_host) {
+        *reinterpret_cast<volatile int64_t *>(total_host) = v;
+        __threadfence_system();
+    }
+}
+
 // Exclusive scan of part[0..nb) in place by one workgroup; writes the total.
 __global__ __launch_bounds__(kThreads) void k_scan_block_sums(int32_t *part, int64_t nb,
-                                                              int64_t *total_out) {
+                                                              int64_t *total_out,
+                                                              int64_t *total_host) {
     __shared__ int lds_waves[kThreads / kWave];
     int64_t carry = 0;
     for (int64_t start = 0; start < nb; start += kThreads) {
@@ -77,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void k_scan_block_sums(int32_t *part, int
         carry += total;
         __syncthreads();  // lds_waves reused by the next chunk
     }
-    if (total_out && threadIdx.x == 0) *total_out = carry;
+    if (threadIdx.x == 0) put_total(carry, total_out, total_host);
 }
 
 // st(i, exclusive prefix of element i, element i) for every i < n.  direct:
@@ -86,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void k_scan_block_sums(int32_t *part, int
 template <class Load, class Store>
 __global__ __launch_bounds__(kThreads) void k_apply(Load ld, Store st, int64_t n,
                                                     const int32_t *part, int direct,
-                                                    int64_t *total_out) {
+                                                    int64_t *total_out, int64_t *total_host) {
     __shared__ int lds_waves[kThreads / kWave];
     __shared__ long long lds_pre[kThreads / kWave];
     const int b = blockIdx.x;
@@ -119,8 +130,8 @@ __global__ __launch_bounds__(kThreads) void k_apply(Load ld, Store st, int64_t n
         if (base + k < n) st(base + k, run, v[k]);
         run += v[k];
     }
-    if (direct && total_out && b == (int)gridDim.x - 1 && threadIdx.x == 0)
-        *total_out = prefix + total;
+    if (direct && b == (int)gridDim.x - 1 && threadIdx.x == 0)
+        put_total(prefix + total, total_out, total_host);
 }
 
 }  // namespace scan_detail
@@ -133,10 +144,11 @@ inline size_t scan_workspace_bytes(int64_t n) {
 }
 
 // Prefix sum of ld(0..n) handed to st; *total_out (optional, device int64)
-// receives the sum.  Launches on `stream`; no host synchronisation.
+// and *total_host (optional, device-visible pinned host int64) receive the sum.
+// Launches on `stream`; no host synchronisation.
 template <class Load, class Store>
-int scan_run(Load ld, Store st, int64_t n, int64_t *total_out, void *ws, size_t ws_bytes,
-             hipStream_t stream) {
+int scan_run(Load ld, Store st, int64_t n, int64_t *total_out, int64_t *total_host, void *ws,
+             size_t ws_bytes, hipStream_t stream) {
     using namespace scan_detail;
     if (n < 0) return GSV_ERR_INVALID_ARGUMENT;
     if (ws_bytes < scan_workspace_bytes(n) || !ws) return GSV_ERR_WORKSPACE_TOO_SMALL;
@@ -144,7 +156,7 @@ int scan_run(Load ld, Store st, int64_t n, int64_t *total_out, void *ws, size_t 
     int32_t *part = static_cast<int32_t *>(ws);
     if (nb == 0) {
         hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(kThreads), 0, stream, part, nb,
-                           total_out);
+                           total_out, total_host);
         return check_launch();
     }
     hipLaunchKernelGGL(k_block_sums<Load>, dim3((unsigned)nb), dim3(kThreads), 0, stream, ld, n,
@@ -153,11 +165,11 @@ int scan_run(Load ld, Store st, int64_t n, int64_t *total_out, void *ws, size_t 
     const int direct = nb <= kDirectBlocks ? 1 : 0;
     if (!direct) {
         hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(kThreads), 0, stream, part, nb,
-                           total_out);
+                           total_out, total_host);
         if (int st_ = check_launch()) return st_;
     }
     hipLaunchKernelGGL((k_apply<Load, Store>), dim3((unsigned)nb), dim3(kThreads), 0, stream, ld,
-                       st, n, part, direct, total_out);
+                       st, n, part, direct, total_out, total_host);
     return check_launch();
 }
 

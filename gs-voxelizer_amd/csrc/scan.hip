@@ -85,10 +85,10 @@ int fill_zero_u32(void *ptr, int64_t n_words, hipStream_t stream) {
 }
 
 int scan_i32(const int32_t *in, int32_t *out, int64_t n, bool inclusive, int64_t *total_out,
-             void *ws, size_t ws_bytes, hipStream_t stream) {
+             int64_t *total_host, void *ws, size_t ws_bytes, hipStream_t stream) {
     if (n > 0 && (!in || !out)) return GSV_ERR_INVALID_ARGUMENT;
-    return scan_run(LoadI32{in}, StoreI32{out, inclusive ? 1 : 0}, n, total_out, ws, ws_bytes,
-                    stream);
+    return scan_run(LoadI32{in}, StoreI32{out, inclusive ? 1 : 0}, n, total_out, total_host, ws,
+                    ws_bytes, stream);
 }
 
 }  // namespace gsv
@@ -162,10 +162,22 @@ extern "C" int gsv_scan_workspace_bytes(int64_t n, size_t *bytes) {
 }
 
 extern "C" int gsv_cumsum_tiles_hit(int32_t n, const int32_t *num_tiles_hit,
-                                    int32_t *cum_tiles_hit, int64_t *total_out, void *workspace,
-                                    size_t workspace_bytes, void *stream) {
+                                    int32_t *cum_tiles_hit, int64_t *total_out,
+                                    int64_t *total_host, void *workspace, size_t workspace_bytes,
+                                    void *stream) {
     if (n < 0) return GSV_ERR_INVALID_ARGUMENT;
     if (n > 0 && (!num_tiles_hit || !cum_tiles_hit)) return GSV_ERR_INVALID_ARGUMENT;
-    return scan_i32(num_tiles_hit, cum_tiles_hit, n, true, total_out, workspace, workspace_bytes,
-                    as_stream(stream));
+    int64_t *host_dev = nullptr;  // the kernels' address of the pinned host int64
+    if (total_host) {
+        void *p = nullptr;
+        const hipError_t e = hipHostGetDevicePointer(&p, total_host, 0);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();  // leave no error behind for the next launch check
+            (void)record_hip_error(e);
+            return GSV_ERR_INVALID_ARGUMENT;  // not pinned, device-visible host memory
+        }
+        host_dev = static_cast<int64_t *>(p);
+    }
+    return scan_i32(num_tiles_hit, cum_tiles_hit, n, true, total_out, host_dev, workspace,
+                    workspace_bytes, as_stream(stream));
 }

@@ -131,6 +131,10 @@ __device__ __forceinline__ bool may_touch(float mx, float my, float mz, float a,
     return !miss;  // NaN anywhere -> comparisons false -> keep
 }
 
+__host__ __device__ inline bool aligned_to(const void *p, uintptr_t a) {
+    return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
 struct TileGeom {
     int x0, y0, z0;
     float xlo, xhi, ylo, yhi, zlo, zhi;  // voxel-centre box of the tile's inside voxels
@@ -315,23 +319,65 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
         const int64_t off = (((int64_t)z * H + y) * W + tg.x0) * C;
         float *o = vol + off;
         const int nx = min(GSV_TILE, W - tg.x0);
+        constexpr int kRowF4 = 2 * C;  // float4s in a full row of 8 voxels
+        if (nx == GSV_TILE && aligned_to(o, 16) &&
+            (target == nullptr || (aligned_to(target + off, 16) && aligned_to(sgn + off, 8)))) {
+            // whole row, vector accesses: 2C float4 stores, and for the fused
+            // L1 2C float4 loads and C 8-byte stores of the sign bytes
+            float v[GSV_TILE * C];
 #pragma unroll
-        for (int u = 0; u < GSV_TILE; ++u)
-            if (u < nx)
+            for (int u = 0; u < GSV_TILE; ++u)
 #pragma unroll
-                for (int c = 0; c < C; ++c) o[u * C + c] = acc[u][c];
-        if (target != nullptr) {
-            const float *tt = target + off;
-            int8_t *sg = sgn + off;
+                for (int c = 0; c < C; ++c) v[u * C + c] = acc[u][c];
+            float4 t4[kRowF4];
+            if (target != nullptr) {
+#pragma unroll
+                for (int q = 0; q < kRowF4; ++q)
+                    t4[q] = reinterpret_cast<const float4 *>(target + off)[q];
+            }
+#pragma unroll
+            for (int q = 0; q < kRowF4; ++q)
+                reinterpret_cast<float4 *>(o)[q] =
+                    make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            if (target != nullptr) {
+                uint32_t words[kRowF4];
+#pragma unroll
+                for (int q = 0; q < kRowF4; ++q) {
+                    const float tq[4] = {t4[q].x, t4[q].y, t4[q].z, t4[q].w};
+                    uint32_t wd = 0;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const float d = v[4 * q + b] - tq[b];
+                        lsum += fabsf(d);
+                        const int8_t sb = d > 0.f ? 1 : (d < 0.f ? -1 : (d == 0.f ? 0 : kSgnNaN));
+                        wd |= (uint32_t)(uint8_t)sb << (8 * b);
+                    }
+                    words[q] = wd;
+                }
+#pragma unroll
+                for (int q = 0; q < C; ++q)
+                    reinterpret_cast<uint2 *>(sgn + off)[q] = make_uint2(words[2 * q], words[2 * q + 1]);
+            }
+        } else {  // a partial edge row, or unaligned buffers: element by element
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u)
                 if (u < nx)
 #pragma unroll
-                    for (int c = 0; c < C; ++c) {
-                        const float d = acc[u][c] - tt[u * C + c];
-                        lsum += fabsf(d);
-                        sg[u * C + c] = d > 0.f ? 1 : (d < 0.f ? -1 : (d == 0.f ? 0 : kSgnNaN));
-                    }
+                    for (int c = 0; c < C; ++c) o[u * C + c] = acc[u][c];
+            if (target != nullptr) {
+                const float *tt = target + off;
+                int8_t *sg = sgn + off;
+#pragma unroll
+                for (int u = 0; u < GSV_TILE; ++u)
+                    if (u < nx)
+#pragma unroll
+                        for (int c = 0; c < C; ++c) {
+                            const float d = acc[u][c] - tt[u * C + c];
+                            lsum += fabsf(d);
+                            sg[u * C + c] =
+                                d > 0.f ? 1 : (d < 0.f ? -1 : (d == 0.f ? 0 : kSgnNaN));
+                        }
+            }
         }
     }
     if (target != nullptr) {  // fixed-order wave sum, one partial per tile
@@ -366,12 +412,10 @@ __global__ __launch_bounds__(kFinishThreads) void k_loss_finish(const float *__r
 // --------------------------------------------------------------- backward --
 
 // pair_tiles[p] = tile of sorted pair p: one wave per tile writes its range.
-// Also zeroes the count of backward waves left for k_vox_bwd_rest.
+// Only needed when the caller has not kept the binning's sorted keys.
 __global__ __launch_bounds__(kWave) void k_pair_tiles(const int2 *__restrict__ bins, int n_isect,
-                                                      int *__restrict__ pair_tiles,
-                                                      int *__restrict__ rest_count) {
+                                                      int *__restrict__ pair_tiles) {
     const int t = blockIdx.x;
-    if (t == 0 && threadIdx.x == 0) *rest_count = 0;
     const int2 r = bins[t];
     const int e = min(r.y, n_isect);
     for (int q = max(r.x, 0) + (int)threadIdx.x; q < e; q += kWave) pair_tiles[q] = t;
@@ -519,7 +563,6 @@ struct BwdArgs {
     float *dpos, *dconic, *dint;
     const int *tile_min, *tile_max, *cum;
     float *partial;
-    int *rest_count, *rest_waves;  // waves spanning more than K tiles
 };
 
 // One backward wave's view: lane = one of 64 consecutive (tile, Gaussian)
@@ -826,7 +869,7 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
 // One wave per 64 consecutive (tile, Gaussian) pairs of the sorted list, lane
 // = pair, so no lane idles except in the last wave.  The wave stages the
 // first K tiles its pairs span (lane = row; each lane reads its own tile's
-// rows); a wave whose pairs span more tiles lists itself for k_vox_bwd_rest.
+// rows); the pairs of further tiles are left to k_vox_bwd_rest.
 template <int C, int K>
 __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
     __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
@@ -837,7 +880,6 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
     uint64_t starts;
     int nslots;
     if (!bwd_slots(a, p0, L, starts, nslots)) return;
-    if (nslots > K && threadIdx.x == 0) a.rest_waves[atomicAdd(a.rest_count, 1)] = (int)wv;
     bwd_gaussian(a, p0, L);
     // one wave-uniform choice: gate-free unless a live lane needs the exact gate
     const bool wave_fast = __all(!L.live || L.fast);
@@ -846,18 +888,24 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
     bwd_group<C, K>(a, L, starts, 0, wave_fast, any_live, s_g);
 }
 
-// The pairs of the listed waves (those spanning more than K tiles), in groups
-// of K tiles after the first.  A fixed grid walks the list; every wave ends
-// when the list does.
-constexpr int kRestBlocks = 512;
-
+// The pairs that k_vox_bwd left: those of the waves spanning more than K tiles,
+// in groups of K tiles after the first.  Block b checks the waves 64 b ..
+// 64 b + 63: the tiles of a wave's first and last pair come from the sorted
+// pair -> tile map, and a wave whose tiles lie within K consecutive ids spans
+// at most K of them.  The others (rare) are counted exactly and processed.
 template <int C, int K>
-__global__ __launch_bounds__(kWave) void k_vox_bwd_rest(BwdArgs a) {
+__global__ __launch_bounds__(kWave) void k_vox_bwd_rest(BwdArgs a, int64_t waves) {
     __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
-    const int count = *a.rest_count;
-    for (int i = blockIdx.x; i < count; i += gridDim.x) {
-        const int64_t p0 = (int64_t)a.rest_waves[i] * kWave;
-        if (p0 < 0 || p0 >= a.n_isect) continue;
+    const int64_t w = (int64_t)blockIdx.x * kWave + threadIdx.x;
+    bool maybe = false;
+    if (w < waves) {
+        const int64_t p0 = w * kWave;
+        const int64_t p1 = min<int64_t>(p0 + kWave, a.n_isect) - 1;
+        const int t0 = a.pair_tiles[p0], t1 = a.pair_tiles[p1];
+        maybe = !(t0 >= 0 && t1 < a.T && t1 >= t0 && t1 - t0 < K);
+    }
+    for (uint64_t m = __ballot(maybe); m; m &= m - 1) {
+        const int64_t p0 = ((int64_t)blockIdx.x * kWave + __builtin_ctzll(m)) * kWave;
         BwdLane<C> L;
         uint64_t starts;
         int nslots;
@@ -929,18 +977,17 @@ __global__ __launch_bounds__(kReduceThreads) void k_pair_reduce(
 }
 
 struct BwdLayout {
-    size_t tiles, rest, partial, end;
+    size_t tiles, partial, end;
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-// pair -> tile map (n_isect ints), the count and list of backward waves left
-// for k_vox_bwd_rest, then the per-pair partials in pairs mode.
+// pair -> tile map (n_isect ints; unused when the caller passes the binning's
+// sorted keys), then the per-pair partials in pairs mode.
 BwdLayout bwd_layout(int64_t n_isect, int channels, bool pairs) {
     BwdLayout L{};
     size_t off = 0;
     L.tiles = off; off += align256((size_t)imax64(n_isect, 1) * 4);
-    L.rest = off; off += align256(((size_t)(n_isect + kWave - 1) / kWave + 1) * 4);  // count, list
     L.partial = off;
     if (pairs) off += align256((size_t)n_isect * (9 + channels) * 4);
     L.end = off;
@@ -1009,7 +1056,8 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
                       const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
                       const float *intensities, const float *vol_grad, const int8_t *l1_sgn,
                       const float *l1_grad, const int32_t *tile_min,
-                      const int32_t *tile_max, const int32_t *cum_tiles_hit, float *dpos3d_radii,
+                      const int32_t *tile_max, const int32_t *cum_tiles_hit,
+                      const int32_t *tiles_sorted, float *dpos3d_radii,
                       float *dconics, float *dintensities, int32_t variant, void *workspace,
                       size_t workspace_bytes, hipStream_t s) {
     if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
@@ -1038,13 +1086,16 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     const BwdLayout L = bwd_layout(num_intersects, channels, pairs);
     if (!workspace || workspace_bytes < L.end) return GSV_ERR_WORKSPACE_TOO_SMALL;
     char *ws = static_cast<char *>(workspace);
-    int *pair_tiles = reinterpret_cast<int *>(ws + L.tiles);
-    int *rest = reinterpret_cast<int *>(ws + L.rest);
+    const int *pair_tiles = tiles_sorted;
     float *partial = pairs ? reinterpret_cast<float *>(ws + L.partial) : nullptr;
     const int ni = (int)num_intersects;
-    hipLaunchKernelGGL(k_pair_tiles, dim3((unsigned)T), dim3(kWave), 0, s,
-                       reinterpret_cast<const int2 *>(tile_bins), ni, pair_tiles, rest);
-    if (int st = check_launch()) return st;
+    if (!pair_tiles) {  // rebuild the pair -> tile map from the tile ranges
+        int *own = reinterpret_cast<int *>(ws + L.tiles);
+        hipLaunchKernelGGL(k_pair_tiles, dim3((unsigned)T), dim3(kWave), 0, s,
+                           reinterpret_cast<const int2 *>(tile_bins), ni, own);
+        if (int st = check_launch()) return st;
+        pair_tiles = own;
+    }
     const int64_t waves = (num_intersects + kWave - 1) / kWave;
     const int64_t per = xcd_per(waves);
     const dim3 grid((unsigned)(kXcds * per)), block(kWave);
@@ -1060,15 +1111,14 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     args.dpos = dpos3d_radii; args.dconic = dconics; args.dint = dintensities;
     args.tile_min = tile_min; args.tile_max = tile_max; args.cum = cum_tiles_hit;
     args.partial = partial;
-    args.rest_count = rest;
-    args.rest_waves = rest + 1;
 #define GSV_VB(CH)                                                                                  \
     {                                                                                               \
         KernelTimer timer(kTimedVoxBwd, s);                                                         \
         hipLaunchKernelGGL((k_vox_bwd<CH, kStageTiles<CH>>), grid, block, 0, s, args);             \
         if (int st = check_launch()) return st;                                                     \
-        hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTiles<CH>>), dim3(kRestBlocks), block, 0, s,  \
-                           args);                                                                   \
+        hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTiles<CH>>),                                  \
+                           dim3((unsigned)((waves + kWave - 1) / kWave)), block, 0, s, args,        \
+                           waves);                                                                  \
     }                                                                                               \
     if (int st = check_launch()) return st;                                                         \
     if (pairs) {                                                                                    \
@@ -1142,12 +1192,12 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
                                 const float *conics, const float *intensities,
                                 const float *vol_grad, const int32_t *tile_min,
                                 const int32_t *tile_max, const int32_t *cum_tiles_hit,
-                                float *dpos3d_radii, float *dconics, float *dintensities,
-                                int32_t variant, void *workspace, size_t workspace_bytes,
-                                void *stream) {
+                                const int32_t *tiles_sorted, float *dpos3d_radii, float *dconics,
+                                float *dintensities, int32_t variant, void *workspace,
+                                size_t workspace_bytes, void *stream) {
     return voxelize_bwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
                              pos3d_radii, conics, intensities, vol_grad, nullptr, nullptr,
-                             tile_min, tile_max, cum_tiles_hit, dpos3d_radii, dconics,
+                             tile_min, tile_max, cum_tiles_hit, tiles_sorted, dpos3d_radii, dconics,
                              dintensities, variant, workspace, workspace_bytes, as_stream(stream));
 }
 
@@ -1158,12 +1208,12 @@ extern "C" int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t chan
                                    const int8_t *sign, const float *grad_loss,
                                    const float *vol_grad, const int32_t *tile_min,
                                    const int32_t *tile_max, const int32_t *cum_tiles_hit,
-                                   float *dpos3d_radii, float *dconics, float *dintensities,
-                                   int32_t variant, void *workspace, size_t workspace_bytes,
-                                   void *stream) {
+                                   const int32_t *tiles_sorted, float *dpos3d_radii,
+                                   float *dconics, float *dintensities, int32_t variant,
+                                   void *workspace, size_t workspace_bytes, void *stream) {
     if (!sign || !grad_loss) return GSV_ERR_INVALID_ARGUMENT;
     return voxelize_bwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
                              pos3d_radii, conics, intensities, vol_grad, sign, grad_loss,
-                             tile_min, tile_max, cum_tiles_hit, dpos3d_radii, dconics,
+                             tile_min, tile_max, cum_tiles_hit, tiles_sorted, dpos3d_radii, dconics,
                              dintensities, variant, workspace, workspace_bytes, as_stream(stream));
 }

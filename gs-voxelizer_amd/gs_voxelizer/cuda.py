@@ -123,11 +123,19 @@ def optim_to_render_backward(num_gaussians: int, pos3d, scale3d, quat, vol_size_
     return dpos, dscale, dquat
 
 
-def cumsum_tiles_hit(num_tiles_hit):
+def cumsum_tiles_hit(num_tiles_hit, total_host=None):
     """Inclusive int32 prefix sum of num_tiles_hit plus its total as a (1,) int64
-    device tensor (one scalar to read back instead of the whole array)."""
+    device tensor (one scalar to read back instead of the whole array).
+
+    total_host: optional (1,) int64 pinned CPU tensor (pin_memory=True) that the
+    scan kernel writes the total into as well; it holds the count once an event
+    recorded after this call has completed, without a device-to-host copy."""
     _check_input(num_tiles_hit, "num_tiles_hit")
     _check_dtype(num_tiles_hit, "num_tiles_hit", torch.int32)
+    if total_host is not None:
+        if (total_host.is_cuda or not total_host.is_pinned() or total_host.dtype != torch.int64
+                or total_host.numel() != 1):
+            raise RuntimeError("total_host must be a pinned (1,) int64 CPU tensor")
     n = num_tiles_hit.numel()
     dev = num_tiles_hit.device
     cum = torch.empty((n,), device=dev, dtype=torch.int32)
@@ -136,14 +144,17 @@ def cumsum_tiles_hit(num_tiles_hit):
     _call("scan_workspace_bytes", n, ctypes.byref(nbytes))
     ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
-        _call("cumsum_tiles_hit", n, _ptr(num_tiles_hit), _ptr(cum), _ptr(total), _ptr(ws),
+        _call("cumsum_tiles_hit", n, _ptr(num_tiles_hit), _ptr(cum), _ptr(total),
+              _ptr(total_host) if total_host is not None else ctypes.c_void_p(0), _ptr(ws),
               nbytes.value, _stream(dev))
     return cum, total
 
 
 def bin_and_sort_gaussians(num_gaussians: int, num_intersects: int, tile_min, tile_max,
-                           cum_tiles_hit, vol_size):
-    """bindings.cu:259-360. Returns (gaussian_ids_sorted (I,), tile_bins (T,2))."""
+                           cum_tiles_hit, vol_size, return_tiles: bool = False):
+    """bindings.cu:259-360. Returns (gaussian_ids_sorted (I,), tile_bins (T,2)), plus
+    the tile id of each sorted pair (I,) when return_tiles (the sort's keys, which
+    voxelize_backward* take as tiles_sorted)."""
     for t, w in ((tile_min, "tile_min"), (tile_max, "tile_max"), (cum_tiles_hit, "cum_tiles_hit")):
         _check_input(t, w)
         _check_dtype(t, w, torch.int32)
@@ -155,23 +166,27 @@ def bin_and_sort_gaussians(num_gaussians: int, num_intersects: int, tile_min, ti
     i32 = dict(device=dev, dtype=torch.int32)
     tile_bins = torch.empty((T, 2), **i32)
     ids = torch.empty((max(I, 0),), **i32)
+    tiles = torch.empty((max(I, 0),), **i32) if return_tiles else None
     nbytes = ctypes.c_size_t(0)
     _call("bin_workspace_bytes", n, max(I, 0), D, H, W, ctypes.byref(nbytes))
     ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
         _call("bin_and_sort", n, I, _ptr(tile_min), _ptr(tile_max), _ptr(cum_tiles_hit), D, H, W,
-              _ptr(ws), nbytes.value, _ptr(ids), _ptr(tile_bins), _stream(dev))
-    return ids, tile_bins
+              _ptr(ws), nbytes.value, _ptr(ids), _ptr(tile_bins),
+              _ptr(tiles) if tiles is not None else ctypes.c_void_p(0), _stream(dev))
+    return (ids, tile_bins, tiles) if return_tiles else (ids, tile_bins)
 
 
 def bin_and_sort_gaussians_device_count(num_gaussians: int, capacity: int, num_intersects_dev,
-                                        tile_min, tile_max, cum_tiles_hit, vol_size):
+                                        tile_min, tile_max, cum_tiles_hit, vol_size,
+                                        return_tiles: bool = False):
     """Binning without the host read of the pair count (voxelize.py:87-88).
 
     num_intersects_dev is a (1,) int64 device tensor, e.g. the total returned by
     cumsum_tiles_hit.  Returns (gaussian_ids_sorted (capacity,), tile_bins (T,2)):
     the first min(count, capacity) ids are sorted, and the result is complete only
     when count <= capacity, which the caller checks once the count is on the host.
+    With return_tiles the tile id of each sorted pair (capacity,) follows.
     """
     for t, w in ((tile_min, "tile_min"), (tile_max, "tile_max"), (cum_tiles_hit, "cum_tiles_hit"),
                  (num_intersects_dev, "num_intersects_dev")):
@@ -186,14 +201,16 @@ def bin_and_sort_gaussians_device_count(num_gaussians: int, capacity: int, num_i
     i32 = dict(device=dev, dtype=torch.int32)
     tile_bins = torch.empty((Tx * Ty * Tz, 2), **i32)
     ids = torch.empty((cap,), **i32)
+    tiles = torch.empty((cap,), **i32) if return_tiles else None
     nbytes = ctypes.c_size_t(0)
     _call("bin_workspace_bytes", n, cap, D, H, W, ctypes.byref(nbytes))
     ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
         _call("bin_and_sort_device_count", n, cap, _ptr(num_intersects_dev), _ptr(tile_min),
               _ptr(tile_max), _ptr(cum_tiles_hit), D, H, W, _ptr(ws), nbytes.value, _ptr(ids),
-              _ptr(tile_bins), _stream(dev))
-    return ids, tile_bins
+              _ptr(tile_bins), _ptr(tiles) if tiles is not None else ctypes.c_void_p(0),
+              _stream(dev))
+    return (ids, tile_bins, tiles) if return_tiles else (ids, tile_bins)
 
 
 def _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities):
@@ -269,8 +286,9 @@ def voxelize_forward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
 
 def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                        intensities, vol_grad_in, tile_min=None, tile_max=None,
-                       cum_tiles_hit=None, l1=None):
-    """l1 = (sign, grad_loss): the fused L1 source, with vol_grad_in optional."""
+                       cum_tiles_hit=None, l1=None, tiles_sorted=None):
+    """l1 = (sign, grad_loss): the fused L1 source, with vol_grad_in optional.
+    tiles_sorted: the binning's tile id per sorted pair (return_tiles), optional."""
     _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
     given = [t is not None for t in (tile_min, tile_max, cum_tiles_hit)]
     if any(given) and not all(given):
@@ -299,6 +317,11 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
     n = pos3d.size(0)
     dev = pos3d.device
     I = gaussian_ids_sorted.numel()
+    if tiles_sorted is not None:
+        _check_input(tiles_sorted, "tiles_sorted")
+        _check_dtype(tiles_sorted, "tiles_sorted", torch.int32)
+        if tiles_sorted.numel() < I:
+            raise RuntimeError("tiles_sorted must hold a tile id for every sorted pair")
     Tx, Ty, Tz = _tiles(vol_size)
     if I > 0 and tile_bins.numel() < 2 * Tx * Ty * Tz:
         raise RuntimeError("tile_bins does not cover the volume's tile grid")
@@ -314,47 +337,52 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
     boxes = ((_ptr(tile_min), _ptr(tile_max), _ptr(cum_tiles_hit)) if deterministic
              else (null, null, null))
     vg = _ptr(vol_grad_in) if vol_grad_in is not None else null
+    ts = _ptr(tiles_sorted) if tiles_sorted is not None else null
     with torch.cuda.device(dev):
         if l1 is None:
             _call("voxelize_bwd", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted),
-                  _ptr(tile_bins), _ptr(pos3d), _ptr(conics), _ptr(intensities), vg, *boxes,
+                  _ptr(tile_bins), _ptr(pos3d), _ptr(conics), _ptr(intensities), vg, *boxes, ts,
                   _ptr(dpos), _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value,
                   _stream(dev))
         else:
             _call("voxelize_bwd_l1", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted),
                   _ptr(tile_bins), _ptr(pos3d), _ptr(conics), _ptr(intensities), _ptr(sign),
-                  _ptr(grad_loss), vg, *boxes, _ptr(dpos), _ptr(dconics), _ptr(dint), variant,
-                  _ptr(ws), nbytes.value, _stream(dev))
+                  _ptr(grad_loss), vg, *boxes, ts, _ptr(dpos), _ptr(dconics), _ptr(dint),
+                  variant, _ptr(ws), nbytes.value, _stream(dev))
     return dpos, dconics, dint
 
 
 def voxelize_backward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
                          sign, grad_loss, vol_grad_in=None, tile_min=None, tile_max=None,
-                         cum_tiles_hit=None, per_gaussian=True):
+                         cum_tiles_hit=None, per_gaussian=True, tiles_sorted=None):
     """Backward of voxelize_forward_l1: dL/dvolume = sign * grad_loss / numel (+
     vol_grad_in, the volume's gradient from other uses, when given), never
     materialised.  Returns (dpos3d_radii, dconics, dintensities)."""
     return _voxelize_backward(1 if per_gaussian else 0, vol_size, gaussian_ids_sorted, tile_bins,
                               pos3d, conics, intensities, vol_grad_in, tile_min, tile_max,
-                              cum_tiles_hit, l1=(sign, grad_loss))
+                              cum_tiles_hit, l1=(sign, grad_loss), tiles_sorted=tiles_sorted)
 
 
 def voxelize_backward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
-                      vol_grad_in, tile_min=None, tile_max=None, cum_tiles_hit=None):
+                      vol_grad_in, tile_min=None, tile_max=None, cum_tiles_hit=None,
+                      tiles_sorted=None):
     """bindings.cu:459-584 (per-voxel variant). Returns (dpos3d_radii, dconics, dintensities).
 
     The optional tile_min / tile_max / cum_tiles_hit (the projection's tile boxes
     and the prefix sum used for binning) select the atomic-free, bitwise
     reproducible reduction; without them float atomics are used, as in the
-    reference."""
+    reference.  tiles_sorted (bin_and_sort_gaussians(..., return_tiles=True)) saves
+    rebuilding the tile of each pair."""
     return _voxelize_backward(0, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
-                              intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit)
+                              intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit,
+                              tiles_sorted=tiles_sorted)
 
 
 def voxelize_backward_per_gaussian(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                                    intensities, vol_grad_in, tile_min=None, tile_max=None,
-                                   cum_tiles_hit=None):
+                                   cum_tiles_hit=None, tiles_sorted=None):
     """bindings.cu:586-781 (per-Gaussian variant). Returns (dpos3d_radii, dconics, dintensities).
     Optional arguments as in voxelize_backward."""
     return _voxelize_backward(1, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
-                              intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit)
+                              intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit,
+                              tiles_sorted=tiles_sorted)

@@ -8,10 +8,10 @@ The reference reads the intersection count back to the host before binning
 (voxelize.py:87-88), which idles the GPU for a round trip every forward.  Here
 the first forward on a device does the same and records a capacity; later
 forwards launch binning and the forward kernel at that capacity with the count
-left on the device, copy the count to pinned host memory meanwhile, and check
-it after the launches.  A count above the capacity (the scene grew) reruns
-binning and the forward with the exact count and raises the capacity; results
-are identical either way.  GSV_SYNC_COUNT=1 restores the reference's host read.
+left on the device (the prefix-sum kernel also writes it into pinned host
+memory, so no copy is enqueued), and check it after the launches.  A count
+above the capacity (the scene grew) reruns binning and the forward with the
+exact count and raises the capacity; results are identical either way.  GSV_SYNC_COUNT=1 restores the reference's host read.
 """
 import os
 from typing import Tuple
@@ -21,8 +21,6 @@ from torch import Tensor
 from torch.autograd import Function
 
 import gs_voxelizer.cuda as _C
-
-from .bin_and_sort_gaussians import bin_and_sort_gaussians
 
 _INT32_MAX = 2**31 - 1
 _capacity = {}  # device index -> intersection capacity of the speculative path
@@ -34,6 +32,25 @@ def _grow(count: int) -> int:
 
 def _speculate() -> bool:
     return os.environ.get("GSV_SYNC_COUNT", "0") != "1"
+
+
+_SPIN_READS = 1 << 21  # reads of the pinned count before falling back to a device sync
+
+
+def _await_count(host: Tensor, dev: torch.device) -> int:
+    """The pair count the prefix-sum kernel writes into pinned memory (-1 until
+    then).  Polling it, rather than recording an event behind the kernel, keeps
+    an extra completion packet out of the queue; the kernels queued after the
+    scan keep the GPU busy meanwhile."""
+    for _ in range(_SPIN_READS):
+        v = int(host[0])
+        if v >= 0:
+            return v
+    torch.cuda.synchronize(dev)
+    v = int(host[0])
+    if v < 0:
+        raise RuntimeError("gs_voxelizer: the intersection count was not written")
+    return v
 
 
 def voxelize_gaussians(
@@ -75,29 +92,31 @@ def voxelize_gaussians(
 
 def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd):
     """Prefix sum, binning and `fwd(gaussian_ids_sorted, tile_bins)` for a
-    non-empty Gaussian set.  Returns (num_intersects, ids, tile_bins, cum,
-    fwd's result); ids is None when there are no intersections."""
-    cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous())
-    dev = cum_tiles_hit.device
+    non-empty Gaussian set.  Returns (num_intersects, ids, tile_bins, tiles, cum,
+    fwd's result), tiles being the tile id of each sorted pair (for the
+    backward); ids and tiles are None when there are no intersections."""
+    dev = num_tiles_hit.device
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     cap = _capacity.get(key) if _speculate() else None
     if cap is not None:
-        # launch at the recorded capacity; the count travels meanwhile
-        host = torch.empty((1,), dtype=torch.int64, pin_memory=True)
-        host.copy_(total, non_blocking=True)
-        copied = torch.cuda.Event()
-        copied.record()
-        ids_cap, tile_bins = _C.bin_and_sort_gaussians_device_count(
-            num_gaussians, cap, total, tile_min, tile_max, cum_tiles_hit, vol_size_voxel)
+        # launch at the recorded capacity; the scan writes the count into pinned
+        # memory meanwhile
+        host = torch.empty((1,), dtype=torch.int64, pin_memory=True).fill_(-1)
+        cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous(), total_host=host)
+        ids_cap, tile_bins, tiles_cap = _C.bin_and_sort_gaussians_device_count(
+            num_gaussians, cap, total, tile_min, tile_max, cum_tiles_hit, vol_size_voxel,
+            return_tiles=True)
         result = fwd(ids_cap, tile_bins)
-        copied.synchronize()  # the queued kernels keep the GPU busy meanwhile
-        num_intersects = int(host[0])
+        num_intersects = _await_count(host, dev)
         if num_intersects <= cap:
             if num_intersects < cap // 4:
                 _capacity[key] = _grow(num_intersects)
-            ids = ids_cap[:num_intersects] if num_intersects > 0 else None
-            return num_intersects, ids, tile_bins, cum_tiles_hit, result
+            if num_intersects < 1:
+                return 0, None, tile_bins, None, cum_tiles_hit, result
+            return (num_intersects, ids_cap[:num_intersects], tile_bins,
+                    tiles_cap[:num_intersects], cum_tiles_hit, result)
     else:
+        cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous())
         num_intersects = int(total.item())
     if num_intersects > _INT32_MAX:
         raise RuntimeError(
@@ -105,11 +124,12 @@ def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tile
     if _speculate():
         _capacity[key] = _grow(num_intersects)
     if num_intersects < 1:
-        return 0, None, None, cum_tiles_hit, None
+        return 0, None, None, None, cum_tiles_hit, None
     # first call on the device, host read requested, or the capacity overflowed
-    ids, tile_bins = bin_and_sort_gaussians(num_gaussians, num_intersects, tile_min, tile_max,
-                                            cum_tiles_hit, vol_size_voxel)
-    return num_intersects, ids, tile_bins, cum_tiles_hit, fwd(ids, tile_bins)
+    ids, tile_bins, tiles = _C.bin_and_sort_gaussians(
+        num_gaussians, num_intersects, tile_min.contiguous(), tile_max.contiguous(),
+        cum_tiles_hit, vol_size_voxel, return_tiles=True)
+    return num_intersects, ids, tile_bins, tiles, cum_tiles_hit, fwd(ids, tile_bins)
 
 
 class _VoxelizeGaussians(Function):
@@ -130,11 +150,12 @@ class _VoxelizeGaussians(Function):
         if num_gaussians > 0:
             fwd = lambda ids, bins: _C.voxelize_forward(vol_size_voxel, ids, bins, pos3d_radii,
                                                         conics, intensities)
-            I, gaussian_ids_sorted, tile_bins, cum_tiles_hit, out = _bin_and_forward(
+            I, gaussian_ids_sorted, tile_bins, tiles, cum_tiles_hit, out = _bin_and_forward(
                 num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd)
             ctx.num_intersects = I
-            # the backward reduces per-pair partials in duplication order (no atomics)
-            boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit)
+            # the backward reduces per-pair partials in duplication order (no
+            # atomics) and takes each sorted pair's tile from the binning
+            boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit, tiles)
         if ctx.num_intersects < 1:
             out = torch.zeros(D, H, W, C, device=dev, dtype=pos3d_radii.dtype)
             gaussian_ids_sorted = torch.zeros(0, 1, device=dev, dtype=torch.int32)
@@ -150,7 +171,7 @@ class _VoxelizeGaussians(Function):
         vol_size_voxel = ctx.vol_size_voxel
         saved = ctx.saved_tensors
         pos3d_radii, conics, intensities, gaussian_ids_sorted, tile_bins = saved[:5]
-        boxes = saved[5:]
+        boxes, tiles = saved[5:8], (saved[8] if len(saved) > 8 else None)
         if ctx.num_intersects < 1 or vol_grad is None:
             pos3d_grad = torch.zeros_like(pos3d_radii)
             conics_grad = torch.zeros_like(conics)
@@ -160,7 +181,7 @@ class _VoxelizeGaussians(Function):
                   else _C.voxelize_backward)
             pos3d_grad, conics_grad, intensities_grad = fn(
                 vol_size_voxel, gaussian_ids_sorted, tile_bins, pos3d_radii, conics, intensities,
-                vol_grad.contiguous(), *boxes)
+                vol_grad.contiguous(), *boxes, tiles_sorted=tiles)
         return pos3d_grad, conics_grad, intensities_grad, None, None, None, None, None
 
 
@@ -216,10 +237,10 @@ class _VoxelizeL1(Function):
         boxes = ()
         ctx.num_intersects = 0
         if num_gaussians > 0:
-            I, ids, tile_bins, cum_tiles_hit, res = _bin_and_forward(
+            I, ids, tile_bins, tiles, cum_tiles_hit, res = _bin_and_forward(
                 num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd)
             ctx.num_intersects = I
-            boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit)
+            boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit, tiles)
         if ctx.num_intersects < 1:
             # no Gaussian touches the volume: it is zero, the loss mean(|target|)
             empty_ids = torch.zeros(0, device=dev, dtype=torch.int32)
@@ -236,7 +257,7 @@ class _VoxelizeL1(Function):
     def backward(ctx, grad_loss, grad_volume):
         saved = ctx.saved_tensors
         pos3d_radii, conics, intensities, ids, tile_bins, sign = saved[:6]
-        boxes = saved[6:]
+        boxes, tiles = saved[6:9], (saved[9] if len(saved) > 9 else None)
         if ctx.num_intersects < 1 or (grad_loss is None and grad_volume is None):
             z = (torch.zeros_like(pos3d_radii), torch.zeros_like(conics),
                  torch.zeros_like(intensities))
@@ -247,5 +268,5 @@ class _VoxelizeL1(Function):
                 ctx.vol_size_voxel, ids, tile_bins, pos3d_radii, conics, intensities, sign,
                 grad_loss.contiguous(),
                 grad_volume.contiguous() if grad_volume is not None else None, *boxes,
-                per_gaussian=ctx.use_per_gaussian_backward)
+                per_gaussian=ctx.use_per_gaussian_backward, tiles_sorted=tiles)
         return z[0], z[1], z[2], None, None, None, None, None, None

@@ -82,13 +82,18 @@ int gsv_project_bwd(int32_t n, const float *pos3d, const float *scale3d, const f
  * Inclusive int32 prefix sum of num_tiles_hit.  Replaces the
  * `torch.cumsum(num_tiles_hit, dim=0, dtype=torch.int32)` of voxelize.py:87.
  * If total_out is non-NULL the last element (the intersection count) is also
- * written to that device int64, so a caller can read one scalar.
- * Workspace size from gsv_scan_workspace_bytes.
+ * written to that device int64, so a caller can read one scalar.  If
+ * total_host is non-NULL it must be pinned host memory (hipHostMalloc, or a
+ * torch tensor made with pin_memory=True): the kernel writes the count there
+ * too, visible to the host once the scan has completed (e.g. after an event
+ * recorded behind this call), so no device-to-host copy is enqueued.  A
+ * total_host that is not device-visible pinned memory returns
+ * GSV_ERR_INVALID_ARGUMENT.  Workspace size from gsv_scan_workspace_bytes.
  */
 int gsv_scan_workspace_bytes(int64_t n, size_t *bytes);
 int gsv_cumsum_tiles_hit(int32_t n, const int32_t *num_tiles_hit, int32_t *cum_tiles_hit,
-                         int64_t *total_out, void *workspace, size_t workspace_bytes,
-                         void *stream);
+                         int64_t *total_out, int64_t *total_host, void *workspace,
+                         size_t workspace_bytes, void *stream);
 
 /*
  * Binning.  Replaces bin_and_sort_gaussians_torch (bindings.cu:259-360):
@@ -99,13 +104,18 @@ int gsv_cumsum_tiles_hit(int32_t n, const int32_t *num_tiles_hit, int32_t *cum_t
  * with (0,0) for empty tiles, T = ceil(W/8)*ceil(H/8)*ceil(D/8).
  * cum_tiles_hit is the inclusive scan of the per-Gaussian tile counts and must
  * end at num_intersects.  num_intersects <= 0 only zero-fills tile_bins.
+ * tiles_sorted (optional, NULL to skip; num_intersects entries, 16-byte
+ * aligned) receives the sorted keys: the tile id of each sorted pair, which
+ * gsv_voxelize_bwd can take instead of rebuilding it from tile_bins.  The
+ * reference keeps these keys in a scratch tensor (bindings.cu:295-345).
  */
 int gsv_bin_workspace_bytes(int32_t n, int64_t num_intersects, int32_t D, int32_t H, int32_t W,
                             size_t *bytes);
 int gsv_bin_and_sort(int32_t n, int64_t num_intersects, const int32_t *tile_min,
                      const int32_t *tile_max, const int32_t *cum_tiles_hit, int32_t D, int32_t H,
                      int32_t W, void *workspace, size_t workspace_bytes,
-                     int32_t *gaussian_ids_sorted, int32_t *tile_bins, void *stream);
+                     int32_t *gaussian_ids_sorted, int32_t *tile_bins, int32_t *tiles_sorted,
+                     void *stream);
 
 /*
  * Binning with the pair count left on the device.  Replaces the same reference
@@ -114,16 +124,17 @@ int gsv_bin_and_sort(int32_t n, int64_t num_intersects, const int32_t *tile_min,
  * count I = *num_intersects_dev (an int64, e.g. the total written by
  * gsv_cumsum_tiles_hit) and sort min(I, capacity) pairs.  Grids, the workspace
  * (gsv_bin_workspace_bytes with num_intersects = capacity) and
- * gaussian_ids_sorted (capacity entries, 16-byte aligned) are sized by
- * capacity.  When I > capacity the output is incomplete: the caller compares
- * I with capacity once the count reaches the host, and runs again with a
- * larger capacity.
+ * gaussian_ids_sorted and tiles_sorted (capacity entries each, 16-byte
+ * aligned; tiles_sorted optional) are sized by capacity.  When I > capacity
+ * the output is incomplete: the caller compares I with capacity once the count
+ * reaches the host, and runs again with a larger capacity.
  */
 int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity, const int64_t *num_intersects_dev,
                                   const int32_t *tile_min, const int32_t *tile_max,
                                   const int32_t *cum_tiles_hit, int32_t D, int32_t H, int32_t W,
                                   void *workspace, size_t workspace_bytes,
-                                  int32_t *gaussian_ids_sorted, int32_t *tile_bins, void *stream);
+                                  int32_t *gaussian_ids_sorted, int32_t *tile_bins,
+                                  int32_t *tiles_sorted, void *stream);
 
 /*
  * Forward voxelization.  Replaces voxelize_forward_torch (bindings.cu:362-457;
@@ -152,6 +163,9 @@ int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
  *     its duplication slot and one pass sums each Gaussian's slots in order.
  *     No atomics, bitwise reproducible; the workspace grows by
  *     num_intersects * (9 + channels) * 4 bytes.
+ * tiles_sorted (optional) is the binning's sorted keys (gsv_bin_and_sort's
+ * tiles_sorted, at least num_intersects entries); without it the tile of each
+ * pair is rebuilt from tile_bins by one more kernel.
  * Workspace size from gsv_voxelize_bwd_workspace_bytes (deterministic = 1 for
  * the second mode).
  */
@@ -162,7 +176,8 @@ int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
                      int64_t num_intersects, const int32_t *gaussian_ids_sorted,
                      const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
                      const float *intensities, const float *vol_grad, const int32_t *tile_min,
-                     const int32_t *tile_max, const int32_t *cum_tiles_hit, float *dpos3d_radii,
+                     const int32_t *tile_max, const int32_t *cum_tiles_hit,
+                     const int32_t *tiles_sorted, float *dpos3d_radii,
                      float *dconics, float *dintensities, int32_t variant, void *workspace,
                      size_t workspace_bytes, void *stream);
 
@@ -197,7 +212,8 @@ int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32
                         const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
                         const float *intensities, const int8_t *sign, const float *grad_loss,
                         const float *vol_grad, const int32_t *tile_min, const int32_t *tile_max,
-                        const int32_t *cum_tiles_hit, float *dpos3d_radii, float *dconics,
+                        const int32_t *cum_tiles_hit, const int32_t *tiles_sorted,
+                        float *dpos3d_radii, float *dconics,
                         float *dintensities, int32_t variant, void *workspace,
                         size_t workspace_bytes, void *stream);
 
