@@ -19,7 +19,7 @@ a second, identical timed region, against the FP32 vector peak.
 reference, OpenMP over the host cores) on the same inputs.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 30] [--config 3]
-                       [--no-cpu-baseline]
+                       [--no-cpu-baseline] [--no-dropin] [--calibrate-copy]
 """
 import argparse
 import ctypes
@@ -45,6 +45,9 @@ def parse():
                          "steady clocks)")
     ap.add_argument("--config", type=int, default=3, help="workload number 1-5 (BASELINE.json)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-dropin", action="store_true",
+                    help="run only the fused step (profiling runs: every voxelize dispatch is "
+                         "then the one `value` times)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one elementwise kernel that reads and writes 1 GiB (a "
@@ -164,7 +167,8 @@ def main():
 
     for _ in range(args.warmup):
         step_fused()
-        step_dropin()
+        if not args.no_dropin:
+            step_dropin()
     torch.cuda.synchronize()
 
     # `value`: the fused step, nothing else in the timed region.
@@ -181,7 +185,7 @@ def main():
         kern[name] = (tot.value / cnt.value) if cnt.value else None
     _C._L.gsv_kernel_timing_enable(0)
     # the unchanged drop-in step (voxelize_gaussians + torch's l1_loss)
-    ms_dropin = timed(step_dropin, args.steps)
+    ms_dropin = None if args.no_dropin else timed(step_dropin, args.steps)
 
     # Per-stage times from a separate, untimed pass: torch events around each
     # native call of the drop-in API (host gaps included in neither figure).
@@ -191,7 +195,7 @@ def main():
                              "optim_to_render_backward"])
     timer.install()
     timer.active = True
-    for _ in range(min(args.steps, 5)):
+    for _ in range(0 if args.no_dropin else min(args.steps, 5)):
         step_dropin()
     torch.cuda.synchronize()
     timer.active = False
@@ -232,7 +236,7 @@ def main():
                    "step": "optim_to_render + voxelize_gaussians_l1_loss (voxelization fused "
                            "with torch's l1_loss; identical gradients) + backward",
                    "dropin_step": "optim_to_render + voxelize_gaussians + torch l1_loss + backward"},
-        "dropin_ms_per_step": round(ms_dropin, 4),
+        "dropin_ms_per_step": None if ms_dropin is None else round(ms_dropin, 4),
         "ms_per_step_with_kernel_events": round(ms_events, 4),
         "evals_per_s": round(2 * evals / (ms * 1e-3), 1),
         "fwd_evals_per_s": round(evals / (fwd_ms * 1e-3), 1),
