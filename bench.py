@@ -11,15 +11,16 @@ Prints one JSON line.  `value` is ms per iteration (lower is better) of the
 step with the voxelization fused with the L1 loss (voxelize_gaussians_l1_loss:
 the same loss, gradients identical bit for bit); `dropin_ms_per_step` is the
 same step through the unchanged drop-in API (voxelize_gaussians, then torch's
-l1_loss).  After the warm-up, `value` comes from an uninstrumented timed
-region.  The `roofline` object reports the dominant kernel (voxelize
+l1_loss), and `graph_ms_per_step` the fused step captured once in a HIP graph
+and replayed (gs_voxelizer.graph).  After the warm-up, `value` comes from an
+uninstrumented timed region.  The `roofline` object reports the dominant kernel (voxelize
 backward), timed with HIP events recorded on the stream it is launched on over
 a second, identical timed region, against the FP32 vector peak.
 `cpu_baseline` times the CPU oracle (a binary32 C restatement of the
 reference, OpenMP over the host cores) on the same inputs.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 30] [--config 3]
-                       [--no-cpu-baseline] [--no-dropin] [--calibrate-copy]
+                       [--no-cpu-baseline] [--no-dropin] [--no-graph] [--calibrate-copy]
 """
 import argparse
 import ctypes
@@ -48,6 +49,8 @@ def parse():
     ap.add_argument("--no-dropin", action="store_true",
                     help="run only the fused step (profiling runs: every voxelize dispatch is "
                          "then the one `value` times)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip timing the fused step captured in one HIP graph")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one elementwise kernel that reads and writes 1 GiB (a "
@@ -186,6 +189,16 @@ def main():
     _C._L.gsv_kernel_timing_enable(0)
     # the unchanged drop-in step (voxelize_gaussians + torch's l1_loss)
     ms_dropin = None if args.no_dropin else timed(step_dropin, args.steps)
+    # the fused step captured once in a HIP graph and replayed (gs_voxelizer.graph):
+    # no host work per step beyond the replay and the check of the pair count
+    ms_graph = None
+    if not args.no_graph:
+        from gs_voxelizer import graph as G
+        captured = G.CapturedStep(step_fused)
+        for _ in range(5):
+            captured.replay()
+        ms_graph = timed(captured.replay, args.steps)
+        del captured
 
     # Per-stage times from a separate, untimed pass: torch events around each
     # native call of the drop-in API (host gaps included in neither figure).
@@ -237,6 +250,7 @@ def main():
                            "with torch's l1_loss; identical gradients) + backward",
                    "dropin_step": "optim_to_render + voxelize_gaussians + torch l1_loss + backward"},
         "dropin_ms_per_step": None if ms_dropin is None else round(ms_dropin, 4),
+        "graph_ms_per_step": None if ms_graph is None else round(ms_graph, 4),
         "ms_per_step_with_kernel_events": round(ms_events, 4),
         "evals_per_s": round(2 * evals / (ms * 1e-3), 1),
         "fwd_evals_per_s": round(evals / (fwd_ms * 1e-3), 1),

@@ -552,7 +552,7 @@ constexpr int kStageTiles = C == 1 ? 3 : 2;
 
 struct BwdArgs {
     int D, H, W, Tx, Ty, n, n_isect;
-    int64_t T, per;
+    int64_t T;
     const int *ids, *pair_tiles;
     const float4 *pos_radii;
     const float2 *conics;
@@ -563,7 +563,15 @@ struct BwdArgs {
     float *dpos, *dconic, *dint;
     const int *tile_min, *tile_max, *cum;
     float *partial;
+    const int64_t *d_count;  // live pair count on the device (n_isect is then the capacity)
 };
+
+// The live pair count: *d_count clamped to [0, cap], or cap without one.
+__device__ __forceinline__ int live_pairs(int cap, const int64_t *d_count) {
+    if (!d_count) return cap;
+    const int64_t v = *d_count;
+    return v < 0 ? 0 : (v < cap ? (int)v : cap);
+}
 
 // One backward wave's view: lane = one of 64 consecutive (tile, Gaussian)
 // pairs of the sorted list; `slot` numbers the runs of equal tiles.
@@ -873,7 +881,13 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
 template <int C, int K>
 __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
     __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
-    const int64_t wv = xcd_remap(blockIdx.x, a.per);
+    a.n_isect = live_pairs(a.n_isect, a.d_count);
+    // XCD slabs sized by the live wave count (the grid may be sized for a
+    // larger capacity), so every XCD gets an equal share; blocks past the
+    // slabs would alias waves of other blocks and leave
+    const int64_t per = xcd_per(((int64_t)a.n_isect + kWave - 1) / kWave);
+    if ((int64_t)(blockIdx.x / kXcds) >= per) return;
+    const int64_t wv = xcd_remap(blockIdx.x, per);
     const int64_t p0 = wv * kWave;
     if (p0 >= a.n_isect) return;
     BwdLane<C> L;
@@ -889,33 +903,43 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
 }
 
 // The pairs that k_vox_bwd left: those of the waves spanning more than K tiles,
-// in groups of K tiles after the first.  Block b checks the waves 64 b ..
-// 64 b + 63: the tiles of a wave's first and last pair come from the sorted
-// pair -> tile map, and a wave whose tiles lie within K consecutive ids spans
-// at most K of them.  The others (rare) are counted exactly and processed.
+// in groups of K tiles after the first.  A fixed grid of kRestBlocks
+// workgroups; workgroup b checks the waves b, b + G, b + 2G, ... (G = the grid
+// size) 64 at a time, so the waves to process (many in a sparse scene, none in
+// most dense ones) spread over the whole grid.  The tiles of a wave's first and
+// last pair come from the sorted pair -> tile map, and a wave whose tiles lie
+// within K consecutive ids spans at most K of them; the others are counted
+// exactly and processed.
+constexpr int kRestBlocks = 512;
+
 template <int C, int K>
-__global__ __launch_bounds__(kWave) void k_vox_bwd_rest(BwdArgs a, int64_t waves) {
+__global__ __launch_bounds__(kWave) void k_vox_bwd_rest(BwdArgs a) {
     __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
-    const int64_t w = (int64_t)blockIdx.x * kWave + threadIdx.x;
-    bool maybe = false;
-    if (w < waves) {
-        const int64_t p0 = w * kWave;
-        const int64_t p1 = min<int64_t>(p0 + kWave, a.n_isect) - 1;
-        const int t0 = a.pair_tiles[p0], t1 = a.pair_tiles[p1];
-        maybe = !(t0 >= 0 && t1 < a.T && t1 >= t0 && t1 - t0 < K);
-    }
-    for (uint64_t m = __ballot(maybe); m; m &= m - 1) {
-        const int64_t p0 = ((int64_t)blockIdx.x * kWave + __builtin_ctzll(m)) * kWave;
-        BwdLane<C> L;
-        uint64_t starts;
-        int nslots;
-        if (!bwd_slots(a, p0, L, starts, nslots) || nslots <= K) continue;
-        bwd_gaussian(a, p0, L);
-        const bool wave_fast = __all(!L.live || L.fast);
-        const bool any_live = __any(L.live);
-        if (!any_live && a.partial == nullptr) continue;
-        for (int g0 = K; g0 < nslots; g0 += K)
-            bwd_group<C, K>(a, L, starts, g0, wave_fast, any_live, s_g);
+    a.n_isect = live_pairs(a.n_isect, a.d_count);
+    const int64_t waves = ((int64_t)a.n_isect + kWave - 1) / kWave;
+    const int64_t G = gridDim.x;
+    for (int64_t base = blockIdx.x; base < waves; base += G * kWave) {
+        const int64_t w = base + (int64_t)threadIdx.x * G;
+        bool maybe = false;
+        if (w < waves) {
+            const int64_t p0 = w * kWave;
+            const int64_t p1 = min<int64_t>(p0 + kWave, a.n_isect) - 1;
+            const int t0 = a.pair_tiles[p0], t1 = a.pair_tiles[p1];
+            maybe = !(t0 >= 0 && t1 < a.T && t1 >= t0 && t1 - t0 < K);
+        }
+        for (uint64_t m = __ballot(maybe); m; m &= m - 1) {
+            const int64_t p0 = (base + (int64_t)__builtin_ctzll(m) * G) * kWave;
+            BwdLane<C> L;
+            uint64_t starts;
+            int nslots;
+            if (!bwd_slots(a, p0, L, starts, nslots) || nslots <= K) continue;
+            bwd_gaussian(a, p0, L);
+            const bool wave_fast = __all(!L.live || L.fast);
+            const bool any_live = __any(L.live);
+            if (!any_live && a.partial == nullptr) continue;
+            for (int g0 = K; g0 < nslots; g0 += K)
+                bwd_group<C, K>(a, L, starts, g0, wave_fast, any_live, s_g);
+        }
     }
 }
 
@@ -946,8 +970,10 @@ __device__ __forceinline__ double row_total(double x) {
 
 template <int C>
 __global__ __launch_bounds__(kReduceThreads) void k_pair_reduce(
-    int n, int n_isect, const int *__restrict__ cum, const float *__restrict__ partial,
-    float *__restrict__ dpos, float *__restrict__ dconic, float *__restrict__ dint) {
+    int n, int cap, const int64_t *__restrict__ d_count, const int *__restrict__ cum,
+    const float *__restrict__ partial, float *__restrict__ dpos, float *__restrict__ dconic,
+    float *__restrict__ dint) {
+    const int n_isect = live_pairs(cap, d_count);
     constexpr int F = 9 + C;
     const int r = threadIdx.x & (kRowLanes - 1);
     const int g = (int)(((int64_t)blockIdx.x * kReduceThreads + threadIdx.x) / kRowLanes);
@@ -1057,7 +1083,7 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
                       const float *intensities, const float *vol_grad, const int8_t *l1_sgn,
                       const float *l1_grad, const int32_t *tile_min,
                       const int32_t *tile_max, const int32_t *cum_tiles_hit,
-                      const int32_t *tiles_sorted, float *dpos3d_radii,
+                      const int32_t *tiles_sorted, const int64_t *count_dev, float *dpos3d_radii,
                       float *dconics, float *dintensities, int32_t variant, void *workspace,
                       size_t workspace_bytes, hipStream_t s) {
     if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
@@ -1102,7 +1128,7 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     const float numel = (float)((int64_t)D * H * W * channels);
     BwdArgs args;
     args.D = D; args.H = H; args.W = W; args.Tx = Tx; args.Ty = Ty; args.n = n; args.n_isect = ni;
-    args.T = T; args.per = per;
+    args.T = T;
     args.ids = gaussian_ids_sorted; args.pair_tiles = pair_tiles;
     args.pos_radii = reinterpret_cast<const float4 *>(pos3d_radii);
     args.conics = reinterpret_cast<const float2 *>(conics);
@@ -1111,14 +1137,14 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     args.dpos = dpos3d_radii; args.dconic = dconics; args.dint = dintensities;
     args.tile_min = tile_min; args.tile_max = tile_max; args.cum = cum_tiles_hit;
     args.partial = partial;
+    args.d_count = count_dev;
 #define GSV_VB(CH)                                                                                  \
     {                                                                                               \
         KernelTimer timer(kTimedVoxBwd, s);                                                         \
         hipLaunchKernelGGL((k_vox_bwd<CH, kStageTiles<CH>>), grid, block, 0, s, args);             \
         if (int st = check_launch()) return st;                                                     \
-        hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTiles<CH>>),                                  \
-                           dim3((unsigned)((waves + kWave - 1) / kWave)), block, 0, s, args,        \
-                           waves);                                                                  \
+        hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTiles<CH>>), dim3(kRestBlocks), block, 0, s,  \
+                           args);                                                                   \
     }                                                                                               \
     if (int st = check_launch()) return st;                                                         \
     if (pairs) {                                                                                    \
@@ -1126,7 +1152,7 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
         hipLaunchKernelGGL(k_pair_reduce<CH>,                                                      \
                            dim3((unsigned)(((int64_t)n * kRowLanes + kReduceThreads - 1) /          \
                                            kReduceThreads)),                                        \
-                           dim3(kReduceThreads), 0, s, n, ni,                                       \
+                           dim3(kReduceThreads), 0, s, n, ni, count_dev,                            \
                            cum_tiles_hit, partial, dpos3d_radii, dconics, dintensities);            \
     }
     switch (channels) {
@@ -1192,12 +1218,14 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
                                 const float *conics, const float *intensities,
                                 const float *vol_grad, const int32_t *tile_min,
                                 const int32_t *tile_max, const int32_t *cum_tiles_hit,
-                                const int32_t *tiles_sorted, float *dpos3d_radii, float *dconics,
-                                float *dintensities, int32_t variant, void *workspace,
-                                size_t workspace_bytes, void *stream) {
+                                const int32_t *tiles_sorted, const int64_t *num_intersects_dev,
+                                float *dpos3d_radii, float *dconics, float *dintensities,
+                                int32_t variant, void *workspace, size_t workspace_bytes,
+                                void *stream) {
     return voxelize_bwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
                              pos3d_radii, conics, intensities, vol_grad, nullptr, nullptr,
-                             tile_min, tile_max, cum_tiles_hit, tiles_sorted, dpos3d_radii, dconics,
+                             tile_min, tile_max, cum_tiles_hit, tiles_sorted, num_intersects_dev,
+                             dpos3d_radii, dconics,
                              dintensities, variant, workspace, workspace_bytes, as_stream(stream));
 }
 
@@ -1208,12 +1236,14 @@ extern "C" int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t chan
                                    const int8_t *sign, const float *grad_loss,
                                    const float *vol_grad, const int32_t *tile_min,
                                    const int32_t *tile_max, const int32_t *cum_tiles_hit,
-                                   const int32_t *tiles_sorted, float *dpos3d_radii,
-                                   float *dconics, float *dintensities, int32_t variant,
-                                   void *workspace, size_t workspace_bytes, void *stream) {
+                                   const int32_t *tiles_sorted, const int64_t *num_intersects_dev,
+                                   float *dpos3d_radii, float *dconics, float *dintensities,
+                                   int32_t variant, void *workspace, size_t workspace_bytes,
+                                   void *stream) {
     if (!sign || !grad_loss) return GSV_ERR_INVALID_ARGUMENT;
     return voxelize_bwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
                              pos3d_radii, conics, intensities, vol_grad, sign, grad_loss,
-                             tile_min, tile_max, cum_tiles_hit, tiles_sorted, dpos3d_radii, dconics,
+                             tile_min, tile_max, cum_tiles_hit, tiles_sorted, num_intersects_dev,
+                             dpos3d_radii, dconics,
                              dintensities, variant, workspace, workspace_bytes, as_stream(stream));
 }

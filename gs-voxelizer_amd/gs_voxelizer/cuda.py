@@ -286,9 +286,11 @@ def voxelize_forward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
 
 def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                        intensities, vol_grad_in, tile_min=None, tile_max=None,
-                       cum_tiles_hit=None, l1=None, tiles_sorted=None):
+                       cum_tiles_hit=None, l1=None, tiles_sorted=None, count_dev=None):
     """l1 = (sign, grad_loss): the fused L1 source, with vol_grad_in optional.
-    tiles_sorted: the binning's tile id per sorted pair (return_tiles), optional."""
+    tiles_sorted: the binning's tile id per sorted pair (return_tiles), optional.
+    count_dev: (1,) int64 device tensor with the live pair count, when the id
+    arrays are capacity-sized (bin_and_sort_gaussians_device_count); optional."""
     _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
     given = [t is not None for t in (tile_min, tile_max, cum_tiles_hit)]
     if any(given) and not all(given):
@@ -317,6 +319,9 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
     n = pos3d.size(0)
     dev = pos3d.device
     I = gaussian_ids_sorted.numel()
+    if count_dev is not None:
+        _check_input(count_dev, "count_dev")
+        _check_dtype(count_dev, "count_dev", torch.int64)
     if tiles_sorted is not None:
         _check_input(tiles_sorted, "tiles_sorted")
         _check_dtype(tiles_sorted, "tiles_sorted", torch.int32)
@@ -338,51 +343,55 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
              else (null, null, null))
     vg = _ptr(vol_grad_in) if vol_grad_in is not None else null
     ts = _ptr(tiles_sorted) if tiles_sorted is not None else null
+    cd = _ptr(count_dev) if count_dev is not None else null
     with torch.cuda.device(dev):
         if l1 is None:
             _call("voxelize_bwd", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted),
                   _ptr(tile_bins), _ptr(pos3d), _ptr(conics), _ptr(intensities), vg, *boxes, ts,
-                  _ptr(dpos), _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value,
+                  cd, _ptr(dpos), _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value,
                   _stream(dev))
         else:
             _call("voxelize_bwd_l1", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted),
                   _ptr(tile_bins), _ptr(pos3d), _ptr(conics), _ptr(intensities), _ptr(sign),
-                  _ptr(grad_loss), vg, *boxes, ts, _ptr(dpos), _ptr(dconics), _ptr(dint),
+                  _ptr(grad_loss), vg, *boxes, ts, cd, _ptr(dpos), _ptr(dconics), _ptr(dint),
                   variant, _ptr(ws), nbytes.value, _stream(dev))
     return dpos, dconics, dint
 
 
 def voxelize_backward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
                          sign, grad_loss, vol_grad_in=None, tile_min=None, tile_max=None,
-                         cum_tiles_hit=None, per_gaussian=True, tiles_sorted=None):
+                         cum_tiles_hit=None, per_gaussian=True, tiles_sorted=None,
+                         count_dev=None):
     """Backward of voxelize_forward_l1: dL/dvolume = sign * grad_loss / numel (+
     vol_grad_in, the volume's gradient from other uses, when given), never
     materialised.  Returns (dpos3d_radii, dconics, dintensities)."""
     return _voxelize_backward(1 if per_gaussian else 0, vol_size, gaussian_ids_sorted, tile_bins,
                               pos3d, conics, intensities, vol_grad_in, tile_min, tile_max,
-                              cum_tiles_hit, l1=(sign, grad_loss), tiles_sorted=tiles_sorted)
+                              cum_tiles_hit, l1=(sign, grad_loss), tiles_sorted=tiles_sorted,
+                              count_dev=count_dev)
 
 
 def voxelize_backward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
                       vol_grad_in, tile_min=None, tile_max=None, cum_tiles_hit=None,
-                      tiles_sorted=None):
+                      tiles_sorted=None, count_dev=None):
     """bindings.cu:459-584 (per-voxel variant). Returns (dpos3d_radii, dconics, dintensities).
 
     The optional tile_min / tile_max / cum_tiles_hit (the projection's tile boxes
     and the prefix sum used for binning) select the atomic-free, bitwise
     reproducible reduction; without them float atomics are used, as in the
     reference.  tiles_sorted (bin_and_sort_gaussians(..., return_tiles=True)) saves
-    rebuilding the tile of each pair."""
+    rebuilding the tile of each pair; count_dev gives the live pair count for
+    capacity-sized id arrays."""
     return _voxelize_backward(0, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                               intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit,
-                              tiles_sorted=tiles_sorted)
+                              tiles_sorted=tiles_sorted, count_dev=count_dev)
 
 
 def voxelize_backward_per_gaussian(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                                    intensities, vol_grad_in, tile_min=None, tile_max=None,
-                                   cum_tiles_hit=None, tiles_sorted=None):
+                                   cum_tiles_hit=None, tiles_sorted=None, count_dev=None):
     """bindings.cu:586-781 (per-Gaussian variant). Returns (dpos3d_radii, dconics, dintensities).
     Optional arguments as in voxelize_backward."""
     return _voxelize_backward(1, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                               intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit,
-                              tiles_sorted=tiles_sorted)
+                              tiles_sorted=tiles_sorted, count_dev=count_dev)

@@ -24,6 +24,7 @@ import gs_voxelizer.cuda as _C
 
 _INT32_MAX = 2**31 - 1
 _capacity = {}  # device index -> intersection capacity of the speculative path
+_count_host = {}  # device index -> pinned int64 the prefix-sum kernel writes the count into
 
 
 def _grow(count: int) -> int:
@@ -35,6 +36,26 @@ def _speculate() -> bool:
 
 
 _SPIN_READS = 1 << 21  # reads of the pinned count before falling back to a device sync
+
+
+def count_buffer(device=None) -> Tensor:
+    """The persistent pinned (1,) int64 that the forward's prefix-sum kernel
+    writes the intersection count of `device` into (also inside a captured
+    graph, at every replay)."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    buf = _count_host.get(key)
+    if buf is None:
+        buf = torch.empty((1,), dtype=torch.int64, pin_memory=True)
+        _count_host[key] = buf
+    return buf
+
+
+def capacity(device=None):
+    """The intersection capacity recorded for `device` (None before the first
+    forward on it)."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    return _capacity.get(dev.index if dev.index is not None else torch.cuda.current_device())
 
 
 def _await_count(host: Tensor, dev: torch.device) -> int:
@@ -93,15 +114,34 @@ def voxelize_gaussians(
 def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd):
     """Prefix sum, binning and `fwd(gaussian_ids_sorted, tile_bins)` for a
     non-empty Gaussian set.  Returns (num_intersects, ids, tile_bins, tiles, cum,
-    fwd's result), tiles being the tile id of each sorted pair (for the
-    backward); ids and tiles are None when there are no intersections."""
+    fwd's result, count_dev), tiles being the tile id of each sorted pair (for
+    the backward); ids and tiles are None when there are no intersections.
+
+    Under graph capture nothing is read back: the arrays keep the recorded
+    capacity, num_intersects is that capacity and count_dev (the live count on
+    the device) bounds the backward; the replay's count lands in count_buffer()
+    for the caller to check against capacity() (gs_voxelizer.graph does)."""
     dev = num_tiles_hit.device
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     cap = _capacity.get(key) if _speculate() else None
+    if torch.cuda.is_current_stream_capturing():
+        if cap is None:
+            raise RuntimeError(
+                "gs_voxelizer: run the step once outside graph capture first (it records the "
+                "intersection capacity the captured arrays are sized for), and leave "
+                "GSV_SYNC_COUNT unset")
+        cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous(),
+                                                   total_host=count_buffer(dev))
+        ids_cap, tile_bins, tiles_cap = _C.bin_and_sort_gaussians_device_count(
+            num_gaussians, cap, total, tile_min, tile_max, cum_tiles_hit, vol_size_voxel,
+            return_tiles=True)
+        return (cap, ids_cap, tile_bins, tiles_cap, cum_tiles_hit, fwd(ids_cap, tile_bins),
+                total)
     if cap is not None:
         # launch at the recorded capacity; the scan writes the count into pinned
         # memory meanwhile
-        host = torch.empty((1,), dtype=torch.int64, pin_memory=True).fill_(-1)
+        host = count_buffer(dev)
+        host.fill_(-1)
         cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous(), total_host=host)
         ids_cap, tile_bins, tiles_cap = _C.bin_and_sort_gaussians_device_count(
             num_gaussians, cap, total, tile_min, tile_max, cum_tiles_hit, vol_size_voxel,
@@ -112,9 +152,9 @@ def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tile
             if num_intersects < cap // 4:
                 _capacity[key] = _grow(num_intersects)
             if num_intersects < 1:
-                return 0, None, tile_bins, None, cum_tiles_hit, result
+                return 0, None, tile_bins, None, cum_tiles_hit, result, None
             return (num_intersects, ids_cap[:num_intersects], tile_bins,
-                    tiles_cap[:num_intersects], cum_tiles_hit, result)
+                    tiles_cap[:num_intersects], cum_tiles_hit, result, None)
     else:
         cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous())
         num_intersects = int(total.item())
@@ -124,12 +164,12 @@ def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tile
     if _speculate():
         _capacity[key] = _grow(num_intersects)
     if num_intersects < 1:
-        return 0, None, None, None, cum_tiles_hit, None
+        return 0, None, None, None, cum_tiles_hit, None, None
     # first call on the device, host read requested, or the capacity overflowed
     ids, tile_bins, tiles = _C.bin_and_sort_gaussians(
         num_gaussians, num_intersects, tile_min.contiguous(), tile_max.contiguous(),
         cum_tiles_hit, vol_size_voxel, return_tiles=True)
-    return num_intersects, ids, tile_bins, tiles, cum_tiles_hit, fwd(ids, tile_bins)
+    return num_intersects, ids, tile_bins, tiles, cum_tiles_hit, fwd(ids, tile_bins), None
 
 
 class _VoxelizeGaussians(Function):
@@ -150,12 +190,14 @@ class _VoxelizeGaussians(Function):
         if num_gaussians > 0:
             fwd = lambda ids, bins: _C.voxelize_forward(vol_size_voxel, ids, bins, pos3d_radii,
                                                         conics, intensities)
-            I, gaussian_ids_sorted, tile_bins, tiles, cum_tiles_hit, out = _bin_and_forward(
+            I, gaussian_ids_sorted, tile_bins, tiles, cum_tiles_hit, out, count = _bin_and_forward(
                 num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd)
             ctx.num_intersects = I
             # the backward reduces per-pair partials in duplication order (no
             # atomics) and takes each sorted pair's tile from the binning
             boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit, tiles)
+            if count is not None:  # captured: capacity-sized arrays, live count on the device
+                boxes += (count,)
         if ctx.num_intersects < 1:
             out = torch.zeros(D, H, W, C, device=dev, dtype=pos3d_radii.dtype)
             gaussian_ids_sorted = torch.zeros(0, 1, device=dev, dtype=torch.int32)
@@ -172,6 +214,7 @@ class _VoxelizeGaussians(Function):
         saved = ctx.saved_tensors
         pos3d_radii, conics, intensities, gaussian_ids_sorted, tile_bins = saved[:5]
         boxes, tiles = saved[5:8], (saved[8] if len(saved) > 8 else None)
+        count = saved[9] if len(saved) > 9 else None
         if ctx.num_intersects < 1 or vol_grad is None:
             pos3d_grad = torch.zeros_like(pos3d_radii)
             conics_grad = torch.zeros_like(conics)
@@ -181,7 +224,7 @@ class _VoxelizeGaussians(Function):
                   else _C.voxelize_backward)
             pos3d_grad, conics_grad, intensities_grad = fn(
                 vol_size_voxel, gaussian_ids_sorted, tile_bins, pos3d_radii, conics, intensities,
-                vol_grad.contiguous(), *boxes, tiles_sorted=tiles)
+                vol_grad.contiguous(), *boxes, tiles_sorted=tiles, count_dev=count)
         return pos3d_grad, conics_grad, intensities_grad, None, None, None, None, None
 
 
@@ -237,10 +280,12 @@ class _VoxelizeL1(Function):
         boxes = ()
         ctx.num_intersects = 0
         if num_gaussians > 0:
-            I, ids, tile_bins, tiles, cum_tiles_hit, res = _bin_and_forward(
+            I, ids, tile_bins, tiles, cum_tiles_hit, res, count = _bin_and_forward(
                 num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd)
             ctx.num_intersects = I
             boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit, tiles)
+            if count is not None:  # captured: capacity-sized arrays, live count on the device
+                boxes += (count,)
         if ctx.num_intersects < 1:
             # no Gaussian touches the volume: it is zero, the loss mean(|target|)
             empty_ids = torch.zeros(0, device=dev, dtype=torch.int32)
@@ -258,6 +303,7 @@ class _VoxelizeL1(Function):
         saved = ctx.saved_tensors
         pos3d_radii, conics, intensities, ids, tile_bins, sign = saved[:6]
         boxes, tiles = saved[6:9], (saved[9] if len(saved) > 9 else None)
+        count = saved[10] if len(saved) > 10 else None
         if ctx.num_intersects < 1 or (grad_loss is None and grad_volume is None):
             z = (torch.zeros_like(pos3d_radii), torch.zeros_like(conics),
                  torch.zeros_like(intensities))
@@ -268,5 +314,5 @@ class _VoxelizeL1(Function):
                 ctx.vol_size_voxel, ids, tile_bins, pos3d_radii, conics, intensities, sign,
                 grad_loss.contiguous(),
                 grad_volume.contiguous() if grad_volume is not None else None, *boxes,
-                per_gaussian=ctx.use_per_gaussian_backward, tiles_sorted=tiles)
+                per_gaussian=ctx.use_per_gaussian_backward, tiles_sorted=tiles, count_dev=count)
         return z[0], z[1], z[2], None, None, None, None, None, None

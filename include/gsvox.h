@@ -166,6 +166,11 @@ int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
  * tiles_sorted (optional) is the binning's sorted keys (gsv_bin_and_sort's
  * tiles_sorted, at least num_intersects entries); without it the tile of each
  * pair is rebuilt from tile_bins by one more kernel.
+ * num_intersects_dev (optional, device int64): the live pair count, as left by
+ * gsv_cumsum_tiles_hit; num_intersects is then the capacity that the id, tile
+ * and workspace arrays and the grids are sized for (gsv_bin_and_sort_device_count
+ * outputs), and the kernels process min(count, capacity) pairs.  With it the
+ * backward needs no host-side count, so a caller can capture it in a graph.
  * Workspace size from gsv_voxelize_bwd_workspace_bytes (deterministic = 1 for
  * the second mode).
  */
@@ -177,9 +182,9 @@ int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
                      const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
                      const float *intensities, const float *vol_grad, const int32_t *tile_min,
                      const int32_t *tile_max, const int32_t *cum_tiles_hit,
-                     const int32_t *tiles_sorted, float *dpos3d_radii,
-                     float *dconics, float *dintensities, int32_t variant, void *workspace,
-                     size_t workspace_bytes, void *stream);
+                     const int32_t *tiles_sorted, const int64_t *num_intersects_dev,
+                     float *dpos3d_radii, float *dconics, float *dintensities, int32_t variant,
+                     void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Voxelization fused with an L1 loss.  These have no reference binding.  They
@@ -213,7 +218,7 @@ int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32
                         const float *intensities, const int8_t *sign, const float *grad_loss,
                         const float *vol_grad, const int32_t *tile_min, const int32_t *tile_max,
                         const int32_t *cum_tiles_hit, const int32_t *tiles_sorted,
-                        float *dpos3d_radii, float *dconics,
+                        const int64_t *num_intersects_dev, float *dpos3d_radii, float *dconics,
                         float *dintensities, int32_t variant, void *workspace,
                         size_t workspace_bytes, void *stream);
 
