@@ -195,7 +195,9 @@ def main():
     if not args.no_graph:
         from gs_voxelizer import graph as G
         captured = G.CapturedStep(step_fused)
-        for _ in range(5):
+        # as many warm replays as eager warm-up steps: the GPU idles during the
+        # capture and needs a few dozen steps to reach its clocks again
+        for _ in range(args.warmup):
             captured.replay()
         ms_graph = timed(captured.replay, args.steps)
         del captured

@@ -331,13 +331,20 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
     for (int k = 0; k < kRounds; ++k) {
         const bool valid = wbase + k * kWave + lane < n;
         const int d = (key[k] >> shift) & (kRadixBins - 1);
-        uint64_t peers = __ballot(valid);
+        // peers = the valid lanes whose digit equals d: per bit b, t = -1 where
+        // bit b of d is set, and a lane keeps the lanes whose ballot bit agrees
+        // (sign-extended bit, xor, and-not: about 6 VALU per bit, against 9
+        // for a per-lane select between m and ~m)
+        const uint64_t vm = __ballot(valid);
+        uint32_t plo = (uint32_t)vm, phi = (uint32_t)(vm >> 32);
 #pragma unroll
         for (int b = 0; b < kRadixBits; ++b) {
-            const bool bit = (d >> b) & 1;
-            const uint64_t m = __ballot(bit);
-            peers &= bit ? m : ~m;
+            const uint32_t t = (uint32_t)__builtin_amdgcn_sbfe(d, b, 1);
+            const uint64_t m = __ballot(t != 0u);
+            plo &= ~((uint32_t)m ^ t);
+            phi &= ~((uint32_t)(m >> 32) ^ t);
         }
+        const uint64_t peers = ((uint64_t)phi << 32) | plo;
         const int r = __popcll(peers & lt);
         // one wave reads then updates its own counters: LDS keeps the order
         const int off = s_wcnt[wave][d];
