@@ -4,8 +4,8 @@
 // with the scan instead of needing launches of their own.
 //
 // Blocks of 256 threads x 8 items (2048 elements).  Two launches when there
-// are at most 1024 blocks: block sums, then an apply pass in which every block
-// adds up its predecessors' sums itself (<= 4 loads per thread).  Above that a
+// are at most 2048 blocks: block sums, then an apply pass in which every block
+// adds up its predecessors' sums itself (<= 8 loads per thread).  Above that a
 // third launch scans the block sums in one workgroup first.  Every pass is
 // HBM-bound: 4 B read per element twice, plus the stores.
 #pragma once
@@ -20,7 +20,7 @@ namespace scan_detail {
 constexpr int kThreads = 256;
 constexpr int kItems = 8;
 constexpr int kTile = kThreads * kItems;
-constexpr int64_t kDirectBlocks = 1024;
+constexpr int64_t kDirectBlocks = 2048;
 
 // Inclusive scan of one int per lane across a 64-wide wave.
 __device__ __forceinline__ int wave_inclusive(int v) {

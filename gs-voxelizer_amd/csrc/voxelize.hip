@@ -41,6 +41,7 @@
 #include <float.h>
 
 #include "gsv_device.h"
+#include "gsv_scan.h"
 
 namespace gsv {
 namespace {
@@ -115,6 +116,14 @@ __device__ __forceinline__ bool gate_free_ok(const Gate &g, float max_abs_i, flo
 // Conservative test: can the ellipsoid {d^T Q d <= K^2}, K^2 = 2 ln(mean*1e6),
 // centred at (mx,my,mz), contain a point of the box [lo, hi]?  Only answers
 // "no" for a positive-definite Q; margins cover binary32 rounding of the gate.
+// Two separating-axis tests: the coordinate axes (the ellipsoid's bounding
+// box), then the axis n = Q (c - mu) through the box centre c.  Along n the
+// ellipsoid spans n.mu +- K sqrt(n^T Q^-1 n) = n.mu +- K sqrt(m) and the box
+// n.c +- sum |n_i| e_i, with m = (c - mu)^T Q (c - mu) = n.(c - mu), so they
+// are apart when m - K sqrt(m) > sum |n_i| e_i.  The reference's 3-sigma tile
+// boxes make the first test pass for every pair they list; the second finds
+// ~90% of the pairs none of whose voxel centres passes the gate (~12% of all
+// pairs on uniform scenes: small Gaussians at the corners of their boxes).
 __device__ __forceinline__ bool may_touch(float mx, float my, float mz, float a, float b, float c,
                                           float d, float e, float f, float t2, float xlo,
                                           float xhi, float ylo, float yhi, float zlo, float zhi) {
@@ -128,7 +137,18 @@ __device__ __forceinline__ bool may_touch(float mx, float my, float mz, float a,
     const float hz = sqrtf(k2 * cfz * inv) * 1.001f + 0.01f;
     const bool miss = (mx + hx < xlo) || (mx - hx > xhi) || (my + hy < ylo) || (my - hy > yhi) ||
                       (mz + hz < zlo) || (mz - hz > zhi);
-    return !miss;  // NaN anywhere -> comparisons false -> keep
+    if (miss) return false;
+    // m and r in binary64: m can cancel for an elongated conic (its binary32
+    // error bound is relative to |d|^T |Q| |d|, not to m)
+    const float ex = 0.5f * (xhi - xlo), ey = 0.5f * (yhi - ylo), ez = 0.5f * (zhi - zlo);
+    const double dx = (xlo + ex) - mx, dy = (ylo + ey) - my, dz = (zlo + ez) - mz;
+    const double nx = (double)a * dx + (double)b * dy + (double)c * dz;
+    const double ny = (double)b * dx + (double)d * dy + (double)e * dz;
+    const double nz = (double)c * dx + (double)e * dy + (double)f * dz;
+    const float m = (float)(dx * nx + dy * ny + dz * nz);
+    const float r = (float)(fabs(nx) * ex + fabs(ny) * ey + fabs(nz) * ez);
+    const float K = sqrtf(k2) * 1.001f + 0.01f, sm = sqrtf(m);
+    return !(sm * (sm - K) > r * 1.001f + 0.01f);  // NaN anywhere -> comparisons false -> keep
 }
 
 __host__ __device__ inline bool aligned_to(const void *p, uintptr_t a) {
@@ -170,7 +190,8 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
     int D, int H, int W, int Tx, int Ty, int64_t T, int n, int n_isect,
     const int *__restrict__ ids, const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
     const float2 *__restrict__ conics, const float *__restrict__ intens, float *__restrict__ vol,
-    const float *__restrict__ target, float *__restrict__ tile_loss, int8_t *__restrict__ sgn) {
+    const float *__restrict__ target, float *__restrict__ tile_loss, int8_t *__restrict__ sgn,
+    uint8_t *__restrict__ pair_live) {
     __shared__ float4 s_rec[kWave][kRecF4<C>];
     const int64_t tile = xcd_runs(blockIdx.x);
     if (tile >= T) return;
@@ -260,6 +281,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                                                      rec[4 * q + 3]);
                 }
             }
+            if (pair_live != nullptr) pair_live[idx] = live ? 1 : 0;
         }
         const uint64_t live_mask = __ballot(live);
         uint64_t fmask = __ballot(fast);  // fast implies live
@@ -564,6 +586,12 @@ struct BwdArgs {
     const int *tile_min, *tile_max, *cum;
     float *partial;
     const int64_t *d_count;  // live pair count on the device (n_isect is then the capacity)
+    // Optional work list: the sorted positions of the pairs the forward's tile
+    // culling kept, ascending, *d_work of them; the culled pairs' partials are
+    // zero already.  Without it the work is every pair.
+    const int *order;
+    const int64_t *d_work;
+    int n_work;  // work items, set by each kernel from the counts
 };
 
 // The live pair count: *d_count clamped to [0, cap], or cap without one.
@@ -573,11 +601,23 @@ __device__ __forceinline__ int live_pairs(int cap, const int64_t *d_count) {
     return v < 0 ? 0 : (v < cap ? (int)v : cap);
 }
 
-// One backward wave's view: lane = one of 64 consecutive (tile, Gaussian)
-// pairs of the sorted list; `slot` numbers the runs of equal tiles.
+// Sets a.n_isect to the live pair count and a.n_work to the work items.
+__device__ __forceinline__ void bwd_counts(BwdArgs &a) {
+    a.n_isect = live_pairs(a.n_isect, a.d_count);
+    a.n_work = a.order ? live_pairs(a.n_isect, a.d_work) : a.n_isect;
+}
+
+// Sorted position of work item q (q < a.n_work).
+__device__ __forceinline__ int bwd_pair(const BwdArgs &a, int64_t q) {
+    return a.order ? a.order[q] : (int)q;
+}
+
+// One backward wave's view: lane = one of 64 consecutive work items (pairs of
+// the sorted list, or of the culled list); `slot` numbers the runs of equal
+// tiles.
 template <int C>
 struct BwdLane {
-    int tile, slot, g;
+    int tile, slot, g, p;
     bool valid, live, fast;
     float mxl, myl, mzl, ca, cb, cc, cd, ce, cf;
     float I[C];
@@ -585,13 +625,148 @@ struct BwdLane {
     TileGeom tg;
 };
 
+// Emission slot of the pair (tile, g): e = cum[g-1] + ((tz-min.z)*ny +
+// (ty-min.y))*nx + (tx-min.x), the order the pairs were duplicated in
+// (gaussian-major, tiles z->y->x), so each Gaussian's partials are contiguous
+// for the reduction pass.  -1 when g or the tile is out of range or the slot
+// lies outside [cum[g-1], cum[g]) or past the pair count.
+__device__ __forceinline__ int64_t emission_slot(int g, int tile, int n, int Tx, int Ty,
+                                                 const int *tile_min, const int *tile_max,
+                                                 const int *cum, int n_isect) {
+    if ((unsigned)g >= (unsigned)n || tile < 0) return -1;
+    const unsigned qt = (unsigned)tile / (unsigned)Tx;
+    const int tx = (int)((unsigned)tile - qt * (unsigned)Tx);
+    const int ty = (int)(qt % (unsigned)Ty), tz = (int)(qt / (unsigned)Ty);
+    const int mnx = tile_min[3 * g], mny = tile_min[3 * g + 1], mnz = tile_min[3 * g + 2];
+    const int nxb = tile_max[3 * g] - mnx, nyb = tile_max[3 * g + 1] - mny;
+    const int64_t base = g == 0 ? 0 : cum[g - 1];
+    const int64_t e = base + ((int64_t)(tz - mnz) * nyb + (ty - mny)) * nxb + (tx - mnx);
+    return (e >= base && e < (int64_t)cum[g] && e < n_isect) ? e : -1;
+}
+
+// The forward's tile culling (pair_live: one byte per sorted pair) as the
+// backward's work list.  order[0 .. kept) = the sorted positions of the pairs
+// the forward kept, ascending; order[np-1], order[np-2], ... = the culled
+// ones (np = the pair count).  Two passes over 4096 flags per block: counts,
+// then positions (each block adds its predecessors' counts itself up to 2048
+// blocks; beyond that one workgroup scans the counts in between).
+constexpr int kKeepThreads = 256;
+constexpr int kKeepItems = 16;
+constexpr int kKeepTile = kKeepThreads * kKeepItems;
+static_assert(kKeepThreads == scan_detail::kThreads, "block scan of gsv_scan.h");
+
+// Flags [i0, i0 + 16) as a bit mask (bit k: pair i0 + k kept); *valid = how
+// many of them lie below the pair count np.
+__device__ __forceinline__ unsigned keep_mask(const uint8_t *flags, int64_t i0, int np,
+                                              int *valid) {
+    const int64_t v = min<int64_t>(kKeepItems, (int64_t)np - i0);
+    *valid = v > 0 ? (int)v : 0;
+    unsigned m = 0;
+    if (v >= kKeepItems) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(flags + i0);
+        const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                if ((ws[q] >> (8 * b)) & 0xffu) m |= 1u << (4 * q + b);
+    } else {
+        for (int k = 0; k < *valid; ++k)
+            if (flags[i0 + k]) m |= 1u << k;
+    }
+    return m;
+}
+
+__global__ __launch_bounds__(kKeepThreads) void k_keep_count(const uint8_t *__restrict__ flags,
+                                                             int cap,
+                                                             const int64_t *__restrict__ d_count,
+                                                             int32_t *__restrict__ part) {
+    __shared__ int lds_waves[kKeepThreads / kWave];
+    const int np = live_pairs(cap, d_count);
+    const int64_t i0 = (int64_t)blockIdx.x * kKeepTile + (int64_t)threadIdx.x * kKeepItems;
+    int valid;
+    const int c = __popc(keep_mask(flags, i0, np, &valid));
+    int total;
+    (void)scan_detail::block_exclusive(c, lds_waves, &total);
+    if (threadIdx.x == 0) part[blockIdx.x] = total;
+}
+
+// direct: part holds raw block counts (nb <= 2048); otherwise part holds their
+// exclusive prefix and *d_kept the total already.  The block's kept positions
+// (ascending) and culled ones (descending) are staged in LDS and stored as
+// two contiguous runs.
+__global__ __launch_bounds__(kKeepThreads) void k_keep_order(
+    const uint8_t *__restrict__ flags, int cap, const int64_t *__restrict__ d_count,
+    const int32_t *__restrict__ part, int nb, int direct, int64_t *__restrict__ d_kept,
+    int *__restrict__ order) {
+    __shared__ int lds_waves[kKeepThreads / kWave];
+    __shared__ long long lds_pre[kKeepThreads / kWave][2];
+    __shared__ int s_pos[kKeepTile];  // kept from the front, culled from the back
+    const int np = live_pairs(cap, d_count);
+    const int b = blockIdx.x;
+    const int64_t base = (int64_t)b * kKeepTile;
+    if (base >= np) {  // uniform: no pair in this block
+        if (b == 0 && direct && threadIdx.x == 0) *d_kept = 0;
+        return;
+    }
+    long long prefix = 0;
+    if (direct) {
+        long long pre = 0, all = 0;
+        for (int j = threadIdx.x; j < nb; j += kKeepThreads) {
+            const int v = part[j];
+            pre += j < b ? v : 0;
+            all += v;
+        }
+#pragma unroll
+        for (int o = kWave / 2; o >= 1; o >>= 1) {
+            pre += __shfl_xor(pre, o, kWave);
+            all += __shfl_xor(all, o, kWave);
+        }
+        if ((threadIdx.x & (kWave - 1)) == 0) {
+            lds_pre[threadIdx.x / kWave][0] = pre;
+            lds_pre[threadIdx.x / kWave][1] = all;
+        }
+        __syncthreads();
+        long long tot = 0;
+#pragma unroll
+        for (int w = 0; w < kKeepThreads / kWave; ++w) {
+            prefix += lds_pre[w][0];
+            tot += lds_pre[w][1];
+        }
+        if (b == 0 && threadIdx.x == 0) *d_kept = tot;
+    } else {
+        prefix = part[b];
+    }
+    const int i_loc = threadIdx.x * kKeepItems;
+    int valid;
+    const unsigned m = keep_mask(flags, base + i_loc, np, &valid);
+    int kept_blk;
+    int kept = scan_detail::block_exclusive(__popc(m), lds_waves, &kept_blk);
+    int culled = i_loc - kept;  // culled pairs of the block before this thread's
+    for (int k = 0; k < valid; ++k) {
+        if ((m >> k) & 1u)
+            s_pos[kept++] = (int)(base + i_loc + k);
+        else
+            s_pos[kKeepTile - 1 - culled++] = (int)(base + i_loc + k);
+    }
+    __syncthreads();
+    const int n_blk = (int)min<int64_t>(kKeepTile, (int64_t)np - base);
+    const int culled_blk = n_blk - kept_blk;
+    const int64_t culled_before = base - prefix;  // every pair before the block is below np
+    for (int j = threadIdx.x; j < kept_blk; j += kKeepThreads) order[prefix + j] = s_pos[j];
+    for (int j = threadIdx.x; j < culled_blk; j += kKeepThreads)
+        order[np - 1 - culled_before - j] = s_pos[kKeepTile - 1 - j];
+}
+
+
 // Which tiles the wave's pairs lie in (cheap: one coalesced load and ballots).
 template <int C>
 __device__ __forceinline__ bool bwd_slots(const BwdArgs &a, int64_t p0, BwdLane<C> &L,
                                           uint64_t &starts, int &nslots) {
     const int lane = threadIdx.x;
-    const int64_t p = p0 + lane;
-    int tile = p < a.n_isect ? a.pair_tiles[p] : -1;
+    const int64_t q = p0 + lane;
+    L.p = q < a.n_work ? bwd_pair(a, q) : -1;
+    int tile = L.p >= 0 ? a.pair_tiles[L.p] : -1;
     if (tile < 0 || tile >= a.T) tile = -1;
     L.tile = tile;
     L.valid = tile >= 0;
@@ -605,7 +780,7 @@ __device__ __forceinline__ bool bwd_slots(const BwdArgs &a, int64_t p0, BwdLane<
 
 // The lane's Gaussian, its gate and its offsets from the tile centre.
 template <int C>
-__device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, int64_t p0, BwdLane<C> &L) {
+__device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
     L.live = L.fast = false;
     L.g = 0;
     L.mxl = L.myl = L.mzl = 0.f;
@@ -615,7 +790,7 @@ __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, int64_t p0, BwdLa
     L.gt = make_gate(0.f);
     L.tg = tile_geom(L.valid ? L.tile : 0, a.Tx, a.Ty, a.D, a.H, a.W);
     if (!L.valid) return;
-    const int g = a.ids[p0 + threadIdx.x];
+    const int g = a.ids[L.p];
     L.g = g;
     if ((unsigned)g >= (unsigned)a.n) return;
     const float4 pr = a.pos_radii[g];
@@ -845,21 +1020,12 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
     const int g = L.g;
     if (a.partial != nullptr) {
         // Deterministic path: this pair's partial goes to its emission slot
-        // e = cum[g-1] + ((tz-min.z)*ny + (ty-min.y))*nx + (tx-min.x), the order
-        // the pairs were duplicated in (gaussian-major, tiles z->y->x), so each
-        // Gaussian's partials are contiguous for the reduction pass.
-        if ((unsigned)g < (unsigned)a.n) {
-            const int tx = L.tg.x0 / GSV_TILE, ty = L.tg.y0 / GSV_TILE, tz = L.tg.z0 / GSV_TILE;
-            const int mnx = a.tile_min[3 * g], mny = a.tile_min[3 * g + 1];
-            const int mnz = a.tile_min[3 * g + 2];
-            const int nxb = a.tile_max[3 * g] - mnx, nyb = a.tile_max[3 * g + 1] - mny;
-            const int64_t base = g == 0 ? 0 : a.cum[g - 1];
-            const int64_t e = base + ((int64_t)(tz - mnz) * nyb + (ty - mny)) * nxb + (tx - mnx);
-            if (e >= base && e < (int64_t)a.cum[g] && e < a.n_isect) {
-                float *dst = a.partial + e * (9 + C);
+        const int64_t e = emission_slot(g, L.tile, a.n, a.Tx, a.Ty, a.tile_min, a.tile_max, a.cum,
+                                        a.n_isect);
+        if (e >= 0) {
+            float *dst = a.partial + e * (9 + C);
 #pragma unroll
-                for (int q = 0; q < 9 + C; ++q) dst[q] = out[q];
-            }
+            for (int q = 0; q < 9 + C; ++q) dst[q] = out[q];
         }
     } else if (L.live) {
         float *dc = a.dconic + 6 * (size_t)g;
@@ -874,27 +1040,55 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
     }
 }
 
-// One wave per 64 consecutive (tile, Gaussian) pairs of the sorted list, lane
-// = pair, so no lane idles except in the last wave.  The wave stages the
+// The zero partials of the pairs the forward culled, spread over the W work
+// waves: wave wv writes those of culled items [wv*c, (wv+1)*c), c =
+// ceil(culled / W), one lane per pair.
+template <int C>
+__device__ __forceinline__ void bwd_zero_culled(const BwdArgs &a, int64_t wv, int64_t W) {
+    const int64_t culled = (int64_t)a.n_isect - a.n_work;
+    if (culled <= 0) return;
+    const int64_t c = (culled + W - 1) / W;
+    const int64_t q1 = min<int64_t>(culled, (wv + 1) * c);
+    for (int64_t q = wv * c + threadIdx.x; q < q1; q += kWave) {
+        const int p = a.order[a.n_isect - 1 - q];
+        const int t = a.pair_tiles[p];
+        if (t < 0 || t >= a.T) continue;
+        const int64_t e = emission_slot(a.ids[p], t, a.n, a.Tx, a.Ty, a.tile_min, a.tile_max,
+                                        a.cum, a.n_isect);
+        if (e < 0) continue;
+        float *dst = a.partial + e * (9 + C);
+#pragma unroll
+        for (int k = 0; k < 9 + C; ++k) dst[k] = 0.f;
+    }
+}
+
+// One wave per 64 consecutive (tile, Gaussian) pairs of the sorted list (or of
+// the work list of kept pairs), lane = pair, so no lane idles except in the
+// last wave.  The wave stages the
 // first K tiles its pairs span (lane = row; each lane reads its own tile's
 // rows); the pairs of further tiles are left to k_vox_bwd_rest.
 template <int C, int K>
 __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
     __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
-    a.n_isect = live_pairs(a.n_isect, a.d_count);
+    bwd_counts(a);
     // XCD slabs sized by the live wave count (the grid may be sized for a
     // larger capacity), so every XCD gets an equal share; blocks past the
-    // slabs would alias waves of other blocks and leave
-    const int64_t per = xcd_per(((int64_t)a.n_isect + kWave - 1) / kWave);
+    // slabs would alias waves of other blocks and leave.  With a work list at
+    // least one wave runs, for the culled pairs' zeros.
+    const bool zeros = a.order != nullptr && a.partial != nullptr;
+    const int64_t waves = ((int64_t)a.n_work + kWave - 1) / kWave;
+    const int64_t W = zeros ? max<int64_t>(waves, 1) : waves;
+    const int64_t per = xcd_per(W);
     if ((int64_t)(blockIdx.x / kXcds) >= per) return;
     const int64_t wv = xcd_remap(blockIdx.x, per);
+    if (zeros) bwd_zero_culled<C>(a, wv, W);
     const int64_t p0 = wv * kWave;
-    if (p0 >= a.n_isect) return;
+    if (p0 >= a.n_work) return;
     BwdLane<C> L;
     uint64_t starts;
     int nslots;
     if (!bwd_slots(a, p0, L, starts, nslots)) return;
-    bwd_gaussian(a, p0, L);
+    bwd_gaussian(a, L);
     // one wave-uniform choice: gate-free unless a live lane needs the exact gate
     const bool wave_fast = __all(!L.live || L.fast);
     const bool any_live = __any(L.live);
@@ -915,16 +1109,16 @@ constexpr int kRestBlocks = 512;
 template <int C, int K>
 __global__ __launch_bounds__(kWave) void k_vox_bwd_rest(BwdArgs a) {
     __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
-    a.n_isect = live_pairs(a.n_isect, a.d_count);
-    const int64_t waves = ((int64_t)a.n_isect + kWave - 1) / kWave;
+    bwd_counts(a);
+    const int64_t waves = ((int64_t)a.n_work + kWave - 1) / kWave;
     const int64_t G = gridDim.x;
     for (int64_t base = blockIdx.x; base < waves; base += G * kWave) {
         const int64_t w = base + (int64_t)threadIdx.x * G;
         bool maybe = false;
         if (w < waves) {
             const int64_t p0 = w * kWave;
-            const int64_t p1 = min<int64_t>(p0 + kWave, a.n_isect) - 1;
-            const int t0 = a.pair_tiles[p0], t1 = a.pair_tiles[p1];
+            const int64_t p1 = min<int64_t>(p0 + kWave, a.n_work) - 1;
+            const int t0 = a.pair_tiles[bwd_pair(a, p0)], t1 = a.pair_tiles[bwd_pair(a, p1)];
             maybe = !(t0 >= 0 && t1 < a.T && t1 >= t0 && t1 - t0 < K);
         }
         for (uint64_t m = __ballot(maybe); m; m &= m - 1) {
@@ -933,7 +1127,7 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd_rest(BwdArgs a) {
             uint64_t starts;
             int nslots;
             if (!bwd_slots(a, p0, L, starts, nslots) || nslots <= K) continue;
-            bwd_gaussian(a, p0, L);
+            bwd_gaussian(a, L);
             const bool wave_fast = __all(!L.live || L.fast);
             const bool any_live = __any(L.live);
             if (!any_live && a.partial == nullptr) continue;
@@ -1003,19 +1197,23 @@ __global__ __launch_bounds__(kReduceThreads) void k_pair_reduce(
 }
 
 struct BwdLayout {
-    size_t tiles, partial, end;
+    size_t tiles, partial, order, part, kept, end;
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 // pair -> tile map (n_isect ints; unused when the caller passes the binning's
-// sorted keys), then the per-pair partials in pairs mode.
+// sorted keys), the per-pair partials in pairs mode, then the work list of the
+// culled mode (order, the per-block counts and the kept count).
 BwdLayout bwd_layout(int64_t n_isect, int channels, bool pairs) {
     BwdLayout L{};
     size_t off = 0;
     L.tiles = off; off += align256((size_t)imax64(n_isect, 1) * 4);
     L.partial = off;
     if (pairs) off += align256((size_t)n_isect * (9 + channels) * 4);
+    L.order = off; off += align256((size_t)imax64(n_isect, 1) * 4);
+    L.part = off; off += align256((size_t)((n_isect + kKeepTile - 1) / kKeepTile + 1) * 4);
+    L.kept = off; off += 256;
     L.end = off;
     return L;
 }
@@ -1034,7 +1232,7 @@ int voxelize_fwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
                       int64_t num_intersects, const int32_t *ids, const int32_t *tile_bins,
                       const float *pos3d_radii, const float *conics, const float *intensities,
                       float *volume, const float *target, float *tile_loss, int8_t *sgn,
-                      float *loss, hipStream_t s) {
+                      float *loss, uint8_t *pair_live, hipStream_t s) {
     if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
     if (n < 0 || D <= 0 || H <= 0 || W <= 0 || !volume || !tile_bins) return GSV_ERR_INVALID_ARGUMENT;
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
@@ -1056,7 +1254,7 @@ int voxelize_fwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
                        reinterpret_cast<const int2 *>(tile_bins),                                  \
                        reinterpret_cast<const float4 *>(pos3d_radii),                              \
                        reinterpret_cast<const float2 *>(conics), intensities, volume, target,      \
-                       tile_loss, sgn)
+                       tile_loss, sgn, pair_live)
         switch (channels) {
             case 1: GSV_VF(1); break;
             case 2: GSV_VF(2); break;
@@ -1083,8 +1281,9 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
                       const float *intensities, const float *vol_grad, const int8_t *l1_sgn,
                       const float *l1_grad, const int32_t *tile_min,
                       const int32_t *tile_max, const int32_t *cum_tiles_hit,
-                      const int32_t *tiles_sorted, const int64_t *count_dev, float *dpos3d_radii,
-                      float *dconics, float *dintensities, int32_t variant, void *workspace,
+                      const int32_t *tiles_sorted, const int64_t *count_dev,
+                      const uint8_t *pair_live, float *dpos3d_radii, float *dconics,
+                      float *dintensities, int32_t variant, void *workspace,
                       size_t workspace_bytes, hipStream_t s) {
     if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
     if (n < 0 || D <= 0 || H <= 0 || W <= 0 || (variant != 0 && variant != 1))
@@ -1122,6 +1321,29 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
         if (int st = check_launch()) return st;
         pair_tiles = own;
     }
+    const int *order = nullptr;
+    const int64_t *d_work = nullptr;
+    if (pair_live) {  // the work list of the pairs the forward kept
+        if (!aligned(pair_live, 16)) return GSV_ERR_INVALID_ARGUMENT;
+        int *ord = reinterpret_cast<int *>(ws + L.order);
+        int32_t *part = reinterpret_cast<int32_t *>(ws + L.part);
+        int64_t *kept = reinterpret_cast<int64_t *>(ws + L.kept);
+        const int64_t nb = (num_intersects + kKeepTile - 1) / kKeepTile;
+        const int direct = nb <= 2048 ? 1 : 0;
+        hipLaunchKernelGGL(k_keep_count, dim3((unsigned)nb), dim3(kKeepThreads), 0, s, pair_live,
+                           ni, count_dev, part);
+        if (int st = check_launch()) return st;
+        if (!direct) {
+            hipLaunchKernelGGL(scan_detail::k_scan_block_sums, dim3(1), dim3(kKeepThreads), 0, s,
+                               part, nb, kept, nullptr);
+            if (int st = check_launch()) return st;
+        }
+        hipLaunchKernelGGL(k_keep_order, dim3((unsigned)nb), dim3(kKeepThreads), 0, s, pair_live,
+                           ni, count_dev, part, (int)nb, direct, kept, ord);
+        if (int st = check_launch()) return st;
+        order = ord;
+        d_work = kept;
+    }
     const int64_t waves = (num_intersects + kWave - 1) / kWave;
     const int64_t per = xcd_per(waves);
     const dim3 grid((unsigned)(kXcds * per)), block(kWave);
@@ -1138,6 +1360,9 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     args.tile_min = tile_min; args.tile_max = tile_max; args.cum = cum_tiles_hit;
     args.partial = partial;
     args.d_count = count_dev;
+    args.order = order;
+    args.d_work = d_work;
+    args.n_work = 0;
 #define GSV_VB(CH)                                                                                  \
     {                                                                                               \
         KernelTimer timer(kTimedVoxBwd, s);                                                         \
@@ -1174,10 +1399,10 @@ extern "C" int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channel
                                 int64_t num_intersects, const int32_t *gaussian_ids_sorted,
                                 const int32_t *tile_bins, const float *pos3d_radii,
                                 const float *conics, const float *intensities, float *volume,
-                                void *stream) {
+                                uint8_t *pair_live, void *stream) {
     return voxelize_fwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
                              pos3d_radii, conics, intensities, volume, nullptr, nullptr, nullptr,
-                             nullptr, as_stream(stream));
+                             nullptr, pair_live, as_stream(stream));
 }
 
 extern "C" int gsv_voxelize_fwd_l1_workspace_bytes(int32_t D, int32_t H, int32_t W,
@@ -1193,14 +1418,16 @@ extern "C" int gsv_voxelize_fwd_l1(int32_t D, int32_t H, int32_t W, int32_t chan
                                    const int32_t *tile_bins, const float *pos3d_radii,
                                    const float *conics, const float *intensities,
                                    const float *target, float *volume, int8_t *sign, float *loss,
-                                   void *workspace, size_t workspace_bytes, void *stream) {
+                                   uint8_t *pair_live, void *workspace, size_t workspace_bytes,
+                                   void *stream) {
     if (!target || !loss || !sign) return GSV_ERR_INVALID_ARGUMENT;
     size_t need = 0;
     if (int st = gsv_voxelize_fwd_l1_workspace_bytes(D, H, W, &need)) return st;
     if (!workspace || workspace_bytes < need) return GSV_ERR_WORKSPACE_TOO_SMALL;
     return voxelize_fwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
                              pos3d_radii, conics, intensities, volume, target,
-                             static_cast<float *>(workspace), sign, loss, as_stream(stream));
+                             static_cast<float *>(workspace), sign, loss, pair_live,
+                             as_stream(stream));
 }
 
 extern "C" int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W,
@@ -1219,13 +1446,13 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
                                 const float *vol_grad, const int32_t *tile_min,
                                 const int32_t *tile_max, const int32_t *cum_tiles_hit,
                                 const int32_t *tiles_sorted, const int64_t *num_intersects_dev,
-                                float *dpos3d_radii, float *dconics, float *dintensities,
-                                int32_t variant, void *workspace, size_t workspace_bytes,
-                                void *stream) {
+                                const uint8_t *pair_live, float *dpos3d_radii, float *dconics,
+                                float *dintensities, int32_t variant, void *workspace,
+                                size_t workspace_bytes, void *stream) {
     return voxelize_bwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
                              pos3d_radii, conics, intensities, vol_grad, nullptr, nullptr,
                              tile_min, tile_max, cum_tiles_hit, tiles_sorted, num_intersects_dev,
-                             dpos3d_radii, dconics,
+                             pair_live, dpos3d_radii, dconics,
                              dintensities, variant, workspace, workspace_bytes, as_stream(stream));
 }
 
@@ -1237,13 +1464,13 @@ extern "C" int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t chan
                                    const float *vol_grad, const int32_t *tile_min,
                                    const int32_t *tile_max, const int32_t *cum_tiles_hit,
                                    const int32_t *tiles_sorted, const int64_t *num_intersects_dev,
-                                   float *dpos3d_radii, float *dconics, float *dintensities,
-                                   int32_t variant, void *workspace, size_t workspace_bytes,
-                                   void *stream) {
+                                   const uint8_t *pair_live, float *dpos3d_radii, float *dconics,
+                                   float *dintensities, int32_t variant, void *workspace,
+                                   size_t workspace_bytes, void *stream) {
     if (!sign || !grad_loss) return GSV_ERR_INVALID_ARGUMENT;
     return voxelize_bwd_impl(D, H, W, channels, n, num_intersects, gaussian_ids_sorted, tile_bins,
                              pos3d_radii, conics, intensities, vol_grad, sign, grad_loss,
                              tile_min, tile_max, cum_tiles_hit, tiles_sorted, num_intersects_dev,
-                             dpos3d_radii, dconics,
+                             pair_live, dpos3d_radii, dconics,
                              dintensities, variant, workspace, workspace_bytes, as_stream(stream));
 }

@@ -33,17 +33,17 @@ SIGNATURES = {
     "gsv_bin_and_sort_device_count": [_c_int, _c_i64, _P, _P, _P, _P, _c_int, _c_int, _c_int, _P,
                                       _c_size_t, _P, _P, _P, _P],
     "gsv_voxelize_fwd": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P, _P,
-                         _P],
+                         _P, _P],
     "gsv_voxelize_fwd_l1_workspace_bytes": [_c_int, _c_int, _c_int, ctypes.POINTER(_c_size_t)],
     "gsv_voxelize_fwd_l1": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P,
-                            _P, _P, _P, _P, _P, _c_size_t, _P],
+                            _P, _P, _P, _P, _P, _P, _c_size_t, _P],
     "gsv_voxelize_bwd_workspace_bytes": [_c_int, _c_int, _c_int, _c_int, _c_i64, _c_int,
                                          ctypes.POINTER(_c_size_t)],
     "gsv_voxelize_bwd": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P, _P,
-                         _P, _P, _P, _P, _P, _P, _P, _P, _c_int, _P, _c_size_t, _P],
+                         _P, _P, _P, _P, _P, _P, _P, _P, _P, _c_int, _P, _c_size_t, _P],
     "gsv_voxelize_bwd_l1": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P,
-                            _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _c_int, _P, _c_size_t,
-                            _P],
+                            _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _c_int, _P,
+                            _c_size_t, _P],
     "gsv_kernel_timing_enable": [_c_int],
     "gsv_kernel_timing_collect": [_c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_int)],
 }

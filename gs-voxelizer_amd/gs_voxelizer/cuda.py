@@ -223,8 +223,25 @@ def _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
         _check_dtype(t, w, torch.float32)
 
 
-def voxelize_forward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities):
-    """bindings.cu:362-457. Returns the (D, H, W, C) volume."""
+def _pair_flags(pair_live, n_pairs):
+    """ctypes pointer of the optional per-pair cull flags (uint8, >= n_pairs)."""
+    if pair_live is None:
+        return ctypes.c_void_p(0)
+    _check_input(pair_live, "pair_live")
+    _check_dtype(pair_live, "pair_live", torch.uint8)
+    if pair_live.numel() < n_pairs:
+        raise RuntimeError("pair_live must hold one byte per sorted pair")
+    return _ptr(pair_live)
+
+
+def voxelize_forward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
+                     pair_live=None):
+    """bindings.cu:362-457. Returns the (D, H, W, C) volume.
+
+    pair_live (optional, uint8, one per sorted pair) receives 1 for every pair
+    the kernel evaluated and 0 for each it culled (no voxel centre of the tile
+    inside the Gaussian's gate); handing it to the backward skips those pairs
+    there too."""
     _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
     channels = _channels(intensities)
     D, H, W = (int(v) for v in vol_size)
@@ -237,7 +254,8 @@ def voxelize_forward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, in
     with torch.cuda.device(dev):
         _call("voxelize_fwd", D, H, W, channels, n, gaussian_ids_sorted.numel(),
               _ptr(gaussian_ids_sorted), _ptr(tile_bins), _ptr(pos3d), _ptr(conics),
-              _ptr(intensities), _ptr(out), _stream(dev))
+              _ptr(intensities), _ptr(out), _pair_flags(pair_live, gaussian_ids_sorted.numel()),
+              _stream(dev))
     return out
 
 
@@ -256,11 +274,11 @@ def _l1_target(target, volume):
 
 
 def voxelize_forward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
-                        target):
+                        target, pair_live=None):
     """voxelize_forward fused with torch.nn.functional.l1_loss(volume, target) (mean).
     Returns (volume (D, H, W, C), loss (0-d device tensor), sign): sign is
     sgn(volume - target) as int8 (2 where the difference is NaN), kept for
-    voxelize_backward_l1."""
+    voxelize_backward_l1.  pair_live as in voxelize_forward."""
     _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
     channels = _channels(intensities)
     D, H, W = (int(v) for v in vol_size)
@@ -279,18 +297,22 @@ def voxelize_forward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
     with torch.cuda.device(dev):
         _call("voxelize_fwd_l1", D, H, W, channels, n, gaussian_ids_sorted.numel(),
               _ptr(gaussian_ids_sorted), _ptr(tile_bins), _ptr(pos3d), _ptr(conics),
-              _ptr(intensities), _ptr(target), _ptr(out), _ptr(sign), _ptr(loss), _ptr(ws),
-              nbytes.value, _stream(dev))
+              _ptr(intensities), _ptr(target), _ptr(out), _ptr(sign), _ptr(loss),
+              _pair_flags(pair_live, gaussian_ids_sorted.numel()), _ptr(ws), nbytes.value,
+              _stream(dev))
     return out, loss, sign
 
 
 def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                        intensities, vol_grad_in, tile_min=None, tile_max=None,
-                       cum_tiles_hit=None, l1=None, tiles_sorted=None, count_dev=None):
+                       cum_tiles_hit=None, l1=None, tiles_sorted=None, count_dev=None,
+                       pair_live=None):
     """l1 = (sign, grad_loss): the fused L1 source, with vol_grad_in optional.
     tiles_sorted: the binning's tile id per sorted pair (return_tiles), optional.
     count_dev: (1,) int64 device tensor with the live pair count, when the id
-    arrays are capacity-sized (bin_and_sort_gaussians_device_count); optional."""
+    arrays are capacity-sized (bin_and_sort_gaussians_device_count); optional.
+    pair_live: the forward's cull flags (voxelize_forward(..., pair_live=)),
+    optional; the backward then skips the culled pairs (same gradients)."""
     _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
     given = [t is not None for t in (tile_min, tile_max, cum_tiles_hit)]
     if any(given) and not all(given):
@@ -344,16 +366,17 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
     vg = _ptr(vol_grad_in) if vol_grad_in is not None else null
     ts = _ptr(tiles_sorted) if tiles_sorted is not None else null
     cd = _ptr(count_dev) if count_dev is not None else null
+    pl = _pair_flags(pair_live, I)
     with torch.cuda.device(dev):
         if l1 is None:
             _call("voxelize_bwd", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted),
                   _ptr(tile_bins), _ptr(pos3d), _ptr(conics), _ptr(intensities), vg, *boxes, ts,
-                  cd, _ptr(dpos), _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value,
+                  cd, pl, _ptr(dpos), _ptr(dconics), _ptr(dint), variant, _ptr(ws), nbytes.value,
                   _stream(dev))
         else:
             _call("voxelize_bwd_l1", D, H, W, channels, n, I, _ptr(gaussian_ids_sorted),
                   _ptr(tile_bins), _ptr(pos3d), _ptr(conics), _ptr(intensities), _ptr(sign),
-                  _ptr(grad_loss), vg, *boxes, ts, cd, _ptr(dpos), _ptr(dconics), _ptr(dint),
+                  _ptr(grad_loss), vg, *boxes, ts, cd, pl, _ptr(dpos), _ptr(dconics), _ptr(dint),
                   variant, _ptr(ws), nbytes.value, _stream(dev))
     return dpos, dconics, dint
 
@@ -361,19 +384,19 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
 def voxelize_backward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
                          sign, grad_loss, vol_grad_in=None, tile_min=None, tile_max=None,
                          cum_tiles_hit=None, per_gaussian=True, tiles_sorted=None,
-                         count_dev=None):
+                         count_dev=None, pair_live=None):
     """Backward of voxelize_forward_l1: dL/dvolume = sign * grad_loss / numel (+
     vol_grad_in, the volume's gradient from other uses, when given), never
     materialised.  Returns (dpos3d_radii, dconics, dintensities)."""
     return _voxelize_backward(1 if per_gaussian else 0, vol_size, gaussian_ids_sorted, tile_bins,
                               pos3d, conics, intensities, vol_grad_in, tile_min, tile_max,
                               cum_tiles_hit, l1=(sign, grad_loss), tiles_sorted=tiles_sorted,
-                              count_dev=count_dev)
+                              count_dev=count_dev, pair_live=pair_live)
 
 
 def voxelize_backward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, intensities,
                       vol_grad_in, tile_min=None, tile_max=None, cum_tiles_hit=None,
-                      tiles_sorted=None, count_dev=None):
+                      tiles_sorted=None, count_dev=None, pair_live=None):
     """bindings.cu:459-584 (per-voxel variant). Returns (dpos3d_radii, dconics, dintensities).
 
     The optional tile_min / tile_max / cum_tiles_hit (the projection's tile boxes
@@ -381,17 +404,21 @@ def voxelize_backward(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics, i
     reproducible reduction; without them float atomics are used, as in the
     reference.  tiles_sorted (bin_and_sort_gaussians(..., return_tiles=True)) saves
     rebuilding the tile of each pair; count_dev gives the live pair count for
-    capacity-sized id arrays."""
+    capacity-sized id arrays; pair_live (the forward's cull flags) skips the pairs
+    the forward culled."""
     return _voxelize_backward(0, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                               intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit,
-                              tiles_sorted=tiles_sorted, count_dev=count_dev)
+                              tiles_sorted=tiles_sorted, count_dev=count_dev,
+                              pair_live=pair_live)
 
 
 def voxelize_backward_per_gaussian(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                                    intensities, vol_grad_in, tile_min=None, tile_max=None,
-                                   cum_tiles_hit=None, tiles_sorted=None, count_dev=None):
+                                   cum_tiles_hit=None, tiles_sorted=None, count_dev=None,
+                                   pair_live=None):
     """bindings.cu:586-781 (per-Gaussian variant). Returns (dpos3d_radii, dconics, dintensities).
     Optional arguments as in voxelize_backward."""
     return _voxelize_backward(1, vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                               intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit,
-                              tiles_sorted=tiles_sorted, count_dev=count_dev)
+                              tiles_sorted=tiles_sorted, count_dev=count_dev,
+                              pair_live=pair_live)

@@ -188,16 +188,21 @@ class _VoxelizeGaussians(Function):
         gaussian_ids_sorted = tile_bins = None
         ctx.num_intersects = 0
         if num_gaussians > 0:
-            fwd = lambda ids, bins: _C.voxelize_forward(vol_size_voxel, ids, bins, pos3d_radii,
-                                                        conics, intensities)
-            I, gaussian_ids_sorted, tile_bins, tiles, cum_tiles_hit, out, count = _bin_and_forward(
+            def fwd(ids, bins):
+                live = torch.empty(ids.numel(), device=dev, dtype=torch.uint8)
+                return _C.voxelize_forward(vol_size_voxel, ids, bins, pos3d_radii, conics,
+                                           intensities, pair_live=live), live
+            I, gaussian_ids_sorted, tile_bins, tiles, cum_tiles_hit, res, count = _bin_and_forward(
                 num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd)
             ctx.num_intersects = I
-            # the backward reduces per-pair partials in duplication order (no
-            # atomics) and takes each sorted pair's tile from the binning
-            boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit, tiles)
-            if count is not None:  # captured: capacity-sized arrays, live count on the device
-                boxes += (count,)
+            if I >= 1:
+                out, live = res
+                # the backward reduces per-pair partials in duplication order (no
+                # atomics), takes each sorted pair's tile from the binning and
+                # skips the pairs the forward culled
+                boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit, tiles, live)
+                if count is not None:  # captured: capacity-sized arrays, live count on device
+                    boxes += (count,)
         if ctx.num_intersects < 1:
             out = torch.zeros(D, H, W, C, device=dev, dtype=pos3d_radii.dtype)
             gaussian_ids_sorted = torch.zeros(0, 1, device=dev, dtype=torch.int32)
@@ -214,7 +219,8 @@ class _VoxelizeGaussians(Function):
         saved = ctx.saved_tensors
         pos3d_radii, conics, intensities, gaussian_ids_sorted, tile_bins = saved[:5]
         boxes, tiles = saved[5:8], (saved[8] if len(saved) > 8 else None)
-        count = saved[9] if len(saved) > 9 else None
+        live = saved[9] if len(saved) > 9 else None
+        count = saved[10] if len(saved) > 10 else None
         if ctx.num_intersects < 1 or vol_grad is None:
             pos3d_grad = torch.zeros_like(pos3d_radii)
             conics_grad = torch.zeros_like(conics)
@@ -224,7 +230,7 @@ class _VoxelizeGaussians(Function):
                   else _C.voxelize_backward)
             pos3d_grad, conics_grad, intensities_grad = fn(
                 vol_size_voxel, gaussian_ids_sorted, tile_bins, pos3d_radii, conics, intensities,
-                vol_grad.contiguous(), *boxes, tiles_sorted=tiles, count_dev=count)
+                vol_grad.contiguous(), *boxes, tiles_sorted=tiles, count_dev=count, pair_live=live)
         return pos3d_grad, conics_grad, intensities_grad, None, None, None, None, None
 
 
@@ -275,17 +281,21 @@ class _VoxelizeL1(Function):
         dev = pos3d_radii.device
         D, H, W = (int(v) for v in vol_size_voxel)
         C = intensities.shape[-1]
-        fwd = lambda ids, bins: _C.voxelize_forward_l1(vol_size_voxel, ids, bins, pos3d_radii,
-                                                       conics, intensities, target)
+        def fwd(ids, bins):
+            live = torch.empty(ids.numel(), device=dev, dtype=torch.uint8)
+            return _C.voxelize_forward_l1(vol_size_voxel, ids, bins, pos3d_radii, conics,
+                                          intensities, target, pair_live=live) + (live,)
         boxes = ()
         ctx.num_intersects = 0
         if num_gaussians > 0:
             I, ids, tile_bins, tiles, cum_tiles_hit, res, count = _bin_and_forward(
                 num_gaussians, vol_size_voxel, tile_min, tile_max, num_tiles_hit, fwd)
             ctx.num_intersects = I
-            boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit, tiles)
-            if count is not None:  # captured: capacity-sized arrays, live count on the device
-                boxes += (count,)
+            if I >= 1:
+                boxes = (tile_min.contiguous(), tile_max.contiguous(), cum_tiles_hit, tiles,
+                         res[3])
+                if count is not None:  # captured: capacity-sized arrays, live count on device
+                    boxes += (count,)
         if ctx.num_intersects < 1:
             # no Gaussian touches the volume: it is zero, the loss mean(|target|)
             empty_ids = torch.zeros(0, device=dev, dtype=torch.int32)
@@ -293,7 +303,7 @@ class _VoxelizeL1(Function):
             bins = torch.zeros(Tx * Ty * Tz, 2, device=dev, dtype=torch.int32)
             res = fwd(empty_ids, bins)
             ids, tile_bins, boxes = empty_ids, bins, ()
-        volume, loss, sign = res
+        volume, loss, sign = res[:3]
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(pos3d_radii, conics, intensities, ids, tile_bins, sign, *boxes)
         return loss, volume
@@ -303,7 +313,8 @@ class _VoxelizeL1(Function):
         saved = ctx.saved_tensors
         pos3d_radii, conics, intensities, ids, tile_bins, sign = saved[:6]
         boxes, tiles = saved[6:9], (saved[9] if len(saved) > 9 else None)
-        count = saved[10] if len(saved) > 10 else None
+        live = saved[10] if len(saved) > 10 else None
+        count = saved[11] if len(saved) > 11 else None
         if ctx.num_intersects < 1 or (grad_loss is None and grad_volume is None):
             z = (torch.zeros_like(pos3d_radii), torch.zeros_like(conics),
                  torch.zeros_like(intensities))
@@ -314,5 +325,6 @@ class _VoxelizeL1(Function):
                 ctx.vol_size_voxel, ids, tile_bins, pos3d_radii, conics, intensities, sign,
                 grad_loss.contiguous(),
                 grad_volume.contiguous() if grad_volume is not None else None, *boxes,
-                per_gaussian=ctx.use_per_gaussian_backward, tiles_sorted=tiles, count_dev=count)
+                per_gaussian=ctx.use_per_gaussian_backward, tiles_sorted=tiles, count_dev=count,
+                pair_live=live)
         return z[0], z[1], z[2], None, None, None, None, None, None

@@ -140,11 +140,17 @@ int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity, const int64_t *nu
  * Forward voxelization.  Replaces voxelize_forward_torch (bindings.cu:362-457;
  * kernel voxelize.cu:39-164).  volume (D,H,W,channels) float32 is fully written.
  * n = number of Gaussians (rows of pos3d_radii / conics / intensities).
+ * pair_live (optional, num_intersects bytes, one per sorted pair): receives 1
+ * for every pair the kernel evaluated and 0 for each it culled, i.e. whose
+ * tile holds no voxel centre inside the Gaussian's gate ellipsoid (such a pair
+ * adds nothing to the volume).  Handing it to the backward lets that skip the
+ * culled pairs too.
  */
 int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
                      int64_t num_intersects, const int32_t *gaussian_ids_sorted,
                      const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
-                     const float *intensities, float *volume, void *stream);
+                     const float *intensities, float *volume, uint8_t *pair_live,
+                     void *stream);
 
 /*
  * Backward voxelization.  Replaces voxelize_backward_per_gaussian_torch
@@ -171,6 +177,10 @@ int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
  * and workspace arrays and the grids are sized for (gsv_bin_and_sort_device_count
  * outputs), and the kernels process min(count, capacity) pairs.  With it the
  * backward needs no host-side count, so a caller can capture it in a graph.
+ * pair_live (optional): the flags the forward wrote (gsv_voxelize_fwd's
+ * pair_live, same pairs); the backward then evaluates only the pairs the
+ * forward kept and gives the culled ones a zero partial.  The gradients are
+ * the same bits as without it.
  * Workspace size from gsv_voxelize_bwd_workspace_bytes (deterministic = 1 for
  * the second mode).
  */
@@ -183,8 +193,9 @@ int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
                      const float *intensities, const float *vol_grad, const int32_t *tile_min,
                      const int32_t *tile_max, const int32_t *cum_tiles_hit,
                      const int32_t *tiles_sorted, const int64_t *num_intersects_dev,
-                     float *dpos3d_radii, float *dconics, float *dintensities, int32_t variant,
-                     void *workspace, size_t workspace_bytes, void *stream);
+                     const uint8_t *pair_live, float *dpos3d_radii, float *dconics,
+                     float *dintensities, int32_t variant, void *workspace,
+                     size_t workspace_bytes, void *stream);
 
 /*
  * Voxelization fused with an L1 loss.  These have no reference binding.  They
@@ -197,6 +208,7 @@ int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
  * out like volume.  The loss is summed per tile in binary32 and over tiles in
  * binary64 in a fixed order.  `sign` (int8, laid out like volume) receives
  * sgn(volume - target): -1, 0, 1, or 2 where the difference is NaN.
+ * pair_live as for gsv_voxelize_fwd.
  * Workspace: gsv_voxelize_fwd_l1_workspace_bytes.
  *
  * gsv_voxelize_bwd_l1: gsv_voxelize_bwd with vol_grad replaced by
@@ -210,17 +222,17 @@ int gsv_voxelize_fwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32
                         int64_t num_intersects, const int32_t *gaussian_ids_sorted,
                         const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
                         const float *intensities, const float *target, float *volume,
-                        int8_t *sign, float *loss, void *workspace, size_t workspace_bytes,
-                        void *stream);
+                        int8_t *sign, float *loss, uint8_t *pair_live, void *workspace,
+                        size_t workspace_bytes, void *stream);
 int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
                         int64_t num_intersects, const int32_t *gaussian_ids_sorted,
                         const int32_t *tile_bins, const float *pos3d_radii, const float *conics,
                         const float *intensities, const int8_t *sign, const float *grad_loss,
                         const float *vol_grad, const int32_t *tile_min, const int32_t *tile_max,
                         const int32_t *cum_tiles_hit, const int32_t *tiles_sorted,
-                        const int64_t *num_intersects_dev, float *dpos3d_radii, float *dconics,
-                        float *dintensities, int32_t variant, void *workspace,
-                        size_t workspace_bytes, void *stream);
+                        const int64_t *num_intersects_dev, const uint8_t *pair_live,
+                        float *dpos3d_radii, float *dconics, float *dintensities,
+                        int32_t variant, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Kernel timing (no counterpart in the reference; for benchmarks and

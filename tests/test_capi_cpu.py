@@ -47,8 +47,8 @@ def test_validation_without_device():
     assert L.gsv_project_fwd(*args) == 1
     args[0] = 0  # empty input is a no-op
     assert L.gsv_project_fwd(*args) == 0
-    assert L.gsv_voxelize_fwd(8, 8, 8, 0, 1, 1, *[null] * 6, null) == 2
-    assert L.gsv_voxelize_bwd(8, 8, 8, 1, 1, 1, *[null] * 14, 7, null, 0, null) == 1
+    assert L.gsv_voxelize_fwd(8, 8, 8, 0, 1, 1, *[null] * 7, null) == 2
+    assert L.gsv_voxelize_bwd(8, 8, 8, 1, 1, 1, *[null] * 15, 7, null, 0, null) == 1
 
 
 def test_workspace_sizes_are_host_only():
