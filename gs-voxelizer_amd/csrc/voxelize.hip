@@ -1064,9 +1064,9 @@ __device__ __forceinline__ void bwd_zero_culled(const BwdArgs &a, int64_t wv, in
 
 // One wave per 64 consecutive (tile, Gaussian) pairs of the sorted list (or of
 // the work list of kept pairs), lane = pair, so no lane idles except in the
-// last wave.  The wave stages the
-// first K tiles its pairs span (lane = row; each lane reads its own tile's
-// rows); the pairs of further tiles are left to k_vox_bwd_rest.
+// last wave.  The wave stages the first K tiles its pairs span (lane = row;
+// each lane reads its own tile's rows); the pairs of further tiles are left to
+// k_vox_bwd_rest.
 template <int C, int K>
 __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
     __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
