@@ -586,9 +586,10 @@ struct BwdArgs {
     const int *tile_min, *tile_max, *cum;
     float *partial;
     const int64_t *d_count;  // live pair count on the device (n_isect is then the capacity)
-    // Optional work list: the sorted positions of the pairs the forward's tile
-    // culling kept, ascending, *d_work of them; the culled pairs' partials are
-    // zero already.  Without it the work is every pair.
+    // Optional work list: order[0 .. *d_work) holds the sorted positions of the
+    // pairs the forward's tile culling kept, ascending, and order[n_isect - 1],
+    // order[n_isect - 2], ... the culled ones, whose zero partials k_vox_bwd
+    // writes.  Without it the work is every pair.
     const int *order;
     const int64_t *d_work;
     int n_work;  // work items, set by each kernel from the counts
@@ -613,8 +614,8 @@ __device__ __forceinline__ int bwd_pair(const BwdArgs &a, int64_t q) {
 }
 
 // One backward wave's view: lane = one of 64 consecutive work items (pairs of
-// the sorted list, or of the culled list); `slot` numbers the runs of equal
-// tiles.
+// the sorted list, or of the work list of kept pairs); `slot` numbers the runs
+// of equal tiles.
 template <int C>
 struct BwdLane {
     int tile, slot, g, p;

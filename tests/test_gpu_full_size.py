@@ -6,7 +6,8 @@
 - backward: the size-independent identity sum_g I_gc dL/dI_gc == sum_v vol_vc g_vc
   per channel (the volume is linear in each channel's intensities once the gate,
   which depends on the mean intensity, is fixed), with finiteness of every
-  gradient.
+  gradient; and the same bits when the backward takes the forward's cull flags
+  as its work list.
 """
 import numpy as np
 import pytest
@@ -96,3 +97,15 @@ def test_backward_intensity_identity(full):
     for t in (dp, dc, di):
         assert torch.isfinite(t).all()
     assert float(dp[:, 3].abs().sum()) == 0.0
+    # the forward's cull flags as the backward's work list (more than 2048
+    # blocks of flags here: the counts are scanned by one workgroup first)
+    live = torch.empty(P["I"], device=inten.device, dtype=torch.uint8)
+    vol2 = _C.voxelize_forward(cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"], inten,
+                               pair_live=live)
+    assert torch.equal(vol2, vol)
+    assert P["I"] > 2048 * 4096
+    got = _C.voxelize_backward_per_gaussian(cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"],
+                                            inten, g, P["tmin"], P["tmax"], P["cum"],
+                                            tiles_sorted=P["tiles"], pair_live=live)
+    for a, b in zip((dp, dc, di), got):
+        assert torch.equal(a, b)
