@@ -50,23 +50,32 @@ class CapturedStep:
         if self.capacity is None:
             raise RuntimeError("gs_voxelizer: the step ran no voxelization before capture")
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.outputs = self.step()
+        _vox.begin_capture()
+        try:
+            with torch.cuda.graph(self.graph):
+                self.outputs = self.step()
+        finally:
+            # (pinned count, capacity) of every voxelization in the step
+            self.counts = _vox.end_capture()
         torch.cuda.synchronize()
 
     def replay(self):
         """Runs the captured step; returns its (static) outputs.  Waits only for
-        the prefix sum of the replay, not for the whole step."""
-        host = _vox.count_buffer(self.device)
-        host.fill_(-1)
+        the prefix sums of the replay, not for the whole step."""
+        for host, _ in self.counts:
+            host.fill_(-1)
         self.graph.replay()
-        count = _vox._await_count(host, self.device)
-        if count > self.capacity:
-            # the replay sorted only a prefix of the intersections: grow the
-            # capacity, capture again and rerun
+        grown = 0
+        for host, cap in self.counts:
+            count = _vox._await_count(host, self.device)
+            if count > cap:
+                grown = max(grown, count)
+        if grown:
+            # the replay sorted only a prefix of some forward's intersections:
+            # grow the capacity, capture again and rerun
             torch.cuda.synchronize()
             key = self.device.index
-            _vox._capacity[key] = max(_vox._capacity.get(key) or 0, _vox._grow(count))
+            _vox._capacity[key] = max(_vox._capacity.get(key) or 0, _vox._grow(grown))
             self.recaptures += 1
             self._capture()
             return self.replay()

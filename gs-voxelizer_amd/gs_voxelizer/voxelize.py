@@ -14,6 +14,7 @@ above the capacity (the scene grew) reruns binning and the forward with the
 exact count and raises the capacity; results are identical either way.  GSV_SYNC_COUNT=1 restores the reference's host read.
 """
 import os
+import threading
 from typing import Tuple
 
 import torch
@@ -24,7 +25,10 @@ import gs_voxelizer.cuda as _C
 
 _INT32_MAX = 2**31 - 1
 _capacity = {}  # device index -> intersection capacity of the speculative path
-_count_host = {}  # device index -> pinned int64 the prefix-sum kernel writes the count into
+_SLOTS = 64  # pinned count slots per device, taken in turn by the forwards
+_slot_pool = {}  # device index -> [pinned int64 (_SLOTS,), next slot]
+_slot_lock = threading.Lock()
+_capture = threading.local()  # .counts: [(pinned count, capacity)] of the capture under way
 
 
 def _grow(count: int) -> int:
@@ -38,17 +42,37 @@ def _speculate() -> bool:
 _SPIN_READS = 1 << 21  # reads of the pinned count before falling back to a device sync
 
 
-def count_buffer(device=None) -> Tensor:
-    """The persistent pinned (1,) int64 that the forward's prefix-sum kernel
-    writes the intersection count of `device` into (also inside a captured
-    graph, at every replay)."""
-    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+def _count_slot(dev: torch.device) -> Tensor:
+    """A pinned (1,) int64 for one eager forward's pair count.  Slots are taken
+    in turn from a per-device pool, so forwards running at the same time on
+    other streams or threads write their own (a forward reads its slot before it
+    returns, long before the pool comes round to it again)."""
     key = dev.index if dev.index is not None else torch.cuda.current_device()
-    buf = _count_host.get(key)
-    if buf is None:
-        buf = torch.empty((1,), dtype=torch.int64, pin_memory=True)
-        _count_host[key] = buf
-    return buf
+    with _slot_lock:
+        pool = _slot_pool.get(key)
+        if pool is None:
+            pool = [torch.empty((_SLOTS,), dtype=torch.int64, pin_memory=True), 0]
+            _slot_pool[key] = pool
+        i = pool[1]
+        pool[1] = (i + 1) % _SLOTS
+    return pool[0][i:i + 1]
+
+
+def begin_capture(max_forwards: int = 16) -> None:
+    """Prepare the graph capture that follows on this thread: pinned counts
+    (allocated here, outside the capture) for up to `max_forwards` captured
+    forwards, each written by its prefix-sum kernel at every replay."""
+    _capture.free = [torch.empty((1,), dtype=torch.int64, pin_memory=True)
+                     for _ in range(max(int(max_forwards), 1))]
+    _capture.counts = []
+
+
+def end_capture():
+    """[(pinned (1,) int64 count, capacity the arrays were captured with)], one
+    per forward captured since begin_capture()."""
+    counts = getattr(_capture, "counts", None) or []
+    _capture.counts = _capture.free = None
+    return counts
 
 
 def capacity(device=None):
@@ -119,8 +143,9 @@ def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tile
 
     Under graph capture nothing is read back: the arrays keep the recorded
     capacity, num_intersects is that capacity and count_dev (the live count on
-    the device) bounds the backward; the replay's count lands in count_buffer()
-    for the caller to check against capacity() (gs_voxelizer.graph does)."""
+    the device) bounds the backward; each replay's count lands in a pinned
+    buffer of this forward's own, listed by end_capture() with the capacity for
+    the caller to check (gs_voxelizer.graph does)."""
     dev = num_tiles_hit.device
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     cap = _capacity.get(key) if _speculate() else None
@@ -130,8 +155,14 @@ def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tile
                 "gs_voxelizer: run the step once outside graph capture first (it records the "
                 "intersection capacity the captured arrays are sized for), and leave "
                 "GSV_SYNC_COUNT unset")
-        cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous(),
-                                                   total_host=count_buffer(dev))
+        free = getattr(_capture, "free", None)
+        if not free:
+            raise RuntimeError(
+                "gs_voxelizer: capture voxelization through gs_voxelizer.graph.CapturedStep "
+                "(it checks every replay's intersection count), at most 16 forwards a step")
+        host = free.pop()
+        _capture.counts.append((host, cap))
+        cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous(), total_host=host)
         ids_cap, tile_bins, tiles_cap = _C.bin_and_sort_gaussians_device_count(
             num_gaussians, cap, total, tile_min, tile_max, cum_tiles_hit, vol_size_voxel,
             return_tiles=True)
@@ -140,7 +171,7 @@ def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tile
     if cap is not None:
         # launch at the recorded capacity; the scan writes the count into pinned
         # memory meanwhile
-        host = count_buffer(dev)
+        host = _count_slot(dev)
         host.fill_(-1)
         cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous(), total_host=host)
         ids_cap, tile_bins, tiles_cap = _C.bin_and_sort_gaussians_device_count(

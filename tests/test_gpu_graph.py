@@ -81,3 +81,67 @@ def test_outgrown_capacity_is_recaptured(device):
     out2 = _snapshot(g.replay(), leaves)
     _assert_same(out2, eager, "second replay")
     assert g.recaptures == 1
+
+
+def test_two_forwards_in_one_captured_step(device):
+    """A step with two voxelizations: each replay checks both counts, and the
+    second outgrowing its capacity is caught."""
+    voxelize._capacity.pop(device.index or 0, None)
+    cfg_a = small_config(3, 4000, vol=(64, 72, 56))
+    cfg_b = small_config(1, 2500, vol=(56, 64, 48))
+    leaves_a, step_a = _make(device, cfg_a, seed=11)
+    leaves_b, step_b = _make(device, cfg_b, seed=12)
+
+    def step():
+        out_a = step_a()
+        out_b = step_b()
+        return out_a[0] + out_b[0], out_a[1]
+
+    eager = _snapshot(step(), leaves_a + leaves_b)
+    g = graph.CapturedStep(step)
+    assert len(g.counts) == 2
+    out = _snapshot(g.replay(), leaves_a + leaves_b)
+    torch.cuda.synchronize()
+    _assert_same(out, eager, "replay")
+    with torch.no_grad():
+        leaves_b[1].mul_(3.0)  # the second scene outgrows the capacity
+    out = _snapshot(g.replay(), leaves_a + leaves_b)
+    torch.cuda.synchronize()
+    assert g.recaptures == 1
+    _assert_same(out, _snapshot(step(), leaves_a + leaves_b), "after re-capture")
+
+
+def test_forwards_on_concurrent_threads_and_streams(device):
+    """Eager steps on two host threads, each with its own stream and scene, give
+    the results of running them alone (each forward reads its own pair count)."""
+    import threading
+    voxelize._capacity.pop(device.index or 0, None)
+    cfgs = (small_config(3, 5000, vol=(64, 64, 64)), small_config(1, 3000, vol=(72, 56, 64)))
+    made = [_make(device, c, seed=20 + i) for i, c in enumerate(cfgs)]
+    alone = []
+    for leaves, step in made:
+        alone.append(_snapshot(step(), leaves))
+    torch.cuda.synchronize()
+    results, errors = [None, None], []
+
+    def run(i):
+        try:
+            s = torch.cuda.Stream(device=device)
+            leaves, step = made[i]
+            with torch.cuda.stream(s):
+                for _ in range(6):
+                    out = step()
+                results[i] = _snapshot(out, leaves)
+            s.synchronize()
+        except Exception as e:  # reported after join
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i in range(2):
+        _assert_same(results[i], alone[i], f"thread {i}")
