@@ -73,20 +73,67 @@ __device__ __forceinline__ void put_total(int64_t v, int64_t *total_out, int64_t
     }
 }
 
-// Exclusive scan of part[0..nb) in place by one workgroup; writes the total.
-__global__ __launch_bounds__(kThreads) void k_scan_block_sums(int32_t *part, int64_t nb,
-                                                              int64_t *total_out,
-                                                              int64_t *total_host) {
-    __shared__ int lds_waves[kThreads / kWave];
-    int64_t carry = 0;
-    for (int64_t start = 0; start < nb; start += kThreads) {
-        const int64_t i = start + threadIdx.x;
-        const int v = i < nb ? part[i] : 0;
-        int total;
-        const int ex = block_exclusive(v, lds_waves, &total);
-        if (i < nb) part[i] = (int32_t)(carry + ex);
+// Exclusive scan of part[0..nb) in place by one workgroup of kSumsThreads;
+// writes the total (int64: a sum beyond int32 stays visible to the caller).
+// Tiles of kSumsThreads * 8: thread t loads 8 consecutive values (two 16-byte
+// loads when part is 16-byte aligned), one block scan gives the offsets, and
+// the prefixes are stored the same way, so every access is coalesced.
+constexpr int kSumsThreads = 1024;
+
+__global__ __launch_bounds__(kSumsThreads) void k_scan_block_sums(int32_t *part, int64_t nb,
+                                                                  int64_t *total_out,
+                                                                  int64_t *total_host) {
+    __shared__ long long lds_waves[kSumsThreads / kWave];
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const bool vec = (reinterpret_cast<uintptr_t>(part) & 15) == 0;
+    long long carry = 0;
+    for (int64_t base = 0; base < nb; base += (int64_t)kSumsThreads * kItems) {
+        const int64_t i0 = base + (int64_t)threadIdx.x * kItems;
+        const bool whole = vec && i0 + kItems <= nb;
+        int v[kItems];
+        if (whole) {
+            const int4 a = *reinterpret_cast<const int4 *>(part + i0);
+            const int4 b = *reinterpret_cast<const int4 *>(part + i0 + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < kItems; ++k) v[k] = i0 + k < nb ? part[i0 + k] : 0;
+        }
+        long long s = 0;
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) s += v[k];
+        long long inc = s;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const long long o = __shfl_up(inc, d, kWave);
+            if (lane >= d) inc += o;
+        }
+        if (lane == kWave - 1) lds_waves[wave] = inc;
+        __syncthreads();
+        long long run = carry + inc - s, total = 0;
+#pragma unroll
+        for (int w = 0; w < kSumsThreads / kWave; ++w) {
+            const long long x = lds_waves[w];
+            run += w < wave ? x : 0;
+            total += x;
+        }
+        int o[kItems];
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) {
+            o[k] = (int32_t)run;
+            run += v[k];
+        }
+        if (whole) {
+            *reinterpret_cast<int4 *>(part + i0) = make_int4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<int4 *>(part + i0 + 4) = make_int4(o[4], o[5], o[6], o[7]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kItems; ++k)
+                if (i0 + k < nb) part[i0 + k] = o[k];
+        }
         carry += total;
-        __syncthreads();  // lds_waves reused by the next chunk
+        __syncthreads();  // lds_waves is rewritten by the next tile
     }
     if (threadIdx.x == 0) put_total(carry, total_out, total_host);
 }
@@ -155,7 +202,7 @@ int scan_run(Load ld, Store st, int64_t n, int64_t *total_out, int64_t *total_ho
     const int64_t nb = (n + kTile - 1) / kTile;
     int32_t *part = static_cast<int32_t *>(ws);
     if (nb == 0) {
-        hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(kThreads), 0, stream, part, nb,
+        hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(kSumsThreads), 0, stream, part, nb,
                            total_out, total_host);
         return check_launch();
     }
@@ -164,7 +211,7 @@ int scan_run(Load ld, Store st, int64_t n, int64_t *total_out, int64_t *total_ho
     if (int st_ = check_launch()) return st_;
     const int direct = nb <= kDirectBlocks ? 1 : 0;
     if (!direct) {
-        hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(kThreads), 0, stream, part, nb,
+        hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(kSumsThreads), 0, stream, part, nb,
                            total_out, total_host);
         if (int st_ = check_launch()) return st_;
     }

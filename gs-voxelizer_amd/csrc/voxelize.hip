@@ -410,16 +410,27 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
 }
 
 // loss = (sum over tiles of the partials) / numel, summed in a fixed order in
-// binary64 by one workgroup.
+// binary64 by one workgroup: float4 loads (when the partials are 16-byte
+// aligned) into four running sums per thread keep many loads in flight.
 constexpr int kFinishThreads = 1024;
 
 __global__ __launch_bounds__(kFinishThreads) void k_loss_finish(const float *__restrict__ tile_loss,
                                                                 int64_t T, double numel,
                                                                 float *__restrict__ loss) {
     __shared__ double s_w[kFinishThreads / kWave];
-    double acc = 0.0;
-#pragma unroll 8
-    for (int64_t i = threadIdx.x; i < T; i += kFinishThreads) acc += (double)tile_loss[i];
+    double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+    const int64_t T4 = aligned_to(tile_loss, 16) ? T / 4 : 0;
+    const float4 *t4 = reinterpret_cast<const float4 *>(tile_loss);
+#pragma unroll 16
+    for (int64_t i = threadIdx.x; i < T4; i += kFinishThreads) {
+        const float4 v = t4[i];
+        a0 += (double)v.x;
+        a1 += (double)v.y;
+        a2 += (double)v.z;
+        a3 += (double)v.w;
+    }
+    for (int64_t i = 4 * T4 + threadIdx.x; i < T; i += kFinishThreads) a0 += (double)tile_loss[i];
+    double acc = (a0 + a1) + (a2 + a3);
 #pragma unroll
     for (int o = kWave / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, kWave);
     if ((threadIdx.x & (kWave - 1)) == 0) s_w[threadIdx.x / kWave] = acc;
@@ -1330,13 +1341,13 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
         int32_t *part = reinterpret_cast<int32_t *>(ws + L.part);
         int64_t *kept = reinterpret_cast<int64_t *>(ws + L.kept);
         const int64_t nb = (num_intersects + kKeepTile - 1) / kKeepTile;
-        const int direct = nb <= 2048 ? 1 : 0;
+        const int direct = nb <= scan_detail::kDirectBlocks ? 1 : 0;
         hipLaunchKernelGGL(k_keep_count, dim3((unsigned)nb), dim3(kKeepThreads), 0, s, pair_live,
                            ni, count_dev, part);
         if (int st = check_launch()) return st;
         if (!direct) {
-            hipLaunchKernelGGL(scan_detail::k_scan_block_sums, dim3(1), dim3(kKeepThreads), 0, s,
-                               part, nb, kept, nullptr);
+            hipLaunchKernelGGL(scan_detail::k_scan_block_sums, dim3(1),
+                               dim3(scan_detail::kSumsThreads), 0, s, part, nb, kept, nullptr);
             if (int st = check_launch()) return st;
         }
         hipLaunchKernelGGL(k_keep_order, dim3((unsigned)nb), dim3(kKeepThreads), 0, s, pair_live,
