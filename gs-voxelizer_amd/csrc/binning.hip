@@ -4,7 +4,8 @@
 // Reference: gs_voxelizer/cuda/bin_and_sort_gaussians.cu:11-62 and the binding
 // bindings.cu:259-360 (which sorts all 32 key bits with cub::DeviceRadixSort).
 // Keys are tile ids < T, so only ceil(log2 T) bits are sorted here (15 at 256^3:
-// two 8-bit passes instead of four).  Because the keys are emitted
+// two 8-bit passes instead of four; 17 or 18, e.g. 512^3: two 9-bit passes
+// instead of three).  Because the keys are emitted
 // gaussian-major and every pass is stable, the result is the reference's exact
 // order: ascending tile, then ascending gaussian id.
 //
@@ -38,11 +39,15 @@ constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / kWave;
 constexpr int kWaveKeys = kChunk / kSortWaves;  // 1024 contiguous keys per wave
 constexpr int kRounds = kWaveKeys / kWave;      // 16
-constexpr int kRadixBits = 8;
-constexpr int kRadixBins = 1 << kRadixBits;
+// Digit width of the LSD passes: 8 bits, or 9 when that saves a pass (keys of
+// 17 or 18 bits: two 9-bit passes instead of 8 + 8 + 1..2).  Arrays shared by
+// the passes are sized for the widest digit.
+constexpr int kRadixBitsMax = 9;
+constexpr int kRadixBinsMax = 1 << kRadixBitsMax;
 constexpr int kEdgeItems = 16;
 constexpr int kInvalidKey = 0x7fffffff;  // slot beyond its Gaussian's box: sorts last, no tile
-static_assert(kRadixBins == kSortThreads, "one digit per thread in the block scans");
+static_assert(kRadixBinsMax % kSortThreads == 0, "whole rounds of digits per thread");
+static_assert(kRadixBinsMax <= kEmitThreads, "one digit per emission thread");
 static_assert(kEmitItems == 8, "two int4 stores per thread");
 
 __device__ __forceinline__ int64_t live_count(int64_t cap, const int64_t *d_n) {
@@ -61,19 +66,21 @@ __device__ __forceinline__ int64_t live_count(int64_t cap, const int64_t *d_n) {
 // 8 consecutive slots: one search and one division per thread, then stepping
 // through the box.  The chunk's digit histogram for the first radix pass is
 // written digit-major: hist[d * hstride + b].
+template <int B>
 __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
     int n, int64_t cap, const int64_t *__restrict__ d_n, const int *__restrict__ tile_min,
     const int *__restrict__ tile_max, const int *__restrict__ cum, int Tx, int Ty, int64_t T,
     int *__restrict__ keys, int *__restrict__ vals, int *__restrict__ hist, int hstride,
     int2 *__restrict__ tile_bins) {
     __shared__ int s_cum[kWindow];
+    constexpr int kBins = 1 << B;
     __shared__ int s_box[kWindow][6];  // min x, y, z; extent x, y, z
-    __shared__ int s_hist[kRadixBins];
+    __shared__ int s_hist[kBins];
     const int t = threadIdx.x;
     for (int64_t i = (int64_t)blockIdx.x * kEmitThreads + t; i < T;
          i += (int64_t)gridDim.x * kEmitThreads)
         tile_bins[i] = make_int2(0, 0);
-    if (t < kRadixBins) s_hist[t] = 0;
+    if (t < kBins) s_hist[t] = 0;
     const int64_t total = live_count(cap, d_n);
     const int64_t base = (int64_t)blockIdx.x * kChunk;
 
@@ -200,22 +207,25 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
         }
 #pragma unroll
         for (int k = 0; k < kEmitItems; ++k)
-            if (p0 + k < total) atomicAdd(&s_hist[key[k] & (kRadixBins - 1)], 1);
+            if (p0 + k < total) atomicAdd(&s_hist[key[k] & (kBins - 1)], 1);
     }
     __syncthreads();
-    if (t < kRadixBins) hist[(int64_t)t * hstride + blockIdx.x] = s_hist[t];
+    if (t < kBins) hist[(int64_t)t * hstride + blockIdx.x] = s_hist[t];
 }
 
 // Per-chunk digit histogram of a later pass, digit-major; chunks past the live
 // count write zeros.
+template <int B>
 __global__ __launch_bounds__(kSortThreads) void k_radix_hist(const int *__restrict__ keys,
                                                              int64_t cap,
                                                              const int64_t *__restrict__ d_n,
                                                              int shift, int *__restrict__ hist,
                                                              int hstride) {
-    __shared__ int s_hist[kRadixBins];
+    constexpr int kBins = 1 << B;
+    __shared__ int s_hist[kBins];
     const int t = threadIdx.x;
-    s_hist[t] = 0;
+#pragma unroll
+    for (int d = t; d < kBins; d += kSortThreads) s_hist[d] = 0;
     __syncthreads();
     const int64_t n = live_count(cap, d_n);
     const int64_t base = (int64_t)blockIdx.x * kChunk;
@@ -224,17 +234,19 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_hist(const int *__restri
         const int64_t i = base + 4 * ((int64_t)q * kSortThreads + t);
         if (i + 4 <= n) {
             const int4 k4 = *reinterpret_cast<const int4 *>(keys + i);
-            atomicAdd(&s_hist[(k4.x >> shift) & (kRadixBins - 1)], 1);
-            atomicAdd(&s_hist[(k4.y >> shift) & (kRadixBins - 1)], 1);
-            atomicAdd(&s_hist[(k4.z >> shift) & (kRadixBins - 1)], 1);
-            atomicAdd(&s_hist[(k4.w >> shift) & (kRadixBins - 1)], 1);
+            atomicAdd(&s_hist[(k4.x >> shift) & (kBins - 1)], 1);
+            atomicAdd(&s_hist[(k4.y >> shift) & (kBins - 1)], 1);
+            atomicAdd(&s_hist[(k4.z >> shift) & (kBins - 1)], 1);
+            atomicAdd(&s_hist[(k4.w >> shift) & (kBins - 1)], 1);
         } else {
             for (int64_t j = i; j < n && j < i + 4; ++j)
-                atomicAdd(&s_hist[(keys[j] >> shift) & (kRadixBins - 1)], 1);
+                atomicAdd(&s_hist[(keys[j] >> shift) & (kBins - 1)], 1);
         }
     }
     __syncthreads();
-    hist[(int64_t)t * hstride + blockIdx.x] = s_hist[t];
+#pragma unroll
+    for (int d = t; d < kBins; d += kSortThreads)
+        hist[(int64_t)d * hstride + blockIdx.x] = s_hist[d];
 }
 
 // Exclusive scan of one int per thread across an NT-thread block; *total
@@ -334,16 +346,21 @@ __device__ __forceinline__ int block_excl_scan(int v, int *s_wtot) {
 // one digit from consecutive chunks are adjacent in the output, so their
 // partial cache lines meet in the same L2 and reach HBM as whole lines (once
 // the arrays outgrow the last-level cache this is worth ~13 % of the sort).
+// With 9-bit digits each thread handles digits t and t + 256 in the per-digit
+// steps; the block scans over digits then run in two rounds.
+template <int B>
 __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
     const int *__restrict__ kin, const int *__restrict__ vin, int *__restrict__ kout,
     int *__restrict__ vout, int64_t cap, const int64_t *__restrict__ d_n, int shift,
     const int *__restrict__ hist_scanned, const int *__restrict__ totals, int nblocks,
     int hstride) {
+    constexpr int kBins = 1 << B;
+    constexpr int kPer = kBins / kSortThreads;  // digits per thread in the per-digit steps
     __shared__ int s_keys[kChunk];
     __shared__ int s_vals[kChunk];
-    __shared__ int s_wcnt[kSortWaves][kRadixBins];
-    __shared__ int s_start[kRadixBins];
-    __shared__ int s_gbase[kRadixBins];
+    __shared__ int s_wcnt[kSortWaves][kBins];
+    __shared__ int s_start[kBins];
+    __shared__ int s_gbase[kBins];
     __shared__ int s_wtot[kSortWaves];
     const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
     const int64_t n = live_count(cap, d_n);
@@ -352,12 +369,21 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
     const int64_t base = chunk * kChunk;
     if (base >= n) return;
 #pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) s_wcnt[w][t] = 0;
-    {   // global start of this chunk's run of digit t
-        const int dbase = block_excl_scan(totals[t], s_wtot);
-        s_gbase[t] = dbase + hist_scanned[(int64_t)t * hstride + chunk];
+    for (int j = 0; j < kPer; ++j)
+#pragma unroll
+        for (int w = 0; w < kSortWaves; ++w) s_wcnt[w][j * kSortThreads + t] = 0;
+    {   // global start of this chunk's run of each digit
+        int carry = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int d = j * kSortThreads + t;
+            int tot;
+            const int dbase = carry + block_scan_total<kSortThreads>(totals[d], s_wtot, &tot);
+            s_gbase[d] = dbase + hist_scanned[(int64_t)d * hstride + chunk];
+            carry += tot;
+            __syncthreads();  // s_wtot is rewritten by the next round
+        }
     }
-    __syncthreads();
 
     const int64_t wbase = base + (int64_t)wave * kWaveKeys;
     int key[kRounds], val[kRounds], rank[kRounds];
@@ -371,7 +397,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
 #pragma unroll
     for (int k = 0; k < kRounds; ++k) {
         const bool valid = wbase + k * kWave + lane < n;
-        const int d = (key[k] >> shift) & (kRadixBins - 1);
+        const int d = (key[k] >> shift) & (kBins - 1);
         // peers = the valid lanes whose digit equals d: per bit b, t = -1 where
         // bit b of d is set, and a lane keeps the lanes whose ballot bit agrees
         // (sign-extended bit, xor, and-not: about 6 VALU per bit, against 9
@@ -379,7 +405,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
         const uint64_t vm = __ballot(valid);
         uint32_t plo = (uint32_t)vm, phi = (uint32_t)(vm >> 32);
 #pragma unroll
-        for (int b = 0; b < kRadixBits; ++b) {
+        for (int b = 0; b < B; ++b) {
             const uint32_t t = (uint32_t)__builtin_amdgcn_sbfe(d, b, 1);
             const uint64_t m = __ballot(t != 0u);
             plo &= ~((uint32_t)m ^ t);
@@ -394,21 +420,33 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
     }
     __syncthreads();
     {   // per-digit wave offsets, then the chunk's digit starts
-        int c[kSortWaves], sum = 0;
+        int sum[kPer];
 #pragma unroll
-        for (int w = 0; w < kSortWaves; ++w) {
-            c[w] = s_wcnt[w][t];
-            s_wcnt[w][t] = sum;
-            sum += c[w];
+        for (int j = 0; j < kPer; ++j) {
+            const int d = j * kSortThreads + t;
+            sum[j] = 0;
+#pragma unroll
+            for (int w = 0; w < kSortWaves; ++w) {
+                const int c = s_wcnt[w][d];
+                s_wcnt[w][d] = sum[j];
+                sum[j] += c;
+            }
         }
-        __syncthreads();  // s_wtot is reused by the scan below
-        s_start[t] = block_excl_scan(sum, s_wtot);
+        int carry = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            __syncthreads();  // s_wtot is rewritten by this round's scan
+            int tot;
+            s_start[j * kSortThreads + t] =
+                carry + block_scan_total<kSortThreads>(sum[j], s_wtot, &tot);
+            carry += tot;
+        }
     }
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kRounds; ++k) {
         if (wbase + k * kWave + lane < n) {
-            const int d = (key[k] >> shift) & (kRadixBins - 1);
+            const int d = (key[k] >> shift) & (kBins - 1);
             const int pos = s_start[d] + s_wcnt[wave][d] + rank[k];
             s_keys[pos] = key[k];
             s_vals[pos] = val[k];
@@ -421,7 +459,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
         const int p = k * kSortThreads + t;
         if (p < n_here) {
             const int kk = s_keys[p];
-            const int d = (kk >> shift) & (kRadixBins - 1);
+            const int d = (kk >> shift) & (kBins - 1);
             const int64_t dst = (int64_t)s_gbase[d] + (p - s_start[d]);
             kout[dst] = kk;
             vout[dst] = s_vals[p];
@@ -465,7 +503,7 @@ __global__ __launch_bounds__(256) void k_tile_edges(const int *__restrict__ keys
 
 struct BinLayout {
     size_t keys_a, vals_a, keys_b, hist, totals, total;
-    int passes, nblocks, hstride;  // hstride: hist row stride, a multiple of 4
+    int bits, passes, nblocks, hstride;  // digit width; hist row stride, a multiple of 4
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
@@ -474,7 +512,8 @@ BinLayout bin_layout(int64_t cap, int64_t n_tiles) {
     BinLayout L{};
     int bits = 0;
     while (bits < 31 && ((int64_t)1 << bits) < n_tiles) ++bits;
-    L.passes = (bits + kRadixBits - 1) / kRadixBits;
+    L.bits = (bits == 17 || bits == 18) ? 9 : 8;
+    L.passes = (bits + L.bits - 1) / L.bits;
     L.nblocks = (int)((cap + kChunk - 1) / kChunk);
     L.hstride = (imax64(L.nblocks, 1) + 3) / 4 * 4;
     const size_t arr = align256((size_t)cap * sizeof(int));
@@ -482,10 +521,47 @@ BinLayout bin_layout(int64_t cap, int64_t n_tiles) {
     L.keys_a = off; off += arr;
     L.vals_a = off; off += arr;
     L.keys_b = off; off += arr;
-    L.hist = off; off += align256((size_t)kRadixBins * L.hstride * sizeof(int));
-    L.totals = off; off += align256(kRadixBins * sizeof(int));
+    L.hist = off; off += align256(((size_t)1 << L.bits) * L.hstride * sizeof(int));
+    L.totals = off; off += align256(((size_t)1 << L.bits) * sizeof(int));
     L.total = off;
     return L;
+}
+
+// Emission and the LSD passes with B-bit digits, ping-ponging between (ka, va)
+// and (kb, vb) so that the last pass ends in (kb, vb); *keys_sorted gets the
+// buffer of the sorted keys.
+template <int B>
+int emit_and_sort(const BinLayout &L, int32_t n, int64_t cap, const int64_t *d_count,
+                  const int32_t *tile_min, const int32_t *tile_max, const int32_t *cum, int Tx,
+                  int Ty, int64_t T, int *ka, int *va, int *kb, int *vb, int *hist, int *totals,
+                  int32_t *tile_bins, hipStream_t s, int **keys_sorted) {
+    int *kin = (L.passes % 2 == 0) ? kb : ka;
+    int *vin = (L.passes % 2 == 0) ? vb : va;
+    hipLaunchKernelGGL(k_emit_chunk<B>, dim3(L.nblocks), dim3(kEmitThreads), 0, s, n, cap,
+                       d_count, tile_min, tile_max, cum, Tx, Ty, T, kin, vin, hist, L.hstride,
+                       reinterpret_cast<int2 *>(tile_bins));
+    if (int st = check_launch()) return st;
+    for (int p = 0; p < L.passes; ++p) {
+        int *kout = (kin == ka) ? kb : ka;
+        int *vout = (vin == va) ? vb : va;
+        const int shift = p * B;
+        if (p > 0) {
+            hipLaunchKernelGGL(k_radix_hist<B>, dim3(L.nblocks), dim3(kSortThreads), 0, s, kin,
+                               cap, d_count, shift, hist, L.hstride);
+            if (int st = check_launch()) return st;
+        }
+        hipLaunchKernelGGL(k_digit_scan, dim3(1u << B), dim3(kDigitScanThreads), 0, s, hist,
+                           L.nblocks, L.hstride, totals);
+        if (int st = check_launch()) return st;
+        hipLaunchKernelGGL(k_radix_scatter<B>, dim3((unsigned)(kXcds * xcd_per(L.nblocks))),
+                           dim3(kSortThreads), 0, s, kin, vin, kout, vout, cap, d_count, shift,
+                           hist, totals, L.nblocks, L.hstride);
+        if (int st = check_launch()) return st;
+        kin = kout;
+        vin = vout;
+    }
+    *keys_sorted = kin;
+    return GSV_OK;
 }
 
 // tiles_out (optional, 16-byte aligned, cap entries): the sorted keys, i.e. the
@@ -514,35 +590,17 @@ int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *
     int *vb = ids_out;
     int *hist = reinterpret_cast<int *>(ws + L.hist);
     int *totals = reinterpret_cast<int *>(ws + L.totals);
-    // Emit into the pair of buffers that leaves the final pass in (kb, vb).
-    int *kin = (L.passes % 2 == 0) ? kb : ka;
-    int *vin = (L.passes % 2 == 0) ? vb : va;
-    hipLaunchKernelGGL(k_emit_chunk, dim3(L.nblocks), dim3(kEmitThreads), 0, s, n, cap, d_count,
-                       tile_min, tile_max, cum, Tx, Ty, T, kin, vin, hist, L.hstride,
-                       reinterpret_cast<int2 *>(tile_bins));
-    if (int st = check_launch()) return st;
-    for (int p = 0; p < L.passes; ++p) {
-        int *kout = (kin == ka) ? kb : ka;
-        int *vout = (vin == va) ? vb : va;
-        const int shift = p * kRadixBits;
-        if (p > 0) {
-            hipLaunchKernelGGL(k_radix_hist, dim3(L.nblocks), dim3(kSortThreads), 0, s, kin, cap,
-                               d_count, shift, hist, L.hstride);
-            if (int st = check_launch()) return st;
-        }
-        hipLaunchKernelGGL(k_digit_scan, dim3(kRadixBins), dim3(kDigitScanThreads), 0, s, hist,
-                           L.nblocks, L.hstride, totals);
-        if (int st = check_launch()) return st;
-        hipLaunchKernelGGL(k_radix_scatter, dim3((unsigned)(kXcds * xcd_per(L.nblocks))),
-                           dim3(kSortThreads), 0, s, kin, vin, kout, vout, cap, d_count, shift,
-                           hist, totals, L.nblocks, L.hstride);
-        if (int st = check_launch()) return st;
-        kin = kout;
-        vin = vout;
-    }
+    int *keys_sorted = nullptr;
+    const int st = L.bits == 9 ? emit_and_sort<9>(L, n, cap, d_count, tile_min, tile_max, cum, Tx,
+                                                  Ty, T, ka, va, kb, vb, hist, totals, tile_bins,
+                                                  s, &keys_sorted)
+                               : emit_and_sort<8>(L, n, cap, d_count, tile_min, tile_max, cum, Tx,
+                                                  Ty, T, ka, va, kb, vb, hist, totals, tile_bins,
+                                                  s, &keys_sorted);
+    if (st) return st;
     const int64_t threads = (cap + kEdgeItems - 1) / kEdgeItems;
-    hipLaunchKernelGGL(k_tile_edges, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, kin,
-                       cap, d_count, T, reinterpret_cast<int2 *>(tile_bins));
+    hipLaunchKernelGGL(k_tile_edges, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                       keys_sorted, cap, d_count, T, reinterpret_cast<int2 *>(tile_bins));
     return check_launch();
 }
 

@@ -15,11 +15,13 @@ from helpers import gpu_bin, np32, oracle_project, small_config
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("n", [1, 7, 2047, 2048, 2049, 100_000, 1_000_003])
+# 5M and 20M elements: more than 2048 blocks of 2048, so the block sums are
+# scanned by their own workgroup (in one tile of 8192, then in several)
+@pytest.mark.parametrize("n", [1, 7, 2047, 2048, 2049, 100_000, 1_000_003, 5_000_011, 20_000_003])
 def test_cumsum_matches_numpy(device, n):
     import gs_voxelizer.cuda as _C
     g = np.random.default_rng(n)
-    x = g.integers(0, 300, size=n).astype(np.int32)
+    x = g.integers(0, 300 if n < 2_000_000 else 50, size=n).astype(np.int32)  # total < 2^31
     x[g.random(n) < 0.3] = 0
     cum, total = _C.cumsum_tiles_hit(torch.from_numpy(x).to(device))
     ref = np.cumsum(x.astype(np.int64))
@@ -31,9 +33,12 @@ def _bin_cases():
     yield "cfg1", S.make_gaussians(S.CONFIGS[1], seed=0)
     yield "cfg2_full", S.make_gaussians(S.CONFIGS[2], seed=0)
     yield "cfg3_full", S.make_gaussians(S.CONFIGS[3], seed=0)
-    # one tile (no radix pass), a few tiles (one pass), > 65536 tiles (three passes)
+    # one tile (no radix pass), a few tiles (one pass), 17- and 18-bit tile ids
+    # (two 9-bit passes), 19 bits (three 8-bit passes)
     yield "one_tile", S.make_gaussians(small_config(1, 500, vol=(5, 7, 6)), seed=4)
     yield "few_tiles", S.make_gaussians(small_config(1, 2000, vol=(20, 40, 33)), seed=5)
+    yield "bits17", S.make_gaussians(small_config(3, 20000, vol=(400, 408, 320)), seed=9)
+    yield "bits18", S.make_gaussians(small_config(3, 30000, vol=(512, 512, 512)), seed=10)
     yield "three_passes", S.make_gaussians(small_config(3, 30000, vol=(520, 520, 520)), seed=6)
     yield "clustered_heavy", S.make_gaussians(small_config(5, 40000), seed=7)
 
