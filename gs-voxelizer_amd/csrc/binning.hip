@@ -124,10 +124,13 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
 
     const int64_t p0 = base + (int64_t)t * kEmitItems;
     if (p0 < total) {
+        // 32-bit slot arithmetic from here: p0 < total <= cap <= INT32_MAX, and
+        // slot p0 + k is only formed for k < rem
+        const int q0 = (int)p0, rem = (int)(total - p0);
         // cum and box at window index i (global memory beyond the window)
         auto cum_at = [&](int i) -> int { return i < wlen ? s_cum[i] : cum[g_lo + i]; };
         int mnx = 0, mny = 0, mnz = 0, ex = 0, ey = 0, ez = 0, dx = 0, dy = 0, dz = 0;
-        auto load_box = [&](int i, int j) {
+        auto load_box = [&](int i) {  // the box of window index i, stepping from its first tile
             if (i < wlen) {
                 mnx = s_box[i][0]; mny = s_box[i][1]; mnz = s_box[i][2];
                 ex = s_box[i][3]; ey = s_box[i][4]; ez = s_box[i][5];
@@ -138,27 +141,21 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
                 ez = tile_max[3 * g + 2] - mnz;
             }
             dx = dy = dz = 0;
-            if (ex > 0 && ey > 0 && ez > 0) {
-                const unsigned r = (unsigned)j / (unsigned)ex;
-                dx = j - (int)r * ex;
-                dy = (int)(r % (unsigned)ey);
-                dz = (int)(r / (unsigned)ey);
-            }
         };
-        // l = min{i : cum_at(i) > p0}, searched in the window, then beyond it
+        // l = min{i : cum_at(i) > q0}, searched in the window, then beyond it
         int l;
-        if (wlen > 0 && (int64_t)s_cum[wlen - 1] > p0) {
+        if (wlen > 0 && s_cum[wlen - 1] > q0) {
             int a = 0, b = wlen - 1;
             while (a < b) {
                 const int m = (a + b) >> 1;
-                if ((int64_t)s_cum[m] > p0) b = m; else a = m + 1;
+                if (s_cum[m] > q0) b = m; else a = m + 1;
             }
             l = a;
         } else {
             int a = wlen, b = n - g_lo;  // answer in [wlen, n - g_lo]
             while (a < b) {
                 const int m = (a + b) >> 1;
-                if ((int64_t)cum[g_lo + m] > p0) b = m; else a = m + 1;
+                if (cum[g_lo + m] > q0) b = m; else a = m + 1;
             }
             l = a;
         }
@@ -166,16 +163,25 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
         int g = g_lo + l;
         int start = l == 0 ? prev : cum_at(l - 1);
         int end = g < n ? cum_at(l) : start;
-        if (g < n) load_box(l, (int)(p0 - start));
+        if (g < n) {  // the thread's first slot may lie inside the box: one division
+            load_box(l);
+            const int j = q0 - start;
+            if (ex > 0 && ey > 0 && ez > 0) {
+                const unsigned r = (unsigned)j / (unsigned)ex;
+                dx = j - (int)r * ex;
+                dy = (int)(r % (unsigned)ey);
+                dz = (int)(r / (unsigned)ey);
+            }
+        }
 #pragma unroll
         for (int k = 0; k < kEmitItems; ++k) {
-            const int64_t p = p0 + k;
-            if (p >= total || g >= n) {
+            if (k >= rem || g >= n) {
                 key[k] = kInvalidKey;
                 val[k] = 0;
                 continue;
             }
-            if (p >= end) {  // next non-empty Gaussian
+            const int p = q0 + k;
+            if (p >= end) {  // next non-empty Gaussian; p is its first slot (p == start)
                 do {
                     ++l;
                     ++g;
@@ -183,7 +189,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
                     end = g < n ? cum_at(l) : start;
                 } while (g < n && p >= end);
                 if (g >= n) { key[k] = kInvalidKey; val[k] = 0; continue; }
-                load_box(l, (int)(p - start));
+                load_box(l);
             }
             val[k] = g;
             // a slot past the box (cum inconsistent with the box) gets no tile
