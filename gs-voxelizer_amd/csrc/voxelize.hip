@@ -934,6 +934,9 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
     if (any_live) {
         uint64_t rest = starts;
         for (int k = 0; k < g0; ++k) rest &= rest - 1;  // skip earlier groups' tiles
+        // the group's tiles; the slots past them are read by no lane, so they
+        // are neither staged nor rescaled
+        const int ntile = min(K, __popcll(rest));
         const int y_l = lane & 7, z_l = lane >> 3;
         // fused L1 (torch's l1_loss, mean): dL/dv = sgn(v - t) * (dL / numel).  The
         // division is a multiply by the binary32 reciprocal, as torch's division
@@ -952,6 +955,7 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
         float mx = 0.f;
 #pragma unroll
         for (int k = 0; k < K; ++k) {
+            if (k >= ntile) break;
             float v[GSV_TILE * C];
 #pragma unroll
             for (int i = 0; i < GSV_TILE * C; ++i) v[i] = 0.f;
@@ -983,13 +987,15 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
             gexp = grad_scale_exp(mx);
             if (gexp != 0) {
 #pragma unroll
-                for (int k = 0; k < K; ++k)
+                for (int k = 0; k < K; ++k) {
+                    if (k >= ntile) break;
 #pragma unroll
                     for (int q = 0; q < kRowF4; ++q) {
                         float4 &t4 = s_g[k * kSlot + lane * kRowF4 + q];
                         t4 = make_float4(ldexpf(t4.x, gexp), ldexpf(t4.y, gexp),
                                          ldexpf(t4.z, gexp), ldexpf(t4.w, gexp));
                     }
+                }
             }
         }
         __syncthreads();
