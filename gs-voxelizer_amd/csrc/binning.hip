@@ -45,6 +45,7 @@ constexpr int kRounds = kWaveKeys / kWave;      // 16
 constexpr int kRadixBitsMax = 9;
 constexpr int kRadixBinsMax = 1 << kRadixBitsMax;
 constexpr int kEdgeItems = 16;
+constexpr int kRemapChunks = 2048;  // XCD-contiguous scatter chunks above 8M pairs
 constexpr int kInvalidKey = 0x7fffffff;  // slot beyond its Gaussian's box: sorts last, no tile
 static_assert(kRadixBinsMax % kSortThreads == 0, "whole rounds of digits per thread");
 static_assert(kRadixBinsMax <= kEmitThreads, "one digit per emission thread");
@@ -348,10 +349,11 @@ __device__ __forceinline__ int block_excl_scan(int v, int *s_wtot) {
 // running digit counts in LDS; after one barrier the per-wave counts become
 // offsets, keys are staged digit-sorted in LDS and written out so that
 // consecutive lanes store consecutive addresses of the same digit run.
-// Chunks are dealt to the XCDs in contiguous ranges (xcd_remap): the runs of
-// one digit from consecutive chunks are adjacent in the output, so their
-// partial cache lines meet in the same L2 and reach HBM as whole lines (once
-// the arrays outgrow the last-level cache this is worth ~13 % of the sort).
+// With `remap`, chunks are dealt to the XCDs in contiguous ranges (xcd_remap):
+// the runs of one digit from consecutive chunks are adjacent in the output, so
+// their partial cache lines meet in the same L2 and reach HBM as whole lines.
+// That pays once the arrays outgrow the last-level cache (~15 % of the sort at
+// 30M pairs) and costs ~1 us per pass below it, where it is left off.
 // With 9-bit digits each thread handles digits t and t + 256 in the per-digit
 // steps; the block scans over digits then run in two rounds.
 template <int B>
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
     const int *__restrict__ kin, const int *__restrict__ vin, int *__restrict__ kout,
     int *__restrict__ vout, int64_t cap, const int64_t *__restrict__ d_n, int shift,
     const int *__restrict__ hist_scanned, const int *__restrict__ totals, int nblocks,
-    int hstride) {
+    int hstride, int remap) {
     constexpr int kBins = 1 << B;
     constexpr int kPer = kBins / kSortThreads;  // digits per thread in the per-digit steps
     __shared__ int s_keys[kChunk];
@@ -370,7 +372,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
     __shared__ int s_wtot[kSortWaves];
     const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
     const int64_t n = live_count(cap, d_n);
-    const int64_t chunk = xcd_remap(blockIdx.x, xcd_per(nblocks));
+    const int64_t chunk = remap ? xcd_remap(blockIdx.x, xcd_per(nblocks)) : blockIdx.x;
     if (chunk >= nblocks) return;
     const int64_t base = chunk * kChunk;
     if (base >= n) return;
@@ -559,9 +561,11 @@ int emit_and_sort(const BinLayout &L, int32_t n, int64_t cap, const int64_t *d_c
         hipLaunchKernelGGL(k_digit_scan, dim3(1u << B), dim3(kDigitScanThreads), 0, s, hist,
                            L.nblocks, L.hstride, totals);
         if (int st = check_launch()) return st;
-        hipLaunchKernelGGL(k_radix_scatter<B>, dim3((unsigned)(kXcds * xcd_per(L.nblocks))),
+        const int remap = L.nblocks > kRemapChunks ? 1 : 0;
+        hipLaunchKernelGGL(k_radix_scatter<B>,
+                           dim3((unsigned)(remap ? kXcds * xcd_per(L.nblocks) : L.nblocks)),
                            dim3(kSortThreads), 0, s, kin, vin, kout, vout, cap, d_count, shift,
-                           hist, totals, L.nblocks, L.hstride);
+                           hist, totals, L.nblocks, L.hstride, remap);
         if (int st = check_launch()) return st;
         kin = kout;
         vin = vout;
