@@ -203,7 +203,9 @@ def main():
         del captured
 
     # Per-stage times from a separate, untimed pass: torch events around each
-    # native call of the drop-in API (host gaps included in neither figure).
+    # native call of the drop-in API. They include the host's launch gaps inside
+    # a call (the GPU waits for the host there), unlike `value`, whose steps
+    # are queued back to back.
     timer = KernelTimer(_C, ["optim_to_render_forward", "cumsum_tiles_hit",
                              "bin_and_sort_gaussians", "bin_and_sort_gaussians_device_count",
                              "voxelize_forward", "voxelize_backward_per_gaussian",
@@ -262,6 +264,7 @@ def main():
         "fwd_fp32_peak_frac": round(fwd_tflops / FP32_PEAK_TFLOPS, 4),
         "bwd_fp32_peak_frac": round(bwd_tflops / FP32_PEAK_TFLOPS, 4),
         "stage_ms": stages,
+        "stage_note": "torch events around each native call of the drop-in step, one call at a time: host launch gaps included (a multi-kernel stage such as binning reads well above its kernels); kernel:* entries are the kernels alone",
         "roofline": {"kernel": "k_vox_bwd (voxelize backward)", "bound": "valu",
                      "achieved": round(bwd_tflops, 3), "peak": FP32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(bwd_tflops / FP32_PEAK_TFLOPS, 4),
