@@ -819,7 +819,10 @@ __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
     L.gt = make_gate(mean);
     L.live = L.gt.live;
     const TileGeom &tg = L.tg;
-    if (L.live && L.gt.bounded)
+    // A work list holds only pairs the forward's identical test kept, so the
+    // test is not repeated for them (a pair it would cull has no passing
+    // voxel and yields zero moments either way).
+    if (L.live && L.gt.bounded && a.order == nullptr)
         L.live = may_touch(pr.x, pr.y, pr.z, L.ca, L.cb, L.cc, L.cd, L.ce, L.cf, L.gt.t2, tg.xlo,
                            tg.xhi, tg.ylo, tg.yhi, tg.zlo, tg.zhi);
     if (L.live) {
