@@ -580,9 +580,15 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
 constexpr int kGradScaleExp = 90;
 
 // Tiles staged at once by a backward wave: the LDS of K tiles (2 KB * C each)
-// must leave room for several waves per CU.
+// must leave room for several waves per CU.  Sparse scenes (fewer than
+// kSparsePairs pairs per tile on average) stage more: their 64-pair waves span
+// several tiles, every tile beyond K costs the wave another 64-row pass in
+// k_vox_bwd_rest, and with few waves in flight occupancy matters little.
 template <int C>
 constexpr int kStageTiles = C == 1 ? 3 : 2;
+template <int C>
+constexpr int kStageTilesSparse = C == 1 ? 6 : 4;
+constexpr int64_t kSparsePairs = 32;
 
 struct BwdArgs {
     int D, H, W, Tx, Ty, n, n_isect;
@@ -1388,10 +1394,17 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
 #define GSV_VB(CH)                                                                                  \
     {                                                                                               \
         KernelTimer timer(kTimedVoxBwd, s);                                                         \
-        hipLaunchKernelGGL((k_vox_bwd<CH, kStageTiles<CH>>), grid, block, 0, s, args);             \
-        if (int st = check_launch()) return st;                                                     \
-        hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTiles<CH>>), dim3(kRestBlocks), block, 0, s,  \
-                           args);                                                                   \
+        if (sparse) {                                                                               \
+            hipLaunchKernelGGL((k_vox_bwd<CH, kStageTilesSparse<CH>>), grid, block, 0, s, args);   \
+            if (int st = check_launch()) return st;                                                 \
+            hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTilesSparse<CH>>), dim3(kRestBlocks),     \
+                               block, 0, s, args);                                                  \
+        } else {                                                                                    \
+            hipLaunchKernelGGL((k_vox_bwd<CH, kStageTiles<CH>>), grid, block, 0, s, args);         \
+            if (int st = check_launch()) return st;                                                 \
+            hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTiles<CH>>), dim3(kRestBlocks), block, 0, \
+                               s, args);                                                            \
+        }                                                                                           \
     }                                                                                               \
     if (int st = check_launch()) return st;                                                         \
     if (pairs) {                                                                                    \
@@ -1402,6 +1415,9 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
                            dim3(kReduceThreads), 0, s, n, ni, count_dev,                            \
                            cum_tiles_hit, partial, dpos3d_radii, dconics, dintensities);            \
     }
+    // pairs per tile from the count the grids are sized for (an upper bound
+    // when the live count is on the device)
+    const bool sparse = num_intersects < kSparsePairs * T;
     switch (channels) {
         case 1: { GSV_VB(1) break; }
         case 2: { GSV_VB(2) break; }
