@@ -54,6 +54,11 @@ def _fwd_cases():
     yield "edge_tiles", S.make_gaussians(small_config(1, 800, vol=(20, 30, 17)), seed=8)
     yield "cfg2_20k", S.make_gaussians(small_config(2, 20000), seed=1)
     yield "cfg5_clustered_c4_8k", S.make_gaussians(small_config(5, 8000, vol=(64, 64, 64)), seed=9)
+    # ~290 pairs per tile: the dense backward kernels at C = 2 and 3 (the small
+    # multichannel scenes above, ~12 pairs per tile, take the sparse ones)
+    for c in (2, 3):
+        cfg = small_config(1, 6000, channels=c, vol=(40, 48, 40))
+        yield f"dense_c{c}", S.make_gaussians(cfg, seed=20 + c)
 
 
 @pytest.mark.parametrize("name,work", list(_fwd_cases()), ids=lambda v: v if isinstance(v, str) else "")
@@ -121,7 +126,8 @@ def test_backward_l1_gradient_matches_oracle(device, name, work, mode):
 
 
 @pytest.mark.parametrize("mode", MODES)
-@pytest.mark.parametrize("name,work", list(_fwd_cases())[:5], ids=lambda v: v if isinstance(v, str) else "")
+@pytest.mark.parametrize("name,work", list(_fwd_cases())[:5] + list(_fwd_cases())[-2:],
+                         ids=lambda v: v if isinstance(v, str) else "")
 def test_backward_random_gradient_conditioned(device, name, work, mode):
     cfg = work.cfg
     C = work.intensities.shape[1]
