@@ -468,12 +468,12 @@ struct Moments {
 // well-conditioned: h is large only where |delta| is small.
 //   kGateFree: a = exp2(sigma2 + bound), zero below the threshold by the
 //              hardware flush (bound = the gate-free offset, shift unused).
-//              For C == 1, along a row sigma2 + bound = S0 + P_k - p' S1 with
+//              Along a row sigma2 + bound = S0 + P_k - p' S1 with
 //              p' = u - 3.5 = +-(k + 1/2): S0 and S1 are the form and its
 //              x-slope at the row centre, P_k = A2 p'^2 + bound is per lane, so
-//              the voxels u and 7 - u share S0 + P_k (C = 2 keeps the plain
-//              form: the four P_k would cost it a wave per SIMD; at C >= 3 the
-//              staged tiles' LDS limits occupancy first);
+//              the voxels u and 7 - u share S0 + P_k (at C = 2 the four P_k
+//              cost a wave per SIMD, 5 -> 4, and still gain ~6 %; at C >= 3
+//              the staged tiles' LDS limits occupancy first);
 //   otherwise: a = exp2(s) if |s| <= bound, s = sigma2 - shift.
 template <int C, bool kGateFree>
 __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int nz,
@@ -486,7 +486,7 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
         dxu[u] = mxl - ((float)u - 3.5f);
         dxu2[u] = dxu[u] * dxu[u];
     }
-    constexpr bool kSym = kGateFree && C != 2;
+    constexpr bool kSym = kGateFree;
     float P[4];
     const float A2m = A2 * mxl, Bm = Bn * mxl, Cm = Cn * mxl;
     if (kSym) {
