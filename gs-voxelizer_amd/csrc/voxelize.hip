@@ -580,15 +580,20 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
 constexpr int kGradScaleExp = 90;
 
 // Tiles staged at once by a backward wave: the LDS of K tiles (2 KB * C each)
-// must leave room for several waves per CU.  Sparse scenes (fewer than
-// kSparsePairs pairs per tile on average) stage more: their 64-pair waves span
-// several tiles, every tile beyond K costs the wave another 64-row pass in
-// k_vox_bwd_rest, and with few waves in flight occupancy matters little.
+// must leave room for several waves per CU.  Sparse scenes stage more: their
+// 64-pair waves span several tiles, and every tile beyond K costs the wave
+// another 64-row pass in k_vox_bwd_rest, far more than the occupancy the
+// larger LDS share takes.  By the mean pairs per tile (measured on 512^3
+// scenes: 17 per tile, C = 1: K = 8 684 us, 6 920 us, 3 2254 us; 41 per tile:
+// K = 6 1252 us, 8 1358 us, 3 1600 us; 81 and 108 per tile: K = 3 best):
 template <int C>
-constexpr int kStageTiles = C == 1 ? 3 : 2;
+constexpr int kStageTiles = C == 1 ? 3 : 2;          // >= kSparsePairs per tile
 template <int C>
-constexpr int kStageTilesSparse = C == 1 ? 6 : 4;
-constexpr int64_t kSparsePairs = 32;
+constexpr int kStageTilesSparse = C == 1 ? 6 : 4;    // < kSparsePairs
+template <int C>
+constexpr int kStageTilesVerySparse = C == 1 ? 8 : 4;  // < kVerySparsePairs
+constexpr int64_t kSparsePairs = 64;
+constexpr int64_t kVerySparsePairs = 24;
 
 struct BwdArgs {
     int D, H, W, Tx, Ty, n, n_isect;
@@ -1394,7 +1399,13 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
 #define GSV_VB(CH)                                                                                  \
     {                                                                                               \
         KernelTimer timer(kTimedVoxBwd, s);                                                         \
-        if (sparse) {                                                                               \
+        if (very_sparse) {                                                                          \
+            hipLaunchKernelGGL((k_vox_bwd<CH, kStageTilesVerySparse<CH>>), grid, block, 0, s,       \
+                               args);                                                               \
+            if (int st = check_launch()) return st;                                                 \
+            hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTilesVerySparse<CH>>),                     \
+                               dim3(kRestBlocks), block, 0, s, args);                               \
+        } else if (sparse) {                                                                        \
             hipLaunchKernelGGL((k_vox_bwd<CH, kStageTilesSparse<CH>>), grid, block, 0, s, args);   \
             if (int st = check_launch()) return st;                                                 \
             hipLaunchKernelGGL((k_vox_bwd_rest<CH, kStageTilesSparse<CH>>), dim3(kRestBlocks),     \
@@ -1418,6 +1429,7 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     // pairs per tile from the count the grids are sized for (an upper bound
     // when the live count is on the device)
     const bool sparse = num_intersects < kSparsePairs * T;
+    const bool very_sparse = num_intersects < kVerySparsePairs * T;
     switch (channels) {
         case 1: { GSV_VB(1) break; }
         case 2: { GSV_VB(2) break; }
