@@ -585,13 +585,14 @@ constexpr int kGradScaleExp = 90;
 // another 64-row pass in k_vox_bwd_rest, far more than the occupancy the
 // larger LDS share takes.  By the mean pairs per tile (measured on 512^3
 // scenes: 17 per tile, C = 1: K = 8 684 us, 6 920 us, 3 2254 us; 41 per tile:
-// K = 6 1252 us, 8 1358 us, 3 1600 us; 81 and 108 per tile: K = 3 best):
+// K = 6 1252 us, 8 1358 us, 3 1600 us; 81 and 108 per tile: K = 3 best;
+// 17 per tile at C = 4: K = 6 2805 us, 4 4060 us; at C = 2: 1415, 2550 us):
 template <int C>
 constexpr int kStageTiles = C == 1 ? 3 : 2;          // >= kSparsePairs per tile
 template <int C>
 constexpr int kStageTilesSparse = C == 1 ? 6 : 4;    // < kSparsePairs
 template <int C>
-constexpr int kStageTilesVerySparse = C == 1 ? 8 : 4;  // < kVerySparsePairs
+constexpr int kStageTilesVerySparse = C == 1 ? 8 : 6;  // < kVerySparsePairs
 constexpr int64_t kSparsePairs = 64;
 constexpr int64_t kVerySparsePairs = 24;
 
