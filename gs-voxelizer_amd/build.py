@@ -36,26 +36,48 @@ def hipcc():
     raise RuntimeError("hipcc not found; the gfx950 library cannot be built")
 
 
-def build(verbose=False):
-    """Compile the library; returns its path. Always recompiles."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    fd, tmp = tempfile.mkstemp(suffix=".so", dir=os.path.dirname(OUT))
-    os.close(fd)
-    cmd = [hipcc()] + HIPCC_FLAGS + srcs + ["-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+def _clean(text):
     # hipcc's host pass does not know the device-only target feature; drop that noise
     noise = ("unknown target feature", "packed-fp32-ops")
-    log = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
-                    if not any(k in l for k in noise))
-    if res.returncode != 0:
-        if os.path.exists(tmp):  # hipcc may already have removed it
-            os.unlink(tmp)
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{log}")
-    if verbose and log.strip():
-        print(log, flush=True)
-    os.replace(tmp, OUT)
+    return "\n".join(l for l in text.splitlines() if not any(k in l for k in noise))
+
+
+def build(verbose=False):
+    """Compile the library; returns its path. Always recompiles.
+
+    Each source is compiled to an object in its own hipcc process (they run
+    concurrently; every translation unit is self-contained), then one link
+    step writes the shared library.
+    """
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(dir=os.path.dirname(OUT)) as tmpdir:
+        procs = []
+        for s in SOURCES:
+            obj = os.path.join(tmpdir, os.path.splitext(s)[0] + ".o")
+            cmd = [hipcc()] + flags + ["-c", os.path.join(CSRC, s), "-o", obj]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append((s, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                   stderr=subprocess.STDOUT, text=True)))
+        failed, objs = [], []
+        for s, obj, pr in procs:
+            out, _ = pr.communicate()
+            log = _clean(out)
+            if pr.returncode != 0:
+                failed.append(f"{s} ({pr.returncode}):\n{log}")
+            elif verbose and log.strip():
+                print(log, flush=True)
+            objs.append(obj)
+        if failed:
+            raise RuntimeError("hipcc failed: " + "\n".join(failed))
+        tmp = os.path.join(tmpdir, "libgsvox.so")
+        cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC"] + objs + ["-o", tmp]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc link failed ({res.returncode}):\n{_clean(res.stdout + res.stderr)}")
+        os.replace(tmp, OUT)
     return OUT
 
 
