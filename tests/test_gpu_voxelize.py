@@ -59,6 +59,8 @@ def _fwd_cases():
     for c in (2, 3):
         cfg = small_config(1, 6000, channels=c, vol=(40, 48, 40))
         yield f"dense_c{c}", S.make_gaussians(cfg, seed=20 + c)
+    # ~46 pairs per tile: the middle staging tier of C > 1
+    yield "mid_c3", S.make_gaussians(small_config(1, 3000, channels=3, vol=(64, 64, 64)), seed=31)
 
 
 @pytest.mark.parametrize("name,work", list(_fwd_cases()), ids=lambda v: v if isinstance(v, str) else "")
@@ -126,7 +128,7 @@ def test_backward_l1_gradient_matches_oracle(device, name, work, mode):
 
 
 @pytest.mark.parametrize("mode", MODES)
-@pytest.mark.parametrize("name,work", list(_fwd_cases())[:5] + list(_fwd_cases())[-2:],
+@pytest.mark.parametrize("name,work", list(_fwd_cases())[:5] + list(_fwd_cases())[-3:],
                          ids=lambda v: v if isinstance(v, str) else "")
 def test_backward_random_gradient_conditioned(device, name, work, mode):
     cfg = work.cfg
