@@ -16,8 +16,11 @@ Parity status of each oracle function (what pins it, in ``tests/``):
   and ``numpy.linalg.inv``, hand-computed tile boxes, special values of the
   extent (``test_oracle_projection.py``).
 * ``project_bwd`` — fp64 central finite differences of an independent fp64
-  forward: dscale exactly, dquat on the unit sphere's tangent space, dpos up
-  to the reference's voxel-size factor (``test_oracle_projection.py``).
+  forward: dscale (rtol 1e-4 where det^2 >> 1e-7), all four dquat components
+  through the unnormalised quadratic rotation polynomial (radial part
+  included), dpos up to the reference's voxel-size factor; the 1e-7 det^2
+  regulariser by its closed form on isotropic 0.2-0.5 voxel Gaussians
+  (``test_oracle_projection.py``).
 * ``bin_and_sort`` — brute force with Python ``sorted`` over (tile, gaussian)
   pairs (``test_oracle_binning.py``).
 * ``voxelize_fwd`` — dense fp64 evaluation with numpy over every voxel, closed

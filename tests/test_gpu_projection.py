@@ -86,3 +86,36 @@ def test_projection_backward_matches_oracle(device, name, work):
     report_close(f"{name}: dscale3d", np32(ds), rds, rtol=1e-5, atol=1e-6 * scale)
     scale = max(1e-30, float(np.abs(rdq).max()))
     report_close(f"{name}: dquat", np32(dq), rdq, rtol=1e-5, atol=1e-6 * scale)
+
+
+@pytest.mark.parametrize("s_vox", [0.2, 0.45])
+def test_projection_backward_regulariser_closed_form(device, s_vox):
+    """The HIP projection backward against the closed form of the 1e-7 det^2
+    regulariser (optim_to_render.cu:200) for identity-quaternion Gaussians that
+    are isotropic in voxel units, one conic diagonal gradient per row, on
+    non-cubic voxels: dscale_k = -2 s^9 g / ((s^12 + 1e-7) vs_k)."""
+    import gs_voxelizer.cuda as _C
+    vol, world, center = (40, 56, 48), (1.0, 1.5, 0.8), (0.5, 0.7, 0.5)
+    vs = np.array([world[2] / vol[2], world[1] / vol[1], world[0] / vol[0]])
+    pix = np.array([[19.3, 21.7, 13.4], [27.6, 9.2, 30.1], [5.3, 37.8, 22.9]])
+    lo = np.array([center[2] - world[2] / 2, center[1] - world[1] / 2, center[0] - world[0] / 2])
+    pos = torch.from_numpy((lo + pix * vs).astype(np.float32))
+    scale = torch.from_numpy(np.tile((s_vox * vs).astype(np.float32), (3, 1)))
+    quat = torch.tensor([[1.0, 0, 0, 0]] * 3)
+    inten = torch.full((3, 1), 0.5)
+    dev = [t.to(device) for t in (pos, scale, quat, inten)]
+    pr, *_ = _C.optim_to_render_forward(3, *dev, vol, world, center)
+    g = (1.5, -0.7, 2.0)
+    dcn = torch.zeros((3, 6))
+    dcn[0, 0], dcn[1, 3], dcn[2, 5] = g
+    dp, ds, dq = _C.optim_to_render_backward(3, dev[0], dev[1], dev[2], vol, world, center,
+                                             torch.zeros((3, 4), device=device),
+                                             dcn.to(device), pr)
+    torch.cuda.synchronize()
+    s_eff = scale.numpy().astype(np.float64) / vs
+    want = np.zeros((3, 3))
+    for r, k in enumerate(range(3)):
+        want[r, k] = -2.0 * s_eff[r, k] ** 9 * g[r] / ((s_eff[r, k] ** 12 + 1e-7) * vs[k])
+    report_close(f"dscale closed form s={s_vox}", np32(ds), want, rtol=1e-4,
+                 atol=1e-6 * np.abs(want).max())
+    assert np.abs(np32(dq)).max() <= 1e-6 * np.abs(want).max()

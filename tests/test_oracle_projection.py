@@ -11,7 +11,13 @@ Backward: fp64 central finite differences of that independent forward give the
 true derivatives; the reference's backward (optim_to_render.cu:246-336)
 matches them for scale3d, for quat on the unit sphere's tangent space (it omits
 the normalisation Jacobian), and for pos3d up to its documented factor: it
-returns dpix * voxel_size where the derivative is dpix / voxel_size.
+returns dpix * voxel_size where the derivative is dpix / voxel_size.  Tighter
+pins: all four dquat components (the radial one included) against central
+differences through the quaternion's quadratic rotation polynomial without
+normalisation, which is the function the reference differentiates
+(optim_to_render_helpers.cuh:15-75); dscale at rtol 1e-4 on well-conditioned
+Gaussians; and the 1e-7 regulariser on det^2 (optim_to_render.cu:200) through
+its closed form for isotropic Gaussians of 0.2-0.5 voxel.
 """
 import math
 
@@ -205,3 +211,134 @@ def test_backward_skips_culled_rows():
     dp, ds, dq = O.project_bwd(pos, scale, quat, vol, world, center, np.ones((4, 4), np.float32), g, pr)
     assert not dp[1].any() and not ds[1].any() and not dq[1].any()
     assert dp[0].any() and ds[0].any()
+
+
+def fp64_project_quadratic(pos, scale, quat, vol, world, center):
+    """fp64 projection whose rotation is the quadratic polynomial R(q) of a
+    quaternion [w, x, y, z] with no normalisation (the entries 1 - 2(y^2 + z^2),
+    2(xy - wz), ... of the unit-quaternion rotation matrix, evaluated at q as
+    given).  At unit q it is the rotation of scipy's restatement above; its
+    derivative with respect to all four components is what a backward without
+    the normalisation Jacobian returns (optim_to_render_helpers.cuh:51-75
+    differentiates these entries; :15-36 builds them)."""
+    D, H, W = vol
+    wz, wy, wx = world
+    cz, cy, cx = center
+    vs = np.array([wx / W, wy / H, wz / D])
+    pix = (pos - np.array([cx, cy, cz]) + 0.5 * np.array([wx, wy, wz])) / vs
+    w, x, y, z = (quat[:, i] for i in range(4))
+    R = np.stack([
+        np.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)], -1),
+        np.stack([2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)], -1),
+        np.stack([2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)], -1),
+    ], 1)
+    S2 = np.einsum("ni,ij->nij", scale ** 2, np.eye(3))
+    cov_vox = (R @ S2 @ np.transpose(R, (0, 2, 1))) / (vs[:, None] * vs[None, :])
+    Q = np.linalg.inv(cov_vox)
+    conic = np.stack([Q[:, 0, 0], Q[:, 0, 1], Q[:, 0, 2], Q[:, 1, 1], Q[:, 1, 2], Q[:, 2, 2]], 1)
+    return pix, conic
+
+
+def _well_conditioned(n, seed):
+    """Random Gaussians of 1.5-5 voxels per axis: det(cov_vox)^2 >= 1.5^12 ~ 130,
+    so the backward's 1e-7 regulariser on det^2 moves nothing above ~1e-9."""
+    pos, scale, quat, inten, vol, world, center = _random(n, seed)
+    vs = np.array([world[2] / vol[2], world[1] / vol[1], world[0] / vol[0]])
+    rng = np.random.default_rng(seed + 100)
+    scale = (np.exp(rng.uniform(np.log(1.5), np.log(5.0), (n, 3))) * vs).astype(np.float32)
+    return pos, scale, quat, inten, vol, world, center
+
+
+def test_dquat_all_four_components_match_unnormalised_rotation():
+    """All four dquat components, the radial one included, against fp64 central
+    differences through R(q) without normalisation, at unit q.  A backward that
+    applied the normalisation Jacobian (the tangential projection) would lose
+    the radial part and fail here."""
+    pos, scale, quat, inten, vol, world, center = _well_conditioned(16, 21)
+    pr, cn, tmin, tmax, nt = O.project_fwd(pos, scale, quat, inten, vol, world, center)
+    assert (nt > 0).all()
+    rng = np.random.default_rng(5)
+    gpos = rng.standard_normal((16, 3))
+    gcon = rng.standard_normal((16, 6))
+    dpr = np.c_[gpos, np.zeros(16)].astype(np.float32)
+    _, _, dq = O.project_bwd(pos, scale, quat, vol, world, center, dpr,
+                             gcon.astype(np.float32), pr)
+    p64, s64, q64 = (a.astype(np.float64) for a in (pos, scale, quat))
+    h = 1e-6
+    fd = np.zeros((16, 4))
+    for i in range(16):
+        for k in range(4):
+            vals = []
+            for sgn in (1, -1):
+                q = q64.copy()
+                q[i, k] += sgn * h
+                pix, conic = fp64_project_quadratic(p64, s64, q, vol, world, center)
+                vals.append((gpos * pix).sum() + (gcon * conic).sum())
+            fd[i, k] = (vals[0] - vals[1]) / (2 * h)
+    radial = np.abs((fd * q64).sum(1))
+    tangential = np.abs(fd - (fd * q64).sum(1, keepdims=True) * q64).max(1)
+    assert (radial > 0.05 * tangential).sum() >= 8, "scene must exercise the radial part"
+    row = np.abs(fd).max(1, keepdims=True)
+    report_close("dquat (all four components)", dq, fd, rtol=1e-4, atol=1e-5 * row)
+
+
+def test_dscale_matches_finite_differences_tightly():
+    """dscale at rtol 1e-4 where det^2 >> 1e-7 (the regulariser is then below
+    1e-9 relative)."""
+    pos, scale, quat, inten, vol, world, center = _well_conditioned(16, 22)
+    pr, cn, tmin, tmax, nt = O.project_fwd(pos, scale, quat, inten, vol, world, center)
+    assert (nt > 0).all()
+    rng = np.random.default_rng(6)
+    gpos = rng.standard_normal((16, 3))
+    gcon = rng.standard_normal((16, 6))
+    dpr = np.c_[gpos, np.zeros(16)].astype(np.float32)
+    _, ds, _ = O.project_bwd(pos, scale, quat, vol, world, center, dpr,
+                             gcon.astype(np.float32), pr)
+    fd = _loss_fd(pos, scale, quat, inten, vol, world, center, gpos, gcon, 1, h=1e-8)
+    row = np.abs(fd).max(1, keepdims=True)
+    report_close("dscale (well conditioned)", ds, fd, rtol=1e-4, atol=1e-5 * row)
+
+
+def regularised_dscale(s_vox, vs, g):
+    """Closed form of the reference's dscale for an identity-quaternion Gaussian
+    that is isotropic in voxel units (cov_vox = s^2 I, det = s^6) with a
+    gradient g on one diagonal conic element: the adjugate derivative scaled by
+    1/(det^2 + 1e-7) (optim_to_render.cu:199-226) gives dL/dcov_kk =
+    -s^8 g / (s^12 + 1e-7), and the chain through cov = (S R)^T (S R) with
+    S = s vs (:300-321) gives dscale_k = -2 s^9 g / ((s^12 + 1e-7) vs_k).
+    Without the regulariser it is the true derivative -2 g / (s^3 vs_k)."""
+    return -2.0 * s_vox ** 9 * g / ((s_vox ** 12 + 1e-7) * vs)
+
+
+@pytest.mark.parametrize("s_vox", [0.2, 0.3, 0.45, 0.5])
+def test_det_regulariser_closed_form(s_vox):
+    """The 1e-7 on det^2: dominant at 0.2 voxel (s^12 = 4e-9), comparable at 0.3
+    (5e-7), a 1.4e-3 relative effect at 0.45 and 4e-4 at 0.5, each above the
+    1e-4 tolerance.  Non-cubic voxels, one conic diagonal element per row, so
+    the x/y/z voxel-size mapping is pinned too."""
+    vol, world, center = (40, 56, 48), (1.0, 1.5, 0.8), (0.5, 0.7, 0.5)
+    vs = np.array([world[2] / vol[2], world[1] / vol[1], world[0] / vol[0]])  # x, y, z
+    # three Gaussians inside the volume, off tile boundaries
+    pix = np.array([[19.3, 21.7, 13.4], [27.6, 9.2, 30.1], [5.3, 37.8, 22.9]])
+    lo = np.array([center[2] - world[2] / 2, center[1] - world[1] / 2, center[0] - world[0] / 2])
+    pos = (lo + pix * vs).astype(np.float32)
+    scale = np.tile((s_vox * vs).astype(np.float32), (3, 1))
+    quat = np.tile(np.array([1, 0, 0, 0], np.float32), (3, 1))
+    inten = np.full((3, 1), 0.5, np.float32)
+    pr, cn, tmin, tmax, nt = O.project_fwd(pos, scale, quat, inten, vol, world, center)
+    assert (pr[:, 3] > 0).all()
+    gcon = np.zeros((3, 6), np.float32)
+    gcon[0, 0], gcon[1, 3], gcon[2, 5] = 1.5, -0.7, 2.0   # xx, yy, zz
+    _, ds, dq = O.project_bwd(pos, scale, quat, vol, world, center,
+                              np.zeros((3, 4), np.float32), gcon, pr)
+    # the closed form uses the binary32 scale's own voxel extent
+    s_eff = scale.astype(np.float64) / vs
+    want = np.zeros((3, 3))
+    for r, (k, g) in enumerate(((0, 1.5), (1, -0.7), (2, 2.0))):
+        want[r, k] = regularised_dscale(s_eff[r, k], vs[k], g)
+    report_close(f"dscale closed form s={s_vox}", ds, want, rtol=1e-4,
+                 atol=1e-6 * np.abs(want).max())
+    unregularised = -2.0 * np.array([1.5, -0.7, 2.0]) / (s_eff[0] ** 3 * vs)
+    gap = np.abs(np.diag(want) - unregularised) / np.abs(unregularised)
+    assert (gap > 1e-4).all(), "the regulariser must be visible at this size"
+    assert np.abs(dq).max() <= 1e-6 * np.abs(want).max()
