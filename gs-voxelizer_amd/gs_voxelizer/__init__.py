@@ -5,4 +5,4 @@ Submodules mirror the reference package: ``optim_to_render``, ``voxelize``,
 gfx950 library libgsvox.so).  ``synthetic`` holds the seeded workload
 generators used by the tests and the benchmark.
 """
-__version__ = "0.1.0"
+__version__ = "0.2.0"
