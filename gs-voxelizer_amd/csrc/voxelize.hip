@@ -176,9 +176,11 @@ __device__ __forceinline__ TileGeom tile_geom(int tile, int Tx, int Ty, int D, i
 // ---------------------------------------------------------------- forward --
 
 // Fused L1: the forward stores sgn(volume - target) per element as one byte
-// (kSgnNaN for an unordered difference) for the backward, which then reads 1
-// byte per element instead of the volume and the target.
-constexpr int8_t kSgnNaN = 2;
+// for the backward, which then reads 1 byte per element instead of the volume
+// and the target.  An unordered difference (a NaN volume or target element)
+// stores 0: torch's sign of NaN is 0, so its l1_loss backward passes
+// grad * 0 there (NaN only when grad itself is not finite, as here).
+__device__ __forceinline__ int8_t l1_sign(float d) { return d > 0.f ? 1 : (d < 0.f ? -1 : 0); }
 
 // float4 slots of one prepared Gaussian record: 13 + C floats (gate-free
 // layout) or 12 + C (exact layout).
@@ -371,7 +373,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                     for (int b = 0; b < 4; ++b) {
                         const float d = v[4 * q + b] - tq[b];
                         lsum += fabsf(d);
-                        const int8_t sb = d > 0.f ? 1 : (d < 0.f ? -1 : (d == 0.f ? 0 : kSgnNaN));
+                        const int8_t sb = l1_sign(d);
                         wd |= (uint32_t)(uint8_t)sb << (8 * b);
                     }
                     words[q] = wd;
@@ -396,8 +398,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                         for (int c = 0; c < C; ++c) {
                             const float d = acc[u][c] - tt[u * C + c];
                             lsum += fabsf(d);
-                            sg[u * C + c] =
-                                d > 0.f ? 1 : (d < 0.f ? -1 : (d == 0.f ? 0 : kSgnNaN));
+                            sg[u * C + c] = l1_sign(d);
                         }
             }
         }
@@ -856,15 +857,9 @@ __device__ __forceinline__ int grad_scale_exp(float m) {
     return kGradScaleExp - e;
 }
 
-// Nonzero when some byte of w equals kSgnNaN (the zero-byte test on w ^ 0x02..).
-__device__ __forceinline__ uint32_t has_nan_byte(uint32_t w) {
-    const uint32_t x = w ^ (0x01010101u * (uint32_t)kSgnNaN);
-    return (x - 0x01010101u) & ~x & 0x80808080u;
-}
-
 // One staged row of the backward's source gradient: x = x0 .. x0+nx-1 of one
 // (y, z), C channels, at element offset `off`.  With the fused L1 sign bytes
-// the value is sc * sgn (NaN for kSgnNaN), plus vol_grad when that is given
+// the value is sc * sgn, plus vol_grad when that is given
 // too; otherwise it is vol_grad.  Full rows at a suitable alignment are read
 // with vector loads (one 8-byte load per 8 sign bytes, float4 for vol_grad).
 template <int C>
@@ -881,28 +876,17 @@ __device__ __forceinline__ void load_grad_row(const BwdArgs &a, int64_t off, int
                 w[2 * q] = t.x;
                 w[2 * q + 1] = t.y;
             }
-            uint32_t nan_bytes = 0;
 #pragma unroll
-            for (int q = 0; q < kN / 4; ++q) {
-                nan_bytes |= has_nan_byte(w[q]);
+            for (int q = 0; q < kN / 4; ++q)
 #pragma unroll
                 for (int b = 0; b < 4; ++b)
                     v[4 * q + b] = sc * (float)(int8_t)(w[q] >> (8 * b));
-            }
-            if (nan_bytes) {
-#pragma unroll
-                for (int i = 0; i < kN; ++i)
-                    if ((int8_t)(w[i / 4] >> (8 * (i % 4))) == kSgnNaN) v[i] = __builtin_nanf("");
-            }
         } else {
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u)
                 if (u < nx)
 #pragma unroll
-                    for (int c = 0; c < C; ++c) {
-                        const int8_t q = sg[u * C + c];
-                        v[u * C + c] = q == kSgnNaN ? __builtin_nanf("") : sc * (float)q;
-                    }
+                    for (int c = 0; c < C; ++c) v[u * C + c] = sc * (float)sg[u * C + c];
         }
         if (a.vol_grad != nullptr) {
 #pragma unroll

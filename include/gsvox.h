@@ -207,7 +207,8 @@ int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
  * = mean over all D*H*W*channels elements of |volume - target|, target laid
  * out like volume.  The loss is summed per tile in binary32 and over tiles in
  * binary64 in a fixed order.  `sign` (int8, laid out like volume) receives
- * sgn(volume - target): -1, 0, 1, or 2 where the difference is NaN.
+ * sgn(volume - target): -1, 0 or 1, and 0 where the difference is NaN (torch's
+ * sign of NaN, so the backward matches l1_loss's there too; the loss is NaN).
  * pair_live as for gsv_voxelize_fwd.
  * Workspace: gsv_voxelize_fwd_l1_workspace_bytes.
  *

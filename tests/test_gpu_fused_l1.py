@@ -94,3 +94,26 @@ def test_fused_l1_no_intersections(device):
     assert float(loss) == pytest.approx(float(target.abs().mean()), rel=1e-6)
     for g in grads:
         assert float(g.abs().sum()) == 0.0
+
+
+@pytest.mark.parametrize("per_gaussian", [True, False])
+def test_fused_l1_nan_and_inf_targets_match_unfused(device, per_gaussian):
+    """Target voxels that are NaN or +-inf, inside the Gaussians' support: torch's
+    l1_loss backward passes grad * sign(NaN) = 0 at a NaN difference and
+    grad * -+1 at an infinite one; the fused backward must give the same
+    gradients bit for bit (the loss is NaN on both paths)."""
+    work = S.make_gaussians(small_config(1, 2000), seed=8)
+    target = S.phantom(work, device=device).clone()
+    g = torch.Generator(device="cpu").manual_seed(9)
+    flat = target.view(-1)
+    idx = torch.randperm(flat.numel(), generator=g)[:600].to(device)
+    flat[idx[:400]] = float("nan")
+    flat[idx[400:500]] = float("inf")
+    flat[idx[500:]] = float("-inf")
+    ref_loss, ref_vol, ref_grads = _unfused(work, device, target, per_gaussian=per_gaussian)
+    loss, vol, grads = _fused(work, device, target, per_gaussian=per_gaussian)
+    assert torch.equal(vol, ref_vol)
+    assert torch.isnan(ref_loss) and torch.isnan(loss)
+    for nm, a, b in zip(("pos3d", "scale3d", "quat", "intensity"), grads, ref_grads):
+        assert torch.isfinite(b).all(), nm
+        assert torch.equal(a, b), f"grad {nm}"
