@@ -2,25 +2,36 @@
 """Benchmark: one full differentiable voxelization iteration on one MI355X.
 
 A step is the reference's training iteration (README.md:28-83 of
-PaPieta/gs-voxelizer): optim_to_render -> voxelization -> L1 loss against the
-phantom -> loss.backward() (voxelize backward + projection backward), on the
-headline workload of BASELINE.json: 256^3 volume, 200,000 Gaussians, 1 channel,
-synthetic seeded inputs already resident in HBM.
+PaPieta/gs-voxelizer): optim_to_render -> voxelize_gaussians -> torch's
+l1_loss against the phantom -> loss.backward() (voxelize backward + projection
+backward), on the headline workload of BASELINE.json: 256^3 volume, 200,000
+Gaussians, 1 channel, synthetic seeded inputs already resident in HBM.
 
-Prints one JSON line.  `value` is ms per iteration (lower is better) of the
-step with the voxelization fused with the L1 loss (voxelize_gaussians_l1_loss:
-the same loss, gradients identical bit for bit); `dropin_ms_per_step` is the
-same step through the unchanged drop-in API (voxelize_gaussians, then torch's
-l1_loss), and `graph_ms_per_step` the fused step captured once in a HIP graph
-and replayed (gs_voxelizer.graph).  After the warm-up, `value` comes from an
-uninstrumented timed region.  The `roofline` object reports the dominant kernel (voxelize
-backward), timed with HIP events recorded on the stream it is launched on over
-a second, identical timed region, against the FP32 vector peak.
-`cpu_baseline` times the CPU oracle (a binary32 C restatement of the
-reference, OpenMP over the host cores) on the same inputs.
+Prints one JSON line.  `value` is ms per iteration (lower is better) of that
+step through the unchanged drop-in API, from an uninstrumented timed region.
+`fused_ms_per_step` is the same step with the voxelization fused with the L1
+loss (voxelize_gaussians_l1_loss: the same loss, gradients identical bit for
+bit; an entry point the reference does not have), and
+`fused_graph_ms_per_step` the fused step captured once in a HIP graph and
+replayed (gs_voxelizer.graph).
+
+`roofline` reports the dominant kernel of the step, the voxelize backward
+(k_vox_bwd + k_vox_bwd_rest).  Its launch duration is timed live with HIP
+events recorded by the library on the stream the kernel is launched on, over a
+second identical timed region of drop-in steps.  `achieved` is the FP32
+arithmetic the kernel executes per launch, read from rocprofv3 counters of the
+same workload (profiles/valu_<workload>.json: 64 lanes x (2 FMA + ADD + MUL +
+TRANS) wave instructions), divided by that duration; `peak` is MI355X's FP32
+vector peak.  `ref_formulation_tflops` is the reference's flop count for the
+same evaluations (E x (65 + 4C), SURVEY's per-evaluation figure) over the same
+duration; this kernel evaluates a cheaper but equivalent formulation and skips
+culled pairs, so that figure can exceed the peak and is not a utilisation.
+`cpu_baseline` times the C oracle (a binary32 C restatement of the reference,
+OpenMP over the host cores) on the same inputs.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 30] [--config 3]
-                       [--no-cpu-baseline] [--no-dropin] [--no-graph] [--calibrate-copy]
+                       [--variants dropin,fused,graph] [--no-cpu-baseline]
+                       [--calibrate-copy]
 """
 import argparse
 import ctypes
@@ -46,11 +57,11 @@ def parse():
                          "steady clocks)")
     ap.add_argument("--config", type=int, default=3, help="workload number 1-5 (BASELINE.json)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-dropin", action="store_true",
-                    help="run only the fused step (profiling runs: every voxelize dispatch is "
-                         "then the one `value` times)")
-    ap.add_argument("--no-graph", action="store_true",
-                    help="skip timing the fused step captured in one HIP graph")
+    ap.add_argument("--variants", default="dropin,fused,graph",
+                    help="comma list of steps to time besides the drop-in step `value` "
+                         "times: fused (voxelize_gaussians_l1_loss), graph (the fused step "
+                         "replayed from a HIP graph); `dropin` alone makes every voxelize "
+                         "dispatch the one `value` times (profiling runs)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one elementwise kernel that reads and writes 1 GiB (a "
@@ -168,31 +179,37 @@ def main():
         evals = int(((bins[:, 1] - bins[:, 0]).long() * inside).sum().item())
         del pr, cn, tmin, tmax, nt, cum, ids, bins
 
+    variants = {v.strip() for v in args.variants.split(",") if v.strip()}
+    unknown = variants - {"dropin", "fused", "graph"}
+    if unknown:
+        raise SystemExit(f"unknown --variants {sorted(unknown)}")
+    run_fused = "fused" in variants or "graph" in variants
+
     for _ in range(args.warmup):
-        step_fused()
-        if not args.no_dropin:
-            step_dropin()
+        step_dropin()
+        if run_fused:
+            step_fused()
     torch.cuda.synchronize()
 
-    # `value`: the fused step, nothing else in the timed region.
-    ms = timed(step_fused, args.steps)
+    # `value`: the drop-in step, nothing else in the timed region.
+    ms = timed(step_dropin, args.steps)
     # The same region again with the library's pooled HIP events around the
     # hot kernels, on their launch stream, for the per-kernel times (the
     # events themselves cost ~15 us of GPU time per step, kept out of `value`).
     _C._L.gsv_kernel_timing_enable(1)
-    ms_events = timed(step_fused, args.steps)
+    ms_events = timed(step_dropin, args.steps)
     kern = {}
     for slot, name in ((0, "k_vox_fwd"), (1, "k_vox_bwd"), (2, "k_pair_reduce")):
         tot, cnt = ctypes.c_double(0), ctypes.c_int32(0)
         _C._L.gsv_kernel_timing_collect(slot, ctypes.byref(tot), ctypes.byref(cnt))
         kern[name] = (tot.value / cnt.value) if cnt.value else None
     _C._L.gsv_kernel_timing_enable(0)
-    # the unchanged drop-in step (voxelize_gaussians + torch's l1_loss)
-    ms_dropin = None if args.no_dropin else timed(step_dropin, args.steps)
+    # the step fused with the L1 loss (voxelize_gaussians_l1_loss)
+    ms_fused = timed(step_fused, args.steps) if "fused" in variants else None
     # the fused step captured once in a HIP graph and replayed (gs_voxelizer.graph):
     # no host work per step beyond the replay and the check of the pair count
     ms_graph = None
-    if not args.no_graph:
+    if "graph" in variants:
         from gs_voxelizer import graph as G
         captured = G.CapturedStep(step_fused)
         # as many warm replays as eager warm-up steps: the GPU idles during the
@@ -212,7 +229,7 @@ def main():
                              "optim_to_render_backward"])
     timer.install()
     timer.active = True
-    for _ in range(0 if args.no_dropin else min(args.steps, 5)):
+    for _ in range(min(args.steps, 5)):
         step_dropin()
     torch.cuda.synchronize()
     timer.active = False
@@ -221,18 +238,33 @@ def main():
     C = cfg.channels
     fwd_ms = kern["k_vox_fwd"]          # kernel alone
     bwd_ms = kern["k_vox_bwd"]          # kernel alone (the dominant one)
-    fwd_flops = evals * (22 + 2 * C)
-    bwd_flops = evals * (65 + 4 * C)
     stages = {k: round(timer.mean_ms(k), 4) for k in timer.names if timer.mean_ms(k) is not None}
     stages.update({f"kernel:{k}": round(v, 4) for k, v in kern.items() if v is not None})
-    bwd_tflops = bwd_flops / (bwd_ms * 1e-3) / 1e12
-    fwd_tflops = fwd_flops / (fwd_ms * 1e-3) / 1e12
-
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"traffic_{cfg.name}.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("voxelize_backward_hbm_bytes_per_launch")
+    # the reference's flop count for the same evaluations (not a utilisation)
+    ref_bwd_tflops = evals * (65 + 4 * C) / (bwd_ms * 1e-3) / 1e12
+    ref_fwd_tflops = evals * (22 + 2 * C) / (fwd_ms * 1e-3) / 1e12
+    counters = _load_profile("valu", cfg.name)
+    traffic = _load_profile("traffic", cfg.name)
+    roof = {"kernel": "k_vox_bwd + k_vox_bwd_rest (voxelize backward)", "bound": "valu",
+            "achieved": None, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": None,
+            "traffic": None, "duration_ms": round(bwd_ms, 4)}
+    if counters is not None and counters.get("evals") == evals:
+        bw = counters["per_launch"]["voxelize_backward"]
+        achieved = bw["fp32_flops"] / (bwd_ms * 1e-3) / 1e12
+        roof.update(achieved=round(achieved, 3), frac=round(achieved / FP32_PEAK_TFLOPS, 4),
+                    fp32_flops_per_launch=bw["fp32_flops"],
+                    valu_issue_nontrans=bw["valu_issue_nontrans"],
+                    counters=f"profiles/valu_{cfg.name}.json")
+        fw = counters["per_launch"].get("voxelize_forward")
+        if fw is not None:
+            roof["forward"] = {"kernel": "k_vox_fwd", "duration_ms": round(fwd_ms, 4),
+                               "achieved": round(fw["fp32_flops"] / (fwd_ms * 1e-3) / 1e12, 3),
+                               "valu_issue_nontrans": fw["valu_issue_nontrans"]}
+            roof["forward"]["frac"] = round(roof["forward"]["achieved"] / FP32_PEAK_TFLOPS, 4)
+    if traffic is not None and traffic.get("evals") == evals:
+        roof["traffic"] = traffic.get("voxelize_backward_hbm_bytes_per_launch")
+    roof["ref_formulation_tflops"] = round(ref_bwd_tflops, 3)
+    roof["ref_formulation_flops_per_eval"] = 65 + 4 * C
 
     result = {
         "metric": METRIC,
@@ -250,26 +282,22 @@ def main():
         "config": {"workload": cfg.name, "volume_zyx": list(cfg.vol), "gaussians": cfg.n,
                    "channels": C, "intersections": n_isect, "evals": evals,
                    "loss": f"l1 vs {cfg.phantom} phantom", "seed": args.seed,
-                   "step": "optim_to_render + voxelize_gaussians_l1_loss (voxelization fused "
-                           "with torch's l1_loss; identical gradients) + backward",
-                   "dropin_step": "optim_to_render + voxelize_gaussians + torch l1_loss + backward"},
-        "dropin_ms_per_step": None if ms_dropin is None else round(ms_dropin, 4),
-        "graph_ms_per_step": None if ms_graph is None else round(ms_graph, 4),
+                   "step": "optim_to_render + voxelize_gaussians + torch l1_loss + backward "
+                           "(the reference's API, unchanged)",
+                   "fused_step": "optim_to_render + voxelize_gaussians_l1_loss (voxelization "
+                                 "fused with the L1 loss; identical gradients) + backward"},
+        "fused_ms_per_step": None if ms_fused is None else round(ms_fused, 4),
+        "fused_graph_ms_per_step": None if ms_graph is None else round(ms_graph, 4),
         "ms_per_step_with_kernel_events": round(ms_events, 4),
         "evals_per_s": round(2 * evals / (ms * 1e-3), 1),
         "fwd_evals_per_s": round(evals / (fwd_ms * 1e-3), 1),
         "bwd_evals_per_s": round(evals / (bwd_ms * 1e-3), 1),
         "fwd_ms": round(fwd_ms, 4),
         "bwd_ms": round(bwd_ms, 4),
-        "fwd_fp32_peak_frac": round(fwd_tflops / FP32_PEAK_TFLOPS, 4),
-        "bwd_fp32_peak_frac": round(bwd_tflops / FP32_PEAK_TFLOPS, 4),
+        "fwd_ref_formulation_tflops": round(ref_fwd_tflops, 3),
         "stage_ms": stages,
         "stage_note": "torch events around each native call of the drop-in step, one call at a time: host launch gaps included (a multi-kernel stage such as binning reads well above its kernels); kernel:* entries are the kernels alone",
-        "roofline": {"kernel": "k_vox_bwd (voxelize backward)", "bound": "valu",
-                     "achieved": round(bwd_tflops, 3), "peak": FP32_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(bwd_tflops / FP32_PEAK_TFLOPS, 4),
-                     "traffic": traffic,
-                     "flops_per_launch": bwd_flops, "flops_per_eval": 65 + 4 * C},
+        "roofline": roof,
         "cpu_baseline": None,
     }
     if args.calibrate_copy:
@@ -286,6 +314,15 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(work)
     print(json.dumps(result), flush=True)
+
+
+def _load_profile(kind, workload):
+    """profiles/<kind>_<workload>.json (rocprofv3 counter summaries), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kind}_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
 
 
 def cpu_baseline(work, repeats=3):
@@ -322,7 +359,7 @@ def cpu_baseline(work, repeats=3):
     runs = sorted((one() for _ in range(repeats)), key=lambda r: r["total"])
     med = runs[len(runs) // 2]
     return {"value": round(med["total"] * 1e3, 1), "unit": "ms/iter", "cores": O.num_threads(),
-            "kind": "port",
+            "kind": "port", "label": "C oracle (test infrastructure), not a dense PyTorch path",
             "sample": (f"the whole {cfg.name} iteration (no subsampling) through oracle/gsv_oracle.c, "
                        f"a binary32 C restatement of the reference (OpenMP); median of {repeats}"),
             "measured_s": {k: round(v, 3) for k, v in med.items()},
