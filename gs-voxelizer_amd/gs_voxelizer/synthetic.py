@@ -11,6 +11,8 @@ Conventions: positions are world units (x, y, z) in a world box of size
 on axis k means scale3d[:, k] = s * world_k / N_k.
 """
 import math
+
+import numpy as np
 from dataclasses import dataclass, field
 from typing import Dict, Optional, Tuple
 
@@ -174,3 +176,60 @@ def phantom(work: Workload, device="cpu") -> torch.Tensor:
 def tile_grid(vol):
     D, H, W = vol
     return (W + 7) // 8, (H + 7) // 8, (D + 7) // 8
+
+
+# The reference's own value scenario (test/test_gs_voxelizer.py:15-26): a
+# (100, 150, 80) volume in a unit world centred at 0.5 and 100,000 Gaussians
+# from random_gauss_init(anisotropicScale=True, rotation=True)
+# (test/utils.py:91-154), intensities divided by 10.  The reference draws
+# from unseeded global generators; here every draw comes from seeded ones.
+REFERENCE_SCENARIO = Config("ref_value_test_100x150x80_100k", (100, 150, 80), 100_000, 1,
+                            ("fixed", 0.03, 0.01, 0.02), "euler_xyz", (0.01, 0.1), "uniform",
+                            "spheres")
+
+
+def sphere_phantom(vol, rng) -> torch.Tensor:
+    """generate_test_volume (test/utils.py:10-29) with a seeded numpy Generator:
+    0.1 everywhere plus 20 balls, centres uniform over the voxel indices, radii
+    uniform integers in [D // 10, D // 5), each adding U(0.5, 1) inside, then
+    clipped to [0, 1].  (D, H, W) float32."""
+    D, H, W = vol
+    out = torch.full((D, H, W), 0.1, dtype=torch.float32)
+    zz = torch.arange(D)[:, None, None]
+    yy = torch.arange(H)[None, :, None]
+    xx = torch.arange(W)[None, None, :]
+    for _ in range(20):
+        c = rng.integers(0, [D, H, W], size=3)
+        r = int(rng.integers(max(1, D // 10), max(2, D // 5)))
+        inside = (zz - int(c[0])) ** 2 + (yy - int(c[1])) ** 2 + (xx - int(c[2])) ** 2 <= r * r
+        out[inside] += float(rng.uniform(0.5, 1.0))
+    return out.clamp_(0.0, 1.0)
+
+
+def reference_value_scenario(seed: int = 0, n: Optional[int] = None):
+    """(Workload, phantom (D, H, W)) of the reference's value test, seeded.
+
+    Positions U[0,1)^3 (world units, x y z); scales (0.02 * 1.5, 0.02 * 0.5,
+    0.02) world units; rotations from XYZ Euler angles U[0, 360) degrees
+    through the half-angle product formula; intensity = the phantom's value at
+    the voxel floor(pos * (size - 1)) per axis, divided by 10, as
+    random_gauss_init reads it in float32."""
+    cfg = REFERENCE_SCENARIO
+    n = cfg.n if n is None else int(n)
+    D, H, W = cfg.vol
+    vol = sphere_phantom(cfg.vol, np.random.default_rng(seed))
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    pos = torch.rand((n, 3), generator=g, dtype=torch.float32)
+    scale = torch.tensor([0.03, 0.01, 0.02], dtype=torch.float32).expand(n, 3).contiguous()
+    half = torch.deg2rad(torch.rand((n, 3), generator=g, dtype=torch.float32) * 360) / 2
+    c, s = torch.cos(half), torch.sin(half)
+    quat = torch.stack([c[:, 0] * c[:, 1] * c[:, 2] + s[:, 0] * s[:, 1] * s[:, 2],
+                        s[:, 0] * c[:, 1] * c[:, 2] - c[:, 0] * s[:, 1] * s[:, 2],
+                        c[:, 0] * s[:, 1] * c[:, 2] + s[:, 0] * c[:, 1] * s[:, 2],
+                        c[:, 0] * c[:, 1] * s[:, 2] - s[:, 0] * s[:, 1] * c[:, 2]], 1)
+    size_xyz = torch.tensor([W, H, D], dtype=torch.float32)
+    idx = torch.clamp((pos * (size_xyz - 1)).long(), min=0)
+    inten = (vol[idx[:, 2], idx[:, 1], idx[:, 0]] / 10).unsqueeze(-1).contiguous()
+    work = Workload(cfg, pos.contiguous(), scale, quat.contiguous(), inten,
+                    {"kind": "spheres"}, seed)
+    return work, vol

@@ -46,9 +46,10 @@ def gpu_bin(n, tmin, tmax, nt, vol):
     return cum, I, ids, bins
 
 
-def report_close(name, got, ref, rtol, atol, bound=None):
+def report_close(name, got, ref, rtol, atol, bound=None, log_only=False):
     """assert |got-ref| <= atol + rtol*|ref| (+ bound, an optional per-element
-    allowance such as a summation-error bound) elementwise; message lists the worst."""
+    allowance such as a summation-error bound) elementwise; message lists the worst.
+    With log_only the comparison is only logged (GSV_MARGIN_LOG), not asserted."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, (name, got.shape, ref.shape)
@@ -61,12 +62,18 @@ def report_close(name, got, ref, rtol, atol, bound=None):
     bad &= ~both_nan
     log = os.environ.get("GSV_MARGIN_LOG")
     if log and err.size:
-        # worst fraction of the allowance used, to watch how close parity runs
+        # how close parity runs: the worst fraction of the whole allowance used,
+        # of the plain atol + rtol*|ref| alone, and how many elements needed the
+        # extra per-element bound (gate ambiguity, conditioning) at all
+        plain = atol + rtol * np.abs(ref)
         with np.errstate(divide="ignore", invalid="ignore"):
             used = np.where(both_nan, 0.0, err / allow)
+            used_plain = np.where(both_nan, 0.0, err / plain)
+        beyond = int(((err > plain) & ~both_nan).sum())
         with open(log, "a") as f:
-            f.write(f"{name}\t{float(np.nanmax(used)):.4g}\n")
-    if bad.any():
+            f.write(f"{name}\t{err.size}\t{beyond}\t{float(np.nanmax(used)):.4g}\t"
+                    f"{float(np.nanmax(used_plain)):.4g}\n")
+    if bad.any() and not log_only:
         idx = np.argsort(-(err - allow).ravel())[:5]
         worst = [(np.unravel_index(i, got.shape), got.ravel()[i], ref.ravel()[i]) for i in idx]
         raise AssertionError(f"{name}: {int(bad.sum())}/{bad.size} elements outside "

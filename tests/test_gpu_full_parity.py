@@ -1,0 +1,180 @@
+"""Element-wise parity at full benchmark sizes, where the time goes.
+
+BASELINE configuration 3 (256^3, 200,000 Gaussians, the headline) and
+configuration 2 (128^3, all 50,000 Gaussians), plus the reference's own value
+scenario (test/test_gs_voxelizer.py:15-26: 100,000 Gaussians on (100,150,80),
+~495 pairs per tile), each against the oracle:
+
+- the whole volume, every voxel;
+- every element of dpos3d_radii, dconics and dintensities from the dominant
+  kernel, for the L1 training gradient and for a seeded N(0,1) vol_grad, in
+  both reduction modes (per-pair, the autograd path; float atomics, the
+  reference's signature without tile boxes);
+- all four leaf gradients through optim_to_render -> voxelize_gaussians ->
+  torch's l1_loss -> backward, the drop-in API end to end, stage by stage.
+
+Bar: rel 1e-4 / abs 1e-6 (north_star) plus, per element, the oracle-reported
+allowances of tests/test_gpu_voxelize.py: gate-ambiguous terms and 1e-5 x the
+sum of |terms| (conditioning).  Every comparison is logged with the number of
+elements that needed more than the plain rel/abs bound (GSV_MARGIN_LOG).
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle as O
+from gs_voxelizer import optim_to_render, synthetic as S, voxelize
+from helpers import np32, report_close
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-6
+
+
+def _scene(key):
+    if key == "reference_scenario":
+        work, target = S.reference_value_scenario(seed=0)
+        return work, target
+    work = S.make_gaussians(S.CONFIGS[key], seed=0)
+    return work, S.phantom(work)
+
+
+@pytest.fixture(scope="module", params=[3, 2, "reference_scenario"],
+                ids=["cfg3_256cube_200k", "cfg2_128cube_50k", "reference_value_scenario"])
+def scene(request, device):
+    """GPU projection, binning and forward of the whole scene, and the oracle's."""
+    import gs_voxelizer.cuda as _C
+    work, target = _scene(request.param)
+    cfg = work.cfg
+    n = work.pos3d.shape[0]
+    print(f"full parity scene {cfg.name}", flush=True)
+    w = work.to(device)
+    pr, cn, tmin, tmax, nt = _C.optim_to_render_forward(n, w.pos3d, w.scale3d, w.quat,
+                                                        w.intensities, cfg.vol, cfg.world,
+                                                        cfg.center)
+    cum, total = _C.cumsum_tiles_hit(nt)
+    I = int(total.item())
+    ids, bins, tiles = _C.bin_and_sort_gaussians(n, I, tmin, tmax, cum, cfg.vol,
+                                                 return_tiles=True)
+    ref = O.pipeline(work.pos3d.numpy(), work.scale3d.numpy(), work.quat.numpy(),
+                     work.intensities.numpy(), cfg.vol, cfg.world, cfg.center)
+    np.testing.assert_array_equal(np32(tmin), ref["tile_min"])
+    np.testing.assert_array_equal(np32(tmax), ref["tile_max"])
+    np.testing.assert_array_equal(np32(nt), ref["num_tiles_hit"])
+    np.testing.assert_array_equal(np32(ids), ref["gaussian_ids_sorted"])
+    np.testing.assert_array_equal(np32(bins), ref["tile_bins"])
+    yield dict(work=work, target=target, w=w, pr=pr, cn=cn, tmin=tmin, tmax=tmax, cum=cum,
+               ids=ids, bins=bins, tiles=tiles, I=I, ref=ref)
+    torch.cuda.empty_cache()
+
+
+def test_whole_volume(scene):
+    import gs_voxelizer.cuda as _C
+    P = scene
+    work, ref = P["work"], P["ref"]
+    cfg = work.cfg
+    vol = _C.voxelize_forward(cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"], P["w"].intensities)
+    torch.cuda.synchronize()
+    rvol, amb = O.voxelize_fwd(cfg.vol, ref["gaussian_ids_sorted"], ref["tile_bins"],
+                               ref["pos3d_radii"], ref["conics"], work.intensities.numpy(),
+                               with_amb=True)
+    report_close(f"{cfg.name}: whole volume", np32(vol), rvol, RTOL, ATOL, bound=amb)
+    if cfg.name.startswith("ref_value_test"):
+        # the reference's own bound for this scenario (test_gs_voxelizer.py:138), logged
+        report_close(f"{cfg.name}: whole volume (reference's bound)", np32(vol), rvol,
+                     1e-3, 5e-2, log_only=True)
+
+
+def _voxelize_grads(P, g_np, mode):
+    import gs_voxelizer.cuda as _C
+    cfg = P["work"].cfg
+    g = torch.from_numpy(g_np).to(P["pr"].device)
+    extra = (P["tmin"], P["tmax"], P["cum"]) if mode == "pairs" else ()
+    kw = {"tiles_sorted": P["tiles"]} if mode == "pairs" else {}
+    out = _C.voxelize_backward_per_gaussian(cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"],
+                                            P["w"].intensities, g, *extra, **kw)
+    torch.cuda.synchronize()
+    return [np32(t) for t in out]
+
+
+@pytest.mark.parametrize("grad", ["l1", "normal"])
+def test_every_voxelize_gradient_element(scene, grad):
+    P = scene
+    work, ref = P["work"], P["ref"]
+    cfg = work.cfg
+    C = work.intensities.shape[1]
+    if grad == "l1":  # the benchmark's gradient, from the oracle's own volume
+        t = P["target"].numpy()[..., None]
+        g = (np.sign(ref["volume"].astype(np.float64) - t) / ref["volume"].size).astype(np.float32)
+    else:
+        g = np.random.default_rng(17).standard_normal(cfg.vol + (C,)).astype(np.float32)
+    rg, absum, amb = O.voxelize_bwd(cfg.vol, ref["gaussian_ids_sorted"], ref["tile_bins"],
+                                    ref["pos3d_radii"], ref["conics"], work.intensities.numpy(),
+                                    g, diagnostics=True)
+    for mode in ("pairs", "atomic"):
+        got = _voxelize_grads(P, g, mode)
+        for nm, a, b, s, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, rg, absum,
+                                  amb):
+            report_close(f"{cfg.name} {grad} {mode}: {nm}", a, b, RTOL, ATOL,
+                         bound=1e-5 * s + m)
+
+
+def test_leaf_gradients_end_to_end(scene, device):
+    """optim_to_render -> voxelize_gaussians -> l1_loss (sum, so the volume
+    gradient is sign(volume - target), +-1) -> backward, checked in the two
+    stages the autograd graph has, each against the oracle on the same inputs:
+
+    1. the voxelize gradients reaching pos3d_radii, conics and intensities
+       (captured with hooks) against the oracle's voxelize backward fed the
+       same volume gradient, with the allowances above;
+    2. the leaf gradients against the oracle's projection backward applied to
+       those captured gradients, rel 1e-5.
+
+    The leaves are not compared with rel 1e-4 against the oracle's own
+    voxelize gradients pushed through its projection backward: that binary32
+    formula (optim_to_render.cu:186-336) is ill-conditioned for thin
+    Gaussians, where a one-ulp change of dconics moves dscale by up to ~4e-4
+    and dquat by more (measured on this scene), so no binary32 evaluation,
+    the reference's included, can be held to it.  That comparison is logged
+    (GSV_MARGIN_LOG) with the number of elements beyond the plain bound."""
+    P = scene
+    work, ref = P["work"], P["ref"]
+    cfg = work.cfg
+    w = P["w"]
+    leaves = [t.clone().requires_grad_() for t in (w.pos3d, w.scale3d, w.quat, w.intensities)]
+    pr, cn, tmin, tmax, nt = optim_to_render.optim_to_render(*leaves, cfg.vol, cfg.world,
+                                                             cfg.center)
+    seen = {}
+    pr.register_hook(lambda t: seen.__setitem__("dpr", t.detach().clone()))
+    cn.register_hook(lambda t: seen.__setitem__("dcn", t.detach().clone()))
+    vol = voxelize.voxelize_gaussians(pr, cn, leaves[3], cfg.vol, tmin, tmax, nt)
+    tgt = P["target"].to(device)[..., None].expand_as(vol)
+    F.l1_loss(vol, tgt, reduction="sum").backward()
+    torch.cuda.synchronize()
+    v = np32(vol)
+    g = np.sign(v.astype(np.float64) - P["target"].numpy()[..., None]).astype(np.float32)
+    inten = work.intensities.numpy()
+    rv, absum, amb = O.voxelize_bwd(cfg.vol, ref["gaussian_ids_sorted"], ref["tile_bins"],
+                                    ref["pos3d_radii"], ref["conics"], inten, g,
+                                    diagnostics=True)
+    got_v = (np32(seen["dpr"]), np32(seen["dcn"]), np32(leaves[3].grad))
+    for nm, a, b, s_, m in zip(("dpos3d_radii", "dconics", "dintensities"), got_v, rv, absum,
+                               amb):
+        report_close(f"{cfg.name} end-to-end stage 1: {nm}", a, b, RTOL, ATOL,
+                     bound=1e-5 * s_ + m)
+    args = (work.pos3d.numpy(), work.scale3d.numpy(), work.quat.numpy(), cfg.vol, cfg.world,
+            cfg.center)
+    same_in = O.project_bwd(*args, got_v[0], got_v[1], np32(pr))
+    indep = O.project_bwd(*args, rv[0], rv[1], ref["pos3d_radii"])
+    for nm, leaf, a, b in zip(("dpos3d", "dscale3d", "dquat"), leaves[:3], same_in, indep):
+        got = np32(leaf.grad)
+        assert np.isfinite(got).all(), nm
+        scale = max(1e-30, float(np.abs(a).max()))
+        report_close(f"{cfg.name} end-to-end stage 2: {nm}", got, a, 1e-5, 1e-6 * scale)
+        report_close(f"{cfg.name} end-to-end vs independent oracle: {nm}", got, b, RTOL, ATOL,
+                     log_only=True)
+        if cfg.name.startswith("ref_value_test"):
+            # the reference's own gradient bound (test_gs_voxelizer.py:142), logged
+            report_close(f"{cfg.name} end-to-end: {nm} (reference's bound)", got, b, 1e-4,
+                         1e-3, log_only=True)

@@ -2,7 +2,12 @@
 30.6M pairs; 500k clustered Gaussians, 4 channels, with 118M pairs).
 
 - projection and binning: bit-exact against the oracle, every element;
-- forward: every voxel of the first z-layer of tiles against the oracle;
+- forward: every voxel of the first z-layer of tiles, and of the z-layer that
+  holds the heaviest tile (cfg5: a cluster centre, ~11.5k pairs), against the
+  oracle;
+- backward on the heaviest layer: vol_grad N(0,1) there and zero elsewhere,
+  so only that layer's tiles contribute, and every element of the three
+  gradients against the oracle restricted to those tiles;
 - backward: the size-independent identity sum_g I_gc dL/dI_gc == sum_v vol_vc g_vc
   per channel (the volume is linear in each channel's intensities once the gate,
   which depends on the mean intensity, is fixed), with finiteness of every
@@ -109,3 +114,54 @@ def test_backward_intensity_identity(full):
                                             tiles_sorted=P["tiles"], pair_live=live)
     for a, b in zip((dp, dc, di), got):
         assert torch.equal(a, b)
+
+
+def _heaviest_layer(P):
+    cfg = P["work"].cfg
+    bins = np32(P["bins"])
+    counts = bins[:, 1] - bins[:, 0]
+    Tx, Ty, _ = O.tile_grid(cfg.vol)
+    t = int(np.argmax(counts))
+    z = t // (Tx * Ty)
+    return z, (z * Tx * Ty, (z + 1) * Tx * Ty), int(counts[t])
+
+
+def test_forward_heaviest_tile_layer(full):
+    import gs_voxelizer.cuda as _C
+    P = full
+    work = P["work"]
+    cfg = work.cfg
+    z, rng, heaviest = _heaviest_layer(P)
+    print(f"{cfg.name}: heaviest tile has {heaviest} pairs, tile layer {z}", flush=True)
+    vol = _C.voxelize_forward(cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"], P["w"].intensities)
+    ref, amb = O.voxelize_fwd(cfg.vol, np32(P["ids"]), np32(P["bins"]), P["rpr"], P["rcn"],
+                              work.intensities.numpy(), tile_range=rng, with_amb=True)
+    zs = slice(8 * z, 8 * z + 8)
+    report_close(f"{cfg.name} heaviest tile layer {z} ({heaviest} pairs)", np32(vol[zs]),
+                 ref[zs], RTOL, ATOL, bound=amb[zs])
+
+
+def test_backward_heaviest_tile_layer_every_element(full):
+    """vol_grad is N(0,1) on the heaviest tile layer and exactly zero elsewhere:
+    every other tile's terms are then exactly zero, so the whole-volume GPU
+    backward equals the oracle's over that layer's tiles."""
+    import gs_voxelizer.cuda as _C
+    P = full
+    work = P["work"]
+    cfg = work.cfg
+    C = work.intensities.shape[1]
+    z, rng, heaviest = _heaviest_layer(P)
+    g = np.zeros(cfg.vol + (C,), np.float32)
+    zs = slice(8 * z, min(8 * z + 8, cfg.vol[0]))
+    g[zs] = np.random.default_rng(23).standard_normal(g[zs].shape).astype(np.float32)
+    got = _C.voxelize_backward_per_gaussian(cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"],
+                                            P["w"].intensities, torch.from_numpy(g).to(
+                                                P["pr"].device), P["tmin"], P["tmax"],
+                                            P["cum"], tiles_sorted=P["tiles"])
+    torch.cuda.synchronize()
+    rg, absum, amb = O.voxelize_bwd(cfg.vol, np32(P["ids"]), np32(P["bins"]), P["rpr"],
+                                    P["rcn"], work.intensities.numpy(), g, tile_range=rng,
+                                    diagnostics=True)
+    for nm, a, b, s, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, rg, absum, amb):
+        report_close(f"{cfg.name} heaviest layer {z}: {nm}", np32(a), b, RTOL, ATOL,
+                     bound=1e-5 * s + m)
