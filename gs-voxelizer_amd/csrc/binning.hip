@@ -26,6 +26,8 @@
 //
 // Data movement per pair: emission writes 8 B; each pass reads 8 B and writes
 // 8 B (later passes read 4 B more for the histogram); the range pass reads 4 B.
+#include <mutex>
+
 #include "gsv_device.h"
 
 namespace gsv {
@@ -614,6 +616,53 @@ int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *
     return check_launch();
 }
 
+// ---------------------------------------------------- allocation-free entry --
+
+// The workspace of gsv_bin_and_sort_noalloc: bin_layout() at the largest
+// supported pair count and the widest digit, plus the 256 bytes of alignment
+// slack bin_and_sort() takes.  One copy per GPU, allocated when the library's
+// code object is loaded on that GPU.
+constexpr int64_t kNoAllocMaxPairs = GSV_NOALLOC_MAX_INTERSECTIONS;
+constexpr size_t kNoAllocArr = ((size_t)kNoAllocMaxPairs * sizeof(int) + 255) / 256 * 256;
+constexpr size_t kNoAllocHistStride = ((kNoAllocMaxPairs + kChunk - 1) / kChunk + 3) / 4 * 4;
+constexpr size_t kNoAllocScratchBytes =
+    3 * kNoAllocArr + ((size_t)kRadixBinsMax * kNoAllocHistStride * sizeof(int) + 255) / 256 * 256 +
+    ((size_t)kRadixBinsMax * sizeof(int) + 255) / 256 * 256 + 256;
+static_assert(kNoAllocScratchBytes == 52431104, "the size gsvox.h states");
+
+}  // namespace
+}  // namespace gsv
+
+// In host code this name is only a handle for hipGetSymbolAddress: each GPU
+// holds its own copy at its own address (noalloc_scratch below).
+static __device__ __align__(256) unsigned char scratch[gsv::kNoAllocScratchBytes];
+
+namespace gsv {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch[kMaxDevices];  // device address of `scratch` on each GPU, once looked up
+
+// The current device's copy of `scratch`, looked up once per device with that
+// device current.
+int noalloc_scratch(void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return record_hip_error(e);
+    if (dev < 0 || dev >= kMaxDevices) return GSV_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch[dev] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return record_hip_error(e);
+        if (p == nullptr) return GSV_ERR_HIP;
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return GSV_OK;
+}
+
 }  // namespace
 }  // namespace gsv
 
@@ -650,4 +699,22 @@ extern "C" int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity,
     return bin_and_sort(n, capacity, num_intersects_dev, tile_min, tile_max, cum_tiles_hit, D, H,
                         W, workspace, workspace_bytes, gaussian_ids_sorted, tile_bins,
                         tiles_sorted, as_stream(stream));
+}
+
+extern "C" int gsv_bin_and_sort_noalloc(int32_t n, int64_t num_intersects,
+                                        const int32_t *tile_min, const int32_t *tile_max,
+                                        const int32_t *cum_tiles_hit, int32_t D, int32_t H,
+                                        int32_t W, int32_t *gaussian_ids_sorted,
+                                        int32_t *tile_bins, int32_t *tiles_sorted, void *stream) {
+    if (num_intersects > kNoAllocMaxPairs) return GSV_ERR_SCRATCH_TOO_SMALL;
+    if (n < 0 || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
+    const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
+    if (T > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
+    if (bin_layout(num_intersects > 0 ? num_intersects : 0, T).total + 256 > kNoAllocScratchBytes)
+        return GSV_ERR_SCRATCH_TOO_SMALL;
+    void *ws = nullptr;
+    if (int st = noalloc_scratch(&ws)) return st;
+    return bin_and_sort(n, num_intersects, nullptr, tile_min, tile_max, cum_tiles_hit, D, H, W,
+                        ws, kNoAllocScratchBytes, gaussian_ids_sorted, tile_bins, tiles_sorted,
+                        as_stream(stream));
 }

@@ -105,6 +105,9 @@ extern "C" const char *gsv_status_string(int status) {
         case GSV_ERR_WORKSPACE_TOO_SMALL: return "workspace too small";
         case GSV_ERR_SIZE_OVERFLOW: return "size exceeds the int32 index range";
         case GSV_ERR_HIP: return "HIP runtime error";
+        case GSV_ERR_SCRATCH_TOO_SMALL:
+            return "more intersections than the allocation-free binning's fixed scratch holds "
+                   "(GSV_NOALLOC_MAX_INTERSECTIONS)";
         default: return "unknown status";
     }
 }

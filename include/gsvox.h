@@ -37,7 +37,8 @@ typedef enum gsv_status {
     GSV_ERR_UNSUPPORTED_CHANNELS = 2, /* channels outside [1, 4] (bindings.cu:61-63) */
     GSV_ERR_WORKSPACE_TOO_SMALL = 3,
     GSV_ERR_SIZE_OVERFLOW = 4,      /* an index would not fit the int32 layout */
-    GSV_ERR_HIP = 5                 /* a HIP runtime call or launch failed */
+    GSV_ERR_HIP = 5,                /* a HIP runtime call or launch failed */
+    GSV_ERR_SCRATCH_TOO_SMALL = 6   /* beyond the fixed scratch of gsv_bin_and_sort_noalloc */
 } gsv_status;
 
 /* Library version, MAJOR*10000 + MINOR*100 + PATCH. */
@@ -135,6 +136,27 @@ int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity, const int64_t *nu
                                   void *workspace, size_t workspace_bytes,
                                   int32_t *gaussian_ids_sorted, int32_t *tile_bins,
                                   int32_t *tiles_sorted, void *stream);
+
+/*
+ * Binning that allocates nothing.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory when they bin (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, outputs and results as gsv_bin_and_sort without the workspace:
+ * the kernels use a fixed array in device memory that the library owns, one per
+ * GPU, 52,431,104 bytes (50 MiB), held until the process ends.
+ * It holds problems of up to GSV_NOALLOC_MAX_INTERSECTIONS (tile, Gaussian)
+ * pairs (the 256^3 / 200,000-Gaussian scene has 3.54 M); a larger
+ * num_intersects returns GSV_ERR_SCRATCH_TOO_SMALL before anything is enqueued.
+ * The stream must belong to the current device.  No part of the array needs
+ * to start at zero: each call writes what it reads.  Every call on one GPU
+ * uses that GPU's single array, so calls that overlap in time on one GPU
+ * (other streams, other host threads) race; the caller serialises them.
+ */
+#define GSV_NOALLOC_MAX_INTERSECTIONS 4194304
+int gsv_bin_and_sort_noalloc(int32_t n, int64_t num_intersects, const int32_t *tile_min,
+                             const int32_t *tile_max, const int32_t *cum_tiles_hit, int32_t D,
+                             int32_t H, int32_t W, int32_t *gaussian_ids_sorted,
+                             int32_t *tile_bins, int32_t *tiles_sorted, void *stream);
 
 /*
  * Forward voxelization.  Replaces voxelize_forward_torch (bindings.cu:362-457;

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 def test_status_strings_and_version():
     L = _lib.load()
     assert L.gsv_version() >= 100
-    for code in range(6):
+    for code in range(7):
         assert L.gsv_status_string(code)
     assert b"MAX_CHANNELS" in L.gsv_status_string(2)
     assert L.gsv_status_string(99) == b"unknown status"
@@ -64,3 +64,16 @@ def test_workspace_sizes_are_host_only():
     assert L.gsv_voxelize_bwd_workspace_bytes(256, 256, 256, 1, 3_542_885, 0, ctypes.byref(b)) == 0
     assert det - b.value >= 3_542_885 * 10 * 4  # per-pair partials of the deterministic mode
     assert small > 0
+
+
+def test_noalloc_binning_rejects_oversize_before_any_launch():
+    """The allocation-free binning holds at most GSV_NOALLOC_MAX_INTERSECTIONS
+    pairs; one more is refused on the host with its own status code."""
+    L = _lib.load()
+    null = ctypes.c_void_p(0)
+    st = L.gsv_bin_and_sort_noalloc(10, 4194304 + 1, null, null, null, 256, 256, 256,
+                                    null, null, null, null)
+    assert st == 6
+    assert b"allocation-free" in L.gsv_status_string(6)
+    assert L.gsv_bin_and_sort_noalloc(-1, 10, null, null, null, 8, 8, 8,
+                                      null, null, null, null) == 1
