@@ -63,6 +63,10 @@ def parse():
                          "replayed from a HIP graph); `dropin` alone makes every voxelize "
                          "dispatch the one `value` times (profiling runs)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--wave-timeline", action="store_true",
+                    help="also record the forward voxelize kernel's per-workgroup start/end "
+                         "over one more drop-in step (gsv_wave_timeline) and summarise its load "
+                         "balance under `wave_timeline`")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one elementwise kernel that reads and writes 1 GiB (a "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -177,6 +181,7 @@ def main():
         inside = ((torch.clamp(W - (t % Tx) * 8, max=8)) * (torch.clamp(H - ((t // Tx) % Ty) * 8, max=8))
                   * (torch.clamp(D - (t // (Tx * Ty)) * 8, max=8)))
         evals = int(((bins[:, 1] - bins[:, 0]).long() * inside).sum().item())
+        tile_pairs = (bins[:, 1] - bins[:, 0]).cpu().numpy()
         del pr, cn, tmin, tmax, nt, cum, ids, bins
 
     variants = {v.strip() for v in args.variants.split(",") if v.strip()}
@@ -300,6 +305,8 @@ def main():
         "roofline": roof,
         "cpu_baseline": None,
     }
+    if args.wave_timeline:
+        result["wave_timeline"] = wave_timeline(_C, step_dropin, cfg, dev, tile_pairs)
     if args.calibrate_copy:
         # an elementwise kernel that reads 1 GiB and writes 1 GiB (a plain hipMemcpy
         # D2D may run on a DMA engine, invisible to the counters); a second 1 GiB
@@ -314,6 +321,57 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(work)
     print(json.dumps(result), flush=True)
+
+
+def wave_timeline(_C, step, cfg, dev, tile_pairs):
+    """Per-workgroup start/end of the forward voxelize kernel (one workgroup per
+    tile) over one drop-in step, summarised: the kernel span, the span an ideal
+    balance would give (the summed workgroup durations over the peak number
+    running at once), when the running count falls below fractions of its
+    peak, and when the heaviest tiles ran."""
+    import numpy as np
+    import torch
+    Tx, Ty, Tz = (cfg.vol[2] + 7) // 8, (cfg.vol[1] + 7) // 8, (cfg.vol[0] + 7) // 8
+    T = Tx * Ty * Tz
+    cap = (T + 63) // 64 * 64
+    rec = torch.zeros((cap, 3), dtype=torch.int64, device=dev)
+    torch.cuda.synchronize()
+    assert _C._L.gsv_wave_timeline(0, ctypes.c_void_p(rec.data_ptr()), cap) == 0
+    try:
+        step()
+        torch.cuda.synchronize()
+    finally:
+        _C._L.gsv_wave_timeline(0, ctypes.c_void_p(0), 0)
+    r = rec.cpu().numpy()
+    ok = (r[:, 0] > 0) & (r[:, 1] > 0)
+    t0 = (r[ok, 0] - r[ok, 0].min()) / 100.0  # 100 MHz ticks -> microseconds
+    t1 = (r[ok, 1] - r[ok, 0].min()) / 100.0
+    tile = r[ok, 2]
+    dur = t1 - t0
+    span = float(t1.max())
+    grid = np.linspace(0.0, span, 512)
+    running = np.array([int(((t0 <= g) & (t1 > g)).sum()) for g in grid])
+    peak = int(running.max())
+    after = grid > grid[int(np.argmax(running))]
+    fall = {}
+    for frac in (0.75, 0.5, 0.25, 0.1):
+        below = grid[(running < frac * peak) & after]
+        fall[f"{int(frac * 100)}%"] = round(float(below.min()) if below.size else span, 1)
+    heavy = np.argsort(-dur)[:5]
+    pairs = tile_pairs[np.clip(tile, 0, tile_pairs.size - 1)]
+    top = np.argsort(-pairs)[:5]
+    return {"workgroups": int(ok.sum()), "span_us": round(span, 1),
+            "balanced_span_us": round(float(dur.sum()) / peak, 1), "peak_running": peak,
+            "running_below_peak_at_us": fall,
+            "longest": [{"tile": int(tile[i]), "pairs": int(pairs[i]),
+                         "start_us": round(float(t0[i]), 1), "end_us": round(float(t1[i]), 1)}
+                        for i in heavy],
+            "heaviest_tiles": [{"tile": int(tile[i]), "pairs": int(pairs[i]),
+                                "start_us": round(float(t0[i]), 1),
+                                "end_us": round(float(t1[i]), 1)} for i in top],
+            "last_start_us": round(float(t0.max()), 1),
+            "note": "forward voxelize kernel of one drop-in step; one workgroup (one wave) per "
+                    "tile; GPU wall clock at 100 MHz"}
 
 
 def _load_profile(kind, workload):

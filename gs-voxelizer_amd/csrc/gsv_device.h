@@ -65,6 +65,10 @@ struct KernelTimer {
 };
 enum TimedKernel { kTimedVoxFwd = 0, kTimedVoxBwd = 1, kTimedPairReduce = 2, kTimedCount = 3 };
 
+// The buffer registered with gsv_wave_timeline for the forward kernel (or
+// nullptr) and its capacity in workgroups.
+uint64_t *wave_timeline_buffer(int *capacity);
+
 // Zero-fills n 32-bit words with a kernel (graph-capture safe, unlike memset).
 int fill_zero_u32(void *ptr, int64_t n_words, hipStream_t stream);
 

@@ -70,6 +70,18 @@ KernelTimer::~KernelTimer() {
     if (on) (void)hipEventRecord(stop, stream);
 }
 
+namespace {
+std::mutex g_wave_mu;
+uint64_t *g_wave_records = nullptr;
+int g_wave_capacity = 0;
+}  // namespace
+
+uint64_t *wave_timeline_buffer(int *capacity) {
+    std::lock_guard<std::mutex> lk(g_wave_mu);
+    *capacity = g_wave_capacity;
+    return g_wave_records;
+}
+
 int record_hip_error(hipError_t e) {
     t_last_hip_error = (int)e;
     return GSV_ERR_HIP;
@@ -183,4 +195,13 @@ extern "C" int gsv_cumsum_tiles_hit(int32_t n, const int32_t *num_tiles_hit,
     }
     return scan_i32(num_tiles_hit, cum_tiles_hit, n, true, total_out, host_dev, workspace,
                     workspace_bytes, as_stream(stream));
+}
+
+extern "C" int gsv_wave_timeline(int32_t kernel, uint64_t *records, int32_t capacity) {
+    if (kernel != 0 || capacity < 0 || (records != nullptr && capacity == 0))
+        return GSV_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(g_wave_mu);
+    g_wave_records = records;
+    g_wave_capacity = records ? capacity : 0;
+    return GSV_OK;
 }

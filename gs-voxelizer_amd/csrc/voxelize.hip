@@ -193,11 +193,16 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
     const int *__restrict__ ids, const int2 *__restrict__ bins, const float4 *__restrict__ pos_radii,
     const float2 *__restrict__ conics, const float *__restrict__ intens, float *__restrict__ vol,
     const float *__restrict__ target, float *__restrict__ tile_loss, int8_t *__restrict__ sgn,
-    uint8_t *__restrict__ pair_live) {
+    uint8_t *__restrict__ pair_live, uint64_t *__restrict__ wave_rec, int wave_cap) {
     __shared__ float4 s_rec[kWave][kRecF4<C>];
     const int64_t tile = xcd_runs(blockIdx.x);
     if (tile >= T) return;
     const int lane = threadIdx.x;
+    const bool timeline = wave_rec != nullptr && (int64_t)blockIdx.x < wave_cap;
+    if (timeline && lane == 0) {
+        wave_rec[3 * (int64_t)blockIdx.x] = wall_clock64();
+        wave_rec[3 * (int64_t)blockIdx.x + 2] = (uint64_t)tile;
+    }
     const TileGeom tg = tile_geom((int)tile, Tx, Ty, D, H, W);
     const float py = (float)(lane & 7) - 3.5f, pz = (float)(lane >> 3) - 3.5f;  // centred, tile-local
     const float py2 = py * py, pyz = py * pz, pz2 = pz * pz;                      // exact
@@ -408,6 +413,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
         for (int o = kWave / 2; o >= 1; o >>= 1) lsum += __shfl_xor(lsum, o, kWave);
         if (lane == 0) tile_loss[tile] = lsum;
     }
+    if (timeline && lane == 0) wave_rec[3 * (int64_t)blockIdx.x + 1] = wall_clock64();
 }
 
 // loss = (sum over tiles of the partials) / numel, summed in a fixed order in
@@ -1265,6 +1271,8 @@ int voxelize_fwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     // an empty list still runs the kernel for the loss: every tile range is empty
     const int ni = empty ? 0 : (int)num_intersects;
     const dim3 grid((unsigned)xcd_runs_grid(T)), block(kWave);
+    int wave_cap = 0;
+    uint64_t *wave_rec = wave_timeline_buffer(&wave_cap);
     {
         KernelTimer timer(kTimedVoxFwd, s);
 #define GSV_VF(CH)                                                                                 \
@@ -1272,7 +1280,7 @@ int voxelize_fwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
                        reinterpret_cast<const int2 *>(tile_bins),                                  \
                        reinterpret_cast<const float4 *>(pos3d_radii),                              \
                        reinterpret_cast<const float2 *>(conics), intensities, volume, target,      \
-                       tile_loss, sgn, pair_live)
+                       tile_loss, sgn, pair_live, wave_rec, wave_cap)
         switch (channels) {
             case 1: GSV_VF(1); break;
             case 2: GSV_VF(2); break;

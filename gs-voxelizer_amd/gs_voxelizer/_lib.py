@@ -48,6 +48,7 @@ SIGNATURES = {
                             _c_size_t, _P],
     "gsv_kernel_timing_enable": [_c_int],
     "gsv_kernel_timing_collect": [_c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_int)],
+    "gsv_wave_timeline": [_c_int, _P, _c_int],
 }
 
 _lib = None

@@ -269,6 +269,19 @@ int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32
 int gsv_kernel_timing_enable(int32_t enable);
 int gsv_kernel_timing_collect(int32_t kernel, double *total_ms, int32_t *count);
 
+/*
+ * Per-workgroup timeline (no counterpart in the reference; for profiling load
+ * balance).  While a buffer is registered, every launch of the forward
+ * voxelize kernel (kernel = 0; the only one supported) writes, for each
+ * workgroup b < capacity that has a tile, records[3b] = its start and
+ * records[3b+1] = its end on the GPU's constant 100 MHz wall clock and
+ * records[3b+2] = its tile index.  `records` is the caller's device buffer of
+ * 3 * capacity uint64; NULL unregisters.  Later launches overwrite earlier
+ * ones; the forward launches one workgroup per tile (rounded up to a multiple
+ * of 64).  Costs one uniform branch per workgroup when unregistered.
+ */
+int gsv_wave_timeline(int32_t kernel, uint64_t *records, int32_t capacity);
+
 #ifdef __cplusplus
 }
 #endif

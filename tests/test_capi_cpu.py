@@ -77,3 +77,12 @@ def test_noalloc_binning_rejects_oversize_before_any_launch():
     assert b"allocation-free" in L.gsv_status_string(6)
     assert L.gsv_bin_and_sort_noalloc(-1, 10, null, null, null, 8, 8, 8,
                                       null, null, null, null) == 1
+
+
+def test_wave_timeline_registration_is_host_only():
+    L = _lib.load()
+    null = ctypes.c_void_p(0)
+    assert L.gsv_wave_timeline(1, null, 0) == 1       # only the forward kernel
+    assert L.gsv_wave_timeline(0, null, -1) == 1
+    assert L.gsv_wave_timeline(0, ctypes.c_void_p(256), 0) == 1
+    assert L.gsv_wave_timeline(0, null, 0) == 0       # unregister
