@@ -74,10 +74,16 @@ namespace {
 std::mutex g_wave_mu;
 uint64_t *g_wave_records = nullptr;
 int g_wave_capacity = 0;
+int g_wave_device = -1;  // the device current when the buffer was registered
 }  // namespace
 
 uint64_t *wave_timeline_buffer(int *capacity) {
     std::lock_guard<std::mutex> lk(g_wave_mu);
+    int dev = -1;
+    if (g_wave_records == nullptr || hipGetDevice(&dev) != hipSuccess || dev != g_wave_device) {
+        *capacity = 0;
+        return nullptr;  // none registered, or registered for another device
+    }
     *capacity = g_wave_capacity;
     return g_wave_records;
 }
@@ -200,8 +206,14 @@ extern "C" int gsv_cumsum_tiles_hit(int32_t n, const int32_t *num_tiles_hit,
 extern "C" int gsv_wave_timeline(int32_t kernel, uint64_t *records, int32_t capacity) {
     if (kernel != 0 || capacity < 0 || (records != nullptr && capacity == 0))
         return GSV_ERR_INVALID_ARGUMENT;
+    int dev = -1;
+    if (records != nullptr) {
+        const hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return record_hip_error(e);
+    }
     std::lock_guard<std::mutex> lk(g_wave_mu);
     g_wave_records = records;
     g_wave_capacity = records ? capacity : 0;
+    g_wave_device = dev;
     return GSV_OK;
 }

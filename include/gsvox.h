@@ -276,7 +276,8 @@ int gsv_kernel_timing_collect(int32_t kernel, double *total_ms, int32_t *count);
  * workgroup b < capacity that has a tile, records[3b] = its start and
  * records[3b+1] = its end on the GPU's constant 100 MHz wall clock and
  * records[3b+2] = its tile index.  `records` is the caller's device buffer of
- * 3 * capacity uint64; NULL unregisters.  Later launches overwrite earlier
+ * 3 * capacity uint64 on the device current at registration, and only launches
+ * on that device record; NULL unregisters.  Later launches overwrite earlier
  * ones; the forward launches one workgroup per tile (rounded up to a multiple
  * of 64).  Costs one uniform branch per workgroup when unregistered.
  */
