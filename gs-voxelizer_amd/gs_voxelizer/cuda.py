@@ -49,6 +49,18 @@ def _check_dtype(t: torch.Tensor, what: str, dtype: torch.dtype) -> None:
         raise RuntimeError(f"{what}: expected scalar type {dtype} but found {t.dtype}")
 
 
+def _check_rows(n: int, tensors) -> None:
+    """The kernels index rows [0, num_points) of every per-Gaussian input: a
+    count beyond a tensor's rows would read past its memory, so it is refused
+    here (the reference's bindings take num_points as given)."""
+    if n < 0:
+        raise RuntimeError(f"num_points must be non-negative, got {n}")
+    for t, w, width in tensors:
+        if t.numel() < n * width:
+            raise RuntimeError(f"{w} holds {t.numel() // max(width, 1)} rows, fewer than "
+                               f"num_points = {n}")
+
+
 def _ptr(t: torch.Tensor):
     return ctypes.c_void_p(t.data_ptr()) if t.numel() > 0 else ctypes.c_void_p(0)
 
@@ -77,6 +89,8 @@ def optim_to_render_forward(num_gaussians: int, pos3d, scale3d, quat, intensitie
         _check_dtype(t, w, torch.float32)
     channels = _channels(intensities)
     n = int(num_gaussians)
+    _check_rows(n, ((pos3d, "pos3d", 3), (scale3d, "scale3d", 3), (quat, "quat", 4),
+                    (intensities, "intensities", channels)))
     D, H, W = (int(v) for v in vol_size_voxel)
     wz, wy, wx = (float(v) for v in vol_size_world)
     cz, cy, cx = (float(v) for v in vol_center_pos)
@@ -109,6 +123,9 @@ def optim_to_render_backward(num_gaussians: int, pos3d, scale3d, quat, vol_size_
                  (dcn, "conics_grad_in"), (pr, "pos3d_radii_out")):
         _check_input(t, w)
         _check_dtype(t, w, torch.float32)
+    _check_rows(n, ((pos3d, "pos3d", 3), (scale3d, "scale3d", 3), (quat, "quat", 4),
+                    (dpr, "pos3d_radii_grad_in", 4), (dcn, "conics_grad_in", 6),
+                    (pr, "pos3d_radii_out", 4)))
     D, H, W = (int(v) for v in vol_size_voxel)
     wz, wy, wx = (float(v) for v in vol_size_world)
     cz, cy, cx = (float(v) for v in vol_center_pos)
@@ -163,6 +180,8 @@ def bin_and_sort_gaussians(num_gaussians: int, num_intersects: int, tile_min, ti
     D, H, W = (int(v) for v in vol_size)
     dev = tile_min.device
     n, I = int(num_gaussians), int(num_intersects)
+    _check_rows(n, ((tile_min, "tile_min", 3), (tile_max, "tile_max", 3),
+                    (cum_tiles_hit, "cum_tiles_hit", 1)))
     i32 = dict(device=dev, dtype=torch.int32)
     tile_bins = torch.empty((T, 2), **i32)
     ids = torch.empty((max(I, 0),), **i32)
@@ -198,6 +217,8 @@ def bin_and_sort_gaussians_device_count(num_gaussians: int, capacity: int, num_i
     D, H, W = (int(v) for v in vol_size)
     dev = tile_min.device
     n, cap = int(num_gaussians), max(int(capacity), 0)
+    _check_rows(n, ((tile_min, "tile_min", 3), (tile_max, "tile_max", 3),
+                    (cum_tiles_hit, "cum_tiles_hit", 1)))
     i32 = dict(device=dev, dtype=torch.int32)
     tile_bins = torch.empty((Tx * Ty * Tz, 2), **i32)
     ids = torch.empty((cap,), **i32)

@@ -119,3 +119,34 @@ def test_projection_backward_regulariser_closed_form(device, s_vox):
     report_close(f"dscale closed form s={s_vox}", np32(ds), want, rtol=1e-4,
                  atol=1e-6 * np.abs(want).max())
     assert np.abs(np32(dq)).max() <= 1e-6 * np.abs(want).max()
+
+
+def test_num_points_beyond_the_rows_is_refused(device):
+    """A num_points larger than the per-Gaussian tensors is refused before any
+    launch (the kernels would index past the tensors), in projection forward
+    and backward and in binning; the GPU is not touched by the refused calls."""
+    import gs_voxelizer.cuda as _C
+    work = S.make_gaussians(small_config(1, 64, vol=(16, 16, 16)), seed=2)
+    w = work.to(device)
+    cfg = work.cfg
+    n = w.pos3d.shape[0]
+    with pytest.raises(RuntimeError, match="num_points"):
+        _C.optim_to_render_forward(n + 1, w.pos3d, w.scale3d, w.quat, w.intensities, cfg.vol,
+                                   cfg.world, cfg.center)
+    pr, cn, tmin, tmax, nt = _C.optim_to_render_forward(n, w.pos3d, w.scale3d, w.quat,
+                                                        w.intensities, cfg.vol, cfg.world,
+                                                        cfg.center)
+    with pytest.raises(RuntimeError, match="num_points"):
+        _C.optim_to_render_backward(n + 1, w.pos3d, w.scale3d, w.quat, cfg.vol, cfg.world,
+                                    cfg.center, torch.zeros_like(pr), torch.zeros_like(cn), pr)
+    cum, total = _C.cumsum_tiles_hit(nt)
+    I = int(total.item())
+    with pytest.raises(RuntimeError, match="num_points"):
+        _C.bin_and_sort_gaussians(n + 1, I, tmin, tmax, cum, cfg.vol)
+    with pytest.raises(RuntimeError, match="num_points"):
+        _C.bin_and_sort_gaussians_device_count(n + 1, I, total, tmin, tmax, cum, cfg.vol)
+    with pytest.raises(RuntimeError, match="non-negative"):
+        _C.bin_and_sort_gaussians(-1, I, tmin, tmax, cum, cfg.vol)
+    ids, bins = _C.bin_and_sort_gaussians(n, I, tmin, tmax, cum, cfg.vol)
+    torch.cuda.synchronize()
+    assert ids.numel() == I
