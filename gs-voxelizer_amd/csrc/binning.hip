@@ -1,31 +1,41 @@
-// binning.hip — (tile, gaussian) key duplication, stable LSD radix sort over the
+// binning.hip — (tile, gaussian) key duplication, a stable sort over the
 // significant tile-id bits, and tile-range extraction, for gfx950.
 //
 // Reference: gs_voxelizer/cuda/bin_and_sort_gaussians.cu:11-62 and the binding
 // bindings.cu:259-360 (which sorts all 32 key bits with cub::DeviceRadixSort).
-// Keys are tile ids < T, so only ceil(log2 T) bits are sorted here (15 at 256^3:
-// two 8-bit passes instead of four; 17 or 18, e.g. 512^3: two 9-bit passes
-// instead of three).  Because the keys are emitted
-// gaussian-major and every pass is stable, the result is the reference's exact
-// order: ascending tile, then ascending gaussian id.
+// Keys are tile ids < T, so only bits = ceil(log2 T) bits are sorted (15 at
+// 256^3, 18 at 512^3).  Because the keys are emitted gaussian-major and every
+// step is stable, the result is the reference's exact order: ascending tile,
+// then ascending gaussian id.  Two paths give the same bits:
 //
-// Kernels (7 launches for two passes):
+// Bucket path (keys of up to 18 bits, up to ~24k pairs per bucket on average:
+// 256^3 / 200k, 512^3 up to ~12M pairs), four launches:
 //   k_emit_chunk     block b writes emission slots [4096 b, 4096 b + 4096) and
-//                    the first pass's digit histogram of that chunk; it also
-//                    zero-fills tile_bins;
+//                    that chunk's histogram of the key's top digit (8 bits, or
+//                    9 for 17- and 18-bit keys);
 //   k_digit_scan     one block per digit: exclusive prefix of the per-chunk
 //                    counts over chunks, plus the digit total;
-//   k_radix_scatter  stable scatter of one 4096-key chunk; ranks come from wave
-//                    ballots within each wave's contiguous 1024 keys, so the
-//                    block synchronises a handful of times per chunk;
+//   k_radix_scatter  stable scatter on the top digit, writing one packed word
+//                    per pair (gaussian << lb | the lb low tile bits), so that
+//                    every bucket of 2^lb tiles is one contiguous run;
+//   k_bucket_sort    one 1024-thread block per bucket sorts it by the low bits
+//                    in LDS and writes ids, tiles and tile_bins.
+// LSD path (wider keys, heavier buckets), 7 launches for two passes:
+//   k_emit_chunk     as above, with the histogram of the lowest digit; it also
+//                    zero-fills tile_bins;
+//   k_digit_scan, k_radix_scatter (keys and ids) per pass;
 //   k_radix_hist     per-chunk digit histogram for the later passes;
 //   k_tile_edges     [start, end) per tile, 16 sorted keys per thread.
 // Every kernel reads the live pair count from device memory when one is given
 // (capped by the capacity its grid was sized for), so the host need not know
 // the count before launching.
 //
-// Data movement per pair: emission writes 8 B; each pass reads 8 B and writes
-// 8 B (later passes read 4 B more for the histogram); the range pass reads 4 B.
+// Data movement per pair, bucket path: emission writes 8 B, the scatter reads
+// 8 B and writes 4 B, the bucket sort reads 4 B and writes 8 B (4 without the
+// tiles).  LSD path: emission writes 8 B; each pass reads 8 B and writes 8 B
+// (later passes read 4 B more for the histogram); the range pass reads 4 B.
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 #include "gsv_device.h"
@@ -67,22 +77,24 @@ __device__ __forceinline__ int64_t live_count(int64_t cap, const int64_t *d_n) {
 // Gaussians that follow in LDS (in rounds of 512 until they cover the chunk,
 // at most kWindow; beyond that it reads global memory), and gives each thread
 // 8 consecutive slots: one search and one division per thread, then stepping
-// through the box.  The chunk's digit histogram for the first radix pass is
-// written digit-major: hist[d * hstride + b].
+// through the box.  The chunk's histogram of the first pass's digit, bits
+// [shift, shift + B) of the key, is written digit-major: hist[d * hstride + b].
+// tile_bins (when given) is zero-filled for k_tile_edges.
 template <int B>
 __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
     int n, int64_t cap, const int64_t *__restrict__ d_n, const int *__restrict__ tile_min,
     const int *__restrict__ tile_max, const int *__restrict__ cum, int Tx, int Ty, int64_t T,
     int *__restrict__ keys, int *__restrict__ vals, int *__restrict__ hist, int hstride,
-    int2 *__restrict__ tile_bins) {
+    int shift, int2 *__restrict__ tile_bins) {
     __shared__ int s_cum[kWindow];
     constexpr int kBins = 1 << B;
     __shared__ int s_box[kWindow][6];  // min x, y, z; extent x, y, z
     __shared__ int s_hist[kBins];
     const int t = threadIdx.x;
-    for (int64_t i = (int64_t)blockIdx.x * kEmitThreads + t; i < T;
-         i += (int64_t)gridDim.x * kEmitThreads)
-        tile_bins[i] = make_int2(0, 0);
+    if (tile_bins != nullptr)
+        for (int64_t i = (int64_t)blockIdx.x * kEmitThreads + t; i < T;
+             i += (int64_t)gridDim.x * kEmitThreads)
+            tile_bins[i] = make_int2(0, 0);
     if (t < kBins) s_hist[t] = 0;
     const int64_t total = live_count(cap, d_n);
     const int64_t base = (int64_t)blockIdx.x * kChunk;
@@ -216,7 +228,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_chunk(
         }
 #pragma unroll
         for (int k = 0; k < kEmitItems; ++k)
-            if (p0 + k < total) atomicAdd(&s_hist[key[k] & (kBins - 1)], 1);
+            if (p0 + k < total) atomicAdd(&s_hist[(key[k] >> shift) & (kBins - 1)], 1);
     }
     __syncthreads();
     if (t < kBins) hist[(int64_t)t * hstride + blockIdx.x] = s_hist[t];
@@ -358,12 +370,14 @@ __device__ __forceinline__ int block_excl_scan(int v, int *s_wtot) {
 // 30M pairs) and costs ~1 us per pass below it, where it is left off.
 // With 9-bit digits each thread handles digits t and t + 256 in the per-digit
 // steps; the block scans over digits then run in two rounds.
+// With pack >= 0 (the bucket path) only vout is written, one word per pair:
+// (val << pack) | the key's low pack bits.
 template <int B>
 __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
     const int *__restrict__ kin, const int *__restrict__ vin, int *__restrict__ kout,
     int *__restrict__ vout, int64_t cap, const int64_t *__restrict__ d_n, int shift,
     const int *__restrict__ hist_scanned, const int *__restrict__ totals, int nblocks,
-    int hstride, int remap) {
+    int hstride, int remap, int pack) {
     constexpr int kBins = 1 << B;
     constexpr int kPer = kBins / kSortThreads;  // digits per thread in the per-digit steps
     __shared__ int s_keys[kChunk];
@@ -471,8 +485,12 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
             const int kk = s_keys[p];
             const int d = (kk >> shift) & (kBins - 1);
             const int64_t dst = (int64_t)s_gbase[d] + (p - s_start[d]);
-            kout[dst] = kk;
-            vout[dst] = s_vals[p];
+            if (pack >= 0) {
+                vout[dst] = (int)(((unsigned)s_vals[p] << pack) | ((unsigned)kk & ((1u << pack) - 1u)));
+            } else {
+                kout[dst] = kk;
+                vout[dst] = s_vals[p];
+            }
         }
     }
 }
@@ -511,19 +529,174 @@ __global__ __launch_bounds__(256) void k_tile_edges(const int *__restrict__ keys
     }
 }
 
+// Second stage of the bucket path.  One stable scatter on the key's top digit
+// (bits [lb, lb + B)) has left every bucket of 2^lb consecutive tiles as one
+// contiguous run of packed words (gaussian << lb | low lb bits of the tile),
+// in emission order; block b sorts bucket b by its low lb bits and writes the
+// ids, the tiles (optional) and tile_bins of its tiles.
+//   1. wave w counts the words of its contiguous segment per tile in its own
+//      row of LDS counters;
+//   2. one thread per tile turns the rows into per-(wave, tile) offsets and the
+//      tile's [start, end) (tiles without pairs get [0, 0), as the reference's
+//      zero-initialised tile_bins has them);
+//   3. each wave walks its segment in order, 64 words a round: ballot-ranked
+//      among the round's lanes with the same tile, plus the wave's running
+//      counter, which gives the stable position directly.
+// A wave loads up to kBatch rounds at once (all in flight), and keeps them in
+// registers from step 1 to step 3 when its segment is one batch (buckets of
+// up to 18,432 pairs).  Sorted words go to LDS when the bucket fits (then
+// copied out coalesced: unstaged, scattered 4-byte stores cost 22 us more at
+// 256^3 / 200k), else straight to global memory (an outsized bucket of a
+// clustered scene: slower, same result).  A slot with an invalid key
+// (cum inconsistent with the boxes) falls in the last bucket at the all-ones
+// low digit, as in the LSD path, and its tile reads 2^bits - 1.
+constexpr int kBucketThreads = 1024;
+constexpr int kBucketWaves = kBucketThreads / kWave;
+constexpr int kBatch = 18;  // rounds of 64 words per wave and batch
+static_assert((1 << kRadixBitsMax) <= kBucketThreads, "one tile per thread in the offset step");
+
+// LB: the widest low digit served (8 with an 8-bit top digit, 9 with a 9-bit
+// one).  The staging area takes what the 160 KiB of LDS leave beside the
+// counters: 140 KiB (LB = 8) or 120 KiB (LB = 9), one workgroup per CU.
+template <int LB>
+constexpr int kStageWords = (LB <= 8 ? 140 : 120) * 1024 / 4;
+
+template <int LB>
+__global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
+    const unsigned *__restrict__ pin, int *__restrict__ kout, int *__restrict__ vout,
+    const int *__restrict__ totals, int lb, int64_t T, int2 *__restrict__ tile_bins) {
+    __shared__ int s_cnt[kBucketWaves << LB];
+    __shared__ int s_wtot[kBucketWaves];
+    __shared__ unsigned s_stage[kStageWords<LB>];
+    const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
+    const int b = blockIdx.x, nb = 1 << lb;
+    const unsigned lmask = (unsigned)nb - 1u;
+    int start;
+    {
+        int tot;
+        block_scan_total<kBucketThreads>(t < b ? totals[t] : 0, s_wtot, &tot);
+        start = tot;
+    }
+    const int size = totals[b];
+    for (int i = t; i < kBucketWaves * nb; i += kBucketThreads) s_cnt[i] = 0;
+    // segments of whole 64-word rounds, in bucket order; batches of kBatch rounds
+    const int seg = (size + kBucketWaves * kWave - 1) / (kBucketWaves * kWave) * kWave;
+    const int s0 = min(wave * seg, size), s1 = min(s0 + seg, size);
+    const int nbatch = (seg + kBatch * kWave - 1) / (kBatch * kWave);  // same for every wave
+    const unsigned *pb = pin + start;
+    int *cnt = s_cnt + wave * nb;
+    unsigned w[kBatch];
+    auto load = [&](int j) {
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+            const int i = s0 + (j * kBatch + q) * kWave + lane;
+            w[q] = i < s1 ? pb[i] : 0u;
+        }
+    };
+    __syncthreads();  // counters zeroed; s_wtot free again
+    for (int j = 0; j < nbatch; ++j) {
+        load(j);
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q)
+            if (s0 + (j * kBatch + q) * kWave + lane < s1) atomicAdd(&cnt[w[q] & lmask], 1);
+    }
+    __syncthreads();
+    {
+        int run = 0;
+        if (t < nb) {
+#pragma unroll 4
+            for (int v = 0; v < kBucketWaves; ++v) {
+                const int c = s_cnt[v * nb + t];
+                s_cnt[v * nb + t] = run;
+                run += c;
+            }
+        }
+        int tot;
+        const int kstart = block_scan_total<kBucketThreads>(run, s_wtot, &tot);
+        if (t < nb) {
+#pragma unroll 4
+            for (int v = 0; v < kBucketWaves; ++v) s_cnt[v * nb + t] += kstart;
+            const int64_t tile = (int64_t)b * nb + t;
+            if (tile < T)
+                tile_bins[tile] = run > 0 ? make_int2(start + kstart, start + kstart + run)
+                                          : make_int2(0, 0);
+        }
+    }
+    const bool staged = size <= kStageWords<LB>;
+    const int tile0 = b << lb;
+    __syncthreads();
+    const uint64_t lt = lanemask_lt();
+    for (int j = 0; j < nbatch; ++j) {
+        if (nbatch > 1) load(j);
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+            const int i0 = s0 + (j * kBatch + q) * kWave;
+            if (i0 >= s1) break;  // uniform in the wave
+            const bool valid = i0 + lane < s1;
+            const int d = (int)(w[q] & lmask);
+            const uint64_t vm = __ballot(valid);
+            uint32_t plo = (uint32_t)vm, phi = (uint32_t)(vm >> 32);
+            for (int bit = 0; bit < lb; ++bit) {  // lanes whose low digit equals d
+                const uint32_t x = (uint32_t)__builtin_amdgcn_sbfe(d, bit, 1);
+                const uint64_t m = __ballot(x != 0u);
+                plo &= ~((uint32_t)m ^ x);
+                phi &= ~((uint32_t)(m >> 32) ^ x);
+            }
+            const uint64_t peers = ((uint64_t)phi << 32) | plo;
+            const int r = __popcll(peers & lt);
+            const int off = cnt[d];  // the wave's own counter: LDS keeps read-then-write order
+            if (valid && r == 0) cnt[d] = off + __popcll(peers);
+            if (valid) {
+                const int pos = off + r;
+                if (staged) {
+                    s_stage[pos] = w[q];
+                } else {
+                    vout[start + pos] = (int)(w[q] >> lb);
+                    if (kout) kout[start + pos] = tile0 | d;
+                }
+            }
+        }
+    }
+    if (staged) {
+        __syncthreads();
+        for (int i = t; i < size; i += kBucketThreads) {
+            const unsigned x = s_stage[i];
+            vout[start + i] = (int)(x >> lb);
+            if (kout) kout[start + i] = tile0 | (int)(x & lmask);
+        }
+    }
+}
+
 struct BinLayout {
     size_t keys_a, vals_a, keys_b, hist, totals, total;
     int bits, passes, nblocks, hstride;  // digit width; hist row stride, a multiple of 4
+    bool bucket;  // one scatter on the top digit + k_bucket_sort, instead of LSD passes
+    int lb;       // bucket path: low bits sorted inside a bucket
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-BinLayout bin_layout(int64_t cap, int64_t n_tiles) {
+// The bucket path serves keys of up to 18 bits while the buckets stay small
+// enough for one workgroup each (mean below kBucketMeanMax pairs); heavier
+// scenes (e.g. 118M pairs on 2^15 tiles) keep the LSD passes, whose every
+// pass spreads over all CUs.  GSV_BINNING=lsd or =bucket overrides the
+// choice (bucket only where the key width allows it), so that tests can run
+// both paths on one scene; the workspace is the same either way.
+constexpr int64_t kBucketMeanMax = 24576;
+
+BinLayout bin_layout(int64_t cap, int64_t n_tiles, int64_t n) {
     BinLayout L{};
     int bits = 0;
     while (bits < 31 && ((int64_t)1 << bits) < n_tiles) ++bits;
     L.bits = (bits == 17 || bits == 18) ? 9 : 8;
     L.passes = (bits + L.bits - 1) / L.bits;
+    L.lb = bits > L.bits ? bits - L.bits : 0;
+    // low digit of at most 9 bits, and gaussian ids that fit beside it in a word
+    const bool allow = bits <= 18 && n <= ((int64_t)1 << (32 - L.lb));
+    const char *force = getenv("GSV_BINNING");
+    if (force && strcmp(force, "lsd") == 0) L.bucket = false;
+    else if (force && strcmp(force, "bucket") == 0) L.bucket = allow;
+    else L.bucket = allow && cap <= ((int64_t)1 << L.bits) * kBucketMeanMax;
     L.nblocks = (int)((cap + kChunk - 1) / kChunk);
     L.hstride = (imax64(L.nblocks, 1) + 3) / 4 * 4;
     const size_t arr = align256((size_t)cap * sizeof(int));
@@ -548,7 +721,7 @@ int emit_and_sort(const BinLayout &L, int32_t n, int64_t cap, const int64_t *d_c
     int *kin = (L.passes % 2 == 0) ? kb : ka;
     int *vin = (L.passes % 2 == 0) ? vb : va;
     hipLaunchKernelGGL(k_emit_chunk<B>, dim3(L.nblocks), dim3(kEmitThreads), 0, s, n, cap,
-                       d_count, tile_min, tile_max, cum, Tx, Ty, T, kin, vin, hist, L.hstride,
+                       d_count, tile_min, tile_max, cum, Tx, Ty, T, kin, vin, hist, L.hstride, 0,
                        reinterpret_cast<int2 *>(tile_bins));
     if (int st = check_launch()) return st;
     for (int p = 0; p < L.passes; ++p) {
@@ -567,13 +740,42 @@ int emit_and_sort(const BinLayout &L, int32_t n, int64_t cap, const int64_t *d_c
         hipLaunchKernelGGL(k_radix_scatter<B>,
                            dim3((unsigned)(remap ? kXcds * xcd_per(L.nblocks) : L.nblocks)),
                            dim3(kSortThreads), 0, s, kin, vin, kout, vout, cap, d_count, shift,
-                           hist, totals, L.nblocks, L.hstride, remap);
+                           hist, totals, L.nblocks, L.hstride, remap, -1);
         if (int st = check_launch()) return st;
         kin = kout;
         vin = vout;
     }
     *keys_sorted = kin;
     return GSV_OK;
+}
+
+// The bucket path with a B-bit top digit: emission into (ka, ids_out), one
+// stable scatter on bits [lb, lb + B) into va as packed words, then
+// k_bucket_sort into (tiles_out, ids_out) and tile_bins.  Four launches.
+template <int B>
+int emit_and_bucket_sort(const BinLayout &L, int32_t n, int64_t cap, const int64_t *d_count,
+                         const int32_t *tile_min, const int32_t *tile_max, const int32_t *cum,
+                         int Tx, int Ty, int64_t T, int *ka, int *va, int *hist, int *totals,
+                         int32_t *ids_out, int32_t *tiles_out, int32_t *tile_bins,
+                         hipStream_t s) {
+    hipLaunchKernelGGL(k_emit_chunk<B>, dim3(L.nblocks), dim3(kEmitThreads), 0, s, n, cap,
+                       d_count, tile_min, tile_max, cum, Tx, Ty, T, ka, ids_out, hist, L.hstride,
+                       L.lb, static_cast<int2 *>(nullptr));
+    if (int st = check_launch()) return st;
+    hipLaunchKernelGGL(k_digit_scan, dim3(1u << B), dim3(kDigitScanThreads), 0, s, hist,
+                       L.nblocks, L.hstride, totals);
+    if (int st = check_launch()) return st;
+    const int remap = L.nblocks > kRemapChunks ? 1 : 0;
+    hipLaunchKernelGGL(k_radix_scatter<B>,
+                       dim3((unsigned)(remap ? kXcds * xcd_per(L.nblocks) : L.nblocks)),
+                       dim3(kSortThreads), 0, s, ka, ids_out, static_cast<int *>(nullptr), va, cap,
+                       d_count, L.lb, hist, totals, L.nblocks, L.hstride, remap, L.lb);
+    if (int st = check_launch()) return st;
+    // every tile of [0, 2^bits) lies in one of the 2^B buckets
+    hipLaunchKernelGGL(k_bucket_sort<B>, dim3(1u << B), dim3(kBucketThreads), 0, s,
+                       reinterpret_cast<const unsigned *>(va), tiles_out, ids_out, totals, L.lb,
+                       T, reinterpret_cast<int2 *>(tile_bins));
+    return check_launch();
 }
 
 // tiles_out (optional, 16-byte aligned, cap entries): the sorted keys, i.e. the
@@ -592,16 +794,24 @@ int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *
     if (!tile_min || !tile_max || !cum || !ids_out || !workspace) return GSV_ERR_INVALID_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(ids_out) & 15) != 0) return GSV_ERR_INVALID_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(tiles_out) & 15) != 0) return GSV_ERR_INVALID_ARGUMENT;
-    const BinLayout L = bin_layout(cap, T);
+    const BinLayout L = bin_layout(cap, T, n);
     if (workspace_bytes < L.total + 256) return GSV_ERR_WORKSPACE_TOO_SMALL;
     char *ws = static_cast<char *>(workspace);
     ws += (256 - (reinterpret_cast<uintptr_t>(ws) & 255)) & 255;  // 16-byte vector access
     int *ka = reinterpret_cast<int *>(ws + L.keys_a);
     int *va = reinterpret_cast<int *>(ws + L.vals_a);
-    int *kb = tiles_out ? tiles_out : reinterpret_cast<int *>(ws + L.keys_b);
-    int *vb = ids_out;
     int *hist = reinterpret_cast<int *>(ws + L.hist);
     int *totals = reinterpret_cast<int *>(ws + L.totals);
+    if (L.bucket) {
+        return L.bits == 9 ? emit_and_bucket_sort<9>(L, n, cap, d_count, tile_min, tile_max, cum,
+                                                     Tx, Ty, T, ka, va, hist, totals, ids_out,
+                                                     tiles_out, tile_bins, s)
+                           : emit_and_bucket_sort<8>(L, n, cap, d_count, tile_min, tile_max, cum,
+                                                     Tx, Ty, T, ka, va, hist, totals, ids_out,
+                                                     tiles_out, tile_bins, s);
+    }
+    int *kb = tiles_out ? tiles_out : reinterpret_cast<int *>(ws + L.keys_b);
+    int *vb = ids_out;
     int *keys_sorted = nullptr;
     const int st = L.bits == 9 ? emit_and_sort<9>(L, n, cap, d_count, tile_min, tile_max, cum, Tx,
                                                   Ty, T, ka, va, kb, vb, hist, totals, tile_bins,
@@ -673,7 +883,7 @@ extern "C" int gsv_bin_workspace_bytes(int32_t n, int64_t num_intersects, int32_
     if (!bytes || n < 0 || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
     if (num_intersects > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
     const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
-    const BinLayout L = bin_layout(num_intersects > 0 ? num_intersects : 0, T);
+    const BinLayout L = bin_layout(num_intersects > 0 ? num_intersects : 0, T, n);
     *bytes = L.total + 256;
     return GSV_OK;
 }
@@ -710,7 +920,7 @@ extern "C" int gsv_bin_and_sort_noalloc(int32_t n, int64_t num_intersects,
     if (n < 0 || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
     const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
     if (T > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
-    if (bin_layout(num_intersects > 0 ? num_intersects : 0, T).total + 256 > kNoAllocScratchBytes)
+    if (bin_layout(num_intersects > 0 ? num_intersects : 0, T, n).total + 256 > kNoAllocScratchBytes)
         return GSV_ERR_SCRATCH_TOO_SMALL;
     void *ws = nullptr;
     if (int st = noalloc_scratch(&ws)) return st;

@@ -109,6 +109,11 @@ int gsv_cumsum_tiles_hit(int32_t n, const int32_t *num_tiles_hit, int32_t *cum_t
  * aligned) receives the sorted keys: the tile id of each sorted pair, which
  * gsv_voxelize_bwd can take instead of rebuilding it from tile_bins.  The
  * reference keeps these keys in a scratch tensor (bindings.cu:295-345).
+ * The library sorts with one of two methods of equal result (a top-digit
+ * split into per-bucket sorts, or LSD radix passes), chosen by the key width,
+ * the pair count and the Gaussian count; the environment variable
+ * GSV_BINNING=lsd or =bucket overrides the choice (for tests).  The workspace
+ * size does not depend on it.
  */
 int gsv_bin_workspace_bytes(int32_t n, int64_t num_intersects, int32_t D, int32_t H, int32_t W,
                             size_t *bytes);

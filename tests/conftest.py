@@ -24,3 +24,15 @@ def device():
     if not torch.cuda.is_available():
         pytest.skip("no HIP device visible")
     return torch.device("cuda:0")
+
+
+@pytest.fixture(params=["auto", "lsd", "bucket"])
+def binning_path(request, monkeypatch):
+    """Binning through each of the library's two sort paths (GSV_BINNING: the
+    LSD passes, or one top-digit scatter plus per-bucket sorts) and through
+    its own choice; both must give the same bits."""
+    if request.param == "auto":
+        monkeypatch.delenv("GSV_BINNING", raising=False)
+    else:
+        monkeypatch.setenv("GSV_BINNING", request.param)
+    return request.param

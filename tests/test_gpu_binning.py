@@ -44,7 +44,7 @@ def _bin_cases():
 
 
 @pytest.mark.parametrize("name,work", list(_bin_cases()), ids=lambda v: v if isinstance(v, str) else "")
-def test_binning_matches_oracle_bit_exact(device, name, work):
+def test_binning_matches_oracle_bit_exact(device, binning_path, name, work):
     cfg = work.cfg
     n = work.pos3d.shape[0]
     rpr, rcn, rtmin, rtmax, rnt = oracle_project(work)
@@ -60,7 +60,7 @@ def test_binning_matches_oracle_bit_exact(device, name, work):
     np.testing.assert_array_equal(np32(ids), rids, err_msg=f"{name}: gaussian_ids_sorted")
 
 
-def test_binning_empty(device):
+def test_binning_empty(device, binning_path):
     import gs_voxelizer.cuda as _C
     z = torch.zeros((3, 3), dtype=torch.int32, device=device)
     cum = torch.zeros((3,), dtype=torch.int32, device=device)
@@ -100,7 +100,7 @@ def _device_count_bin(device, n, tmin, tmax, nt, vol, capacity):
 @pytest.mark.parametrize("name,work", [c for c in _bin_cases() if c[0] in
                                        ("cfg1", "few_tiles", "three_passes", "clustered_heavy")],
                          ids=lambda v: v if isinstance(v, str) else "")
-def test_device_count_binning_matches_host_count(device, name, work):
+def test_device_count_binning_matches_host_count(device, binning_path, name, work):
     """The count read on the device, capacity above it: same bits as the oracle."""
     cfg = work.cfg
     n = work.pos3d.shape[0]
@@ -114,7 +114,7 @@ def test_device_count_binning_matches_host_count(device, name, work):
     np.testing.assert_array_equal(ids[:rI], rids)
 
 
-def test_device_count_binning_over_capacity_sorts_the_prefix(device):
+def test_device_count_binning_over_capacity_sorts_the_prefix(device, binning_path):
     """Capacity below the count: exactly the first `capacity` emitted pairs are
     sorted (stable by tile), and the call neither fails nor writes past it."""
     work = S.make_gaussians(small_config(1, 3000, vol=(40, 48, 56)), seed=3)
@@ -132,7 +132,7 @@ def test_device_count_binning_over_capacity_sorts_the_prefix(device):
     np.testing.assert_array_equal(bins[:, 1] - bins[:, 0], counts)
 
 
-def test_binning_long_runs_of_empty_gaussians(device):
+def test_binning_long_runs_of_empty_gaussians(device, binning_path):
     """Runs of 5000 Gaussians without tiles between large boxes: chunks whose
     Gaussians lie beyond the emission block's cached window of cum."""
     import gs_voxelizer.cuda as _C

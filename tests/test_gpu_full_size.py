@@ -69,6 +69,21 @@ def test_binning_bit_exact(full):
     np.testing.assert_array_equal(np.bincount(np32(P["tiles"]), minlength=counts.size), counts)
 
 
+@pytest.mark.parametrize("path", ["lsd", "bucket"])
+def test_binning_each_path_same_bits(full, path, monkeypatch):
+    """Both sort paths at full size (cfg5 through the bucket path: buckets of
+    ~460k pairs, far beyond the LDS staging) give the bits checked above."""
+    import gs_voxelizer.cuda as _C
+    P = full
+    cfg = P["work"].cfg
+    monkeypatch.setenv("GSV_BINNING", path)
+    ids, bins, tiles = _C.bin_and_sort_gaussians(cfg.n, P["I"], P["tmin"], P["tmax"], P["cum"],
+                                                 cfg.vol, return_tiles=True)
+    assert torch.equal(bins, P["bins"])
+    assert torch.equal(ids, P["ids"])
+    assert torch.equal(tiles, P["tiles"])
+
+
 def test_forward_first_tile_layer(full):
     import gs_voxelizer.cuda as _C
     P = full

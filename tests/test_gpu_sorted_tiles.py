@@ -50,7 +50,7 @@ def _tiles_from_bins(bins, I):
 
 
 @pytest.mark.parametrize("name,work", list(_cases()), ids=lambda v: v if isinstance(v, str) else "")
-def test_tiles_sorted_is_the_tile_of_each_sorted_pair(device, name, work):
+def test_tiles_sorted_is_the_tile_of_each_sorted_pair(device, binning_path, name, work):
     import gs_voxelizer.cuda as _C
     cfg = work.cfg
     w, n, pr, cn, tmin, tmax, nt = _project(work, device)
