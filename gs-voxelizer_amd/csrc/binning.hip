@@ -8,32 +8,40 @@
 // step is stable, the result is the reference's exact order: ascending tile,
 // then ascending gaussian id.  Two paths give the same bits:
 //
-// Bucket path (keys of up to 18 bits, up to ~24k pairs per bucket on average:
-// 256^3 / 200k, 512^3 up to ~12M pairs), four launches:
-//   k_emit_chunk     block b writes emission slots [4096 b, 4096 b + 4096) and
-//                    that chunk's histogram of the key's top digit (8 bits, or
-//                    9 for 17- and 18-bit keys);
+// Bucket path (padded keys of up to 18 bits, up to ~24k pairs per bucket on
+// average: 256^3 / 200k, 512^3 up to ~12M pairs), four launches.  It sorts
+// padded keys (tile row << xb | tx, 2^xb >= Tx), which order the pairs as the
+// tile ids do, and whose low bits hold whole tile rows, so that each row of a
+// Gaussian's box falls in one bucket:
+//   k_bucket_hist    per chunk of 256 Gaussians, its pair count per top digit
+//                    (8 bits, or 9 for 17- and 18-bit keys), from the boxes'
+//                    rows (no pair is emitted);
 //   k_digit_scan     one block per digit: exclusive prefix of the per-chunk
 //                    counts over chunks, plus the digit total;
-//   k_radix_scatter  stable scatter on the top digit, writing one packed word
-//                    per pair (gaussian << lb | the lb low tile bits), so that
-//                    every bucket of 2^lb tiles is one contiguous run;
+//   k_bucket_split   stable split of the chunk's box rows by top digit, each
+//                    row ranked once and expanded into one packed word per
+//                    pair (gaussian << lb | the lb low key bits), so that every
+//                    bucket of 2^lb keys is one contiguous run;
 //   k_bucket_sort    one 1024-thread block per bucket sorts it by the low bits
 //                    in LDS and writes ids, tiles and tile_bins.
+// These read cum and the boxes, never the pair count: slots at or above the
+// capacity are left out.
 // LSD path (wider keys, heavier buckets), 7 launches for two passes:
-//   k_emit_chunk     as above, with the histogram of the lowest digit; it also
+//   k_emit_chunk     block b writes emission slots [4096 b, 4096 b + 4096) and
+//                    that chunk's histogram of the lowest digit; it also
 //                    zero-fills tile_bins;
 //   k_digit_scan, k_radix_scatter (keys and ids) per pass;
 //   k_radix_hist     per-chunk digit histogram for the later passes;
 //   k_tile_edges     [start, end) per tile, 16 sorted keys per thread.
-// Every kernel reads the live pair count from device memory when one is given
-// (capped by the capacity its grid was sized for), so the host need not know
-// the count before launching.
+// Every LSD kernel reads the live pair count from device memory when one is
+// given (capped by the capacity its grid was sized for), so the host need not
+// know the count before launching.
 //
-// Data movement per pair, bucket path: emission writes 8 B, the scatter reads
-// 8 B and writes 4 B, the bucket sort reads 4 B and writes 8 B (4 without the
-// tiles).  LSD path: emission writes 8 B; each pass reads 8 B and writes 8 B
-// (later passes read 4 B more for the histogram); the range pass reads 4 B.
+// Data movement per pair, bucket path: the split writes 4 B, the bucket sort
+// reads 4 B and writes 8 B (4 without the tiles); the boxes are read twice
+// (28 B per Gaussian each time).  LSD path: emission writes 8 B; each pass
+// reads 8 B and writes 8 B (later passes read 4 B more for the histogram); the
+// range pass reads 4 B.
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -370,14 +378,12 @@ __device__ __forceinline__ int block_excl_scan(int v, int *s_wtot) {
 // 30M pairs) and costs ~1 us per pass below it, where it is left off.
 // With 9-bit digits each thread handles digits t and t + 256 in the per-digit
 // steps; the block scans over digits then run in two rounds.
-// With pack >= 0 (the bucket path) only vout is written, one word per pair:
-// (val << pack) | the key's low pack bits.
 template <int B>
 __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
     const int *__restrict__ kin, const int *__restrict__ vin, int *__restrict__ kout,
     int *__restrict__ vout, int64_t cap, const int64_t *__restrict__ d_n, int shift,
     const int *__restrict__ hist_scanned, const int *__restrict__ totals, int nblocks,
-    int hstride, int remap, int pack) {
+    int hstride, int remap) {
     constexpr int kBins = 1 << B;
     constexpr int kPer = kBins / kSortThreads;  // digits per thread in the per-digit steps
     __shared__ int s_keys[kChunk];
@@ -485,12 +491,8 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
             const int kk = s_keys[p];
             const int d = (kk >> shift) & (kBins - 1);
             const int64_t dst = (int64_t)s_gbase[d] + (p - s_start[d]);
-            if (pack >= 0) {
-                vout[dst] = (int)(((unsigned)s_vals[p] << pack) | ((unsigned)kk & ((1u << pack) - 1u)));
-            } else {
-                kout[dst] = kk;
-                vout[dst] = s_vals[p];
-            }
+            kout[dst] = kk;
+            vout[dst] = s_vals[p];
         }
     }
 }
@@ -529,47 +531,291 @@ __global__ __launch_bounds__(256) void k_tile_edges(const int *__restrict__ keys
     }
 }
 
-// Second stage of the bucket path.  One stable scatter on the key's top digit
-// (bits [lb, lb + B)) has left every bucket of 2^lb consecutive tiles as one
-// contiguous run of packed words (gaussian << lb | low lb bits of the tile),
-// in emission order; block b sorts bucket b by its low lb bits and writes the
-// ids, the tiles (optional) and tile_bins of its tiles.
-//   1. wave w counts the words of its contiguous segment per tile in its own
+// ------------------------------------------------ bucket path: box rows --
+//
+// The bucket path sorts padded keys, key = row << xb | tx with row = tz * Ty +
+// ty and 2^xb the tile count along x rounded up to a power of two.  Tile id ->
+// padded key is increasing, so both give the same order.  The low lb >= xb
+// bits of a key hold whole rows, so every row of a Gaussian's box lies in one
+// bucket (top digit = key >> lb), and the emission order of a Gaussian's pairs
+// (its box z -> y -> x) is a sequence of rows of ex consecutive tiles.  The
+// split into buckets therefore works on rows: a row is one entry with one
+// digit and a weight of ex pairs, never a pair at a time.
+struct BucketGeom {
+    int Tx, Ty;  // tiles along x and y
+    int rows;    // Ty * Tz
+    int xb;      // bits of the padded x coordinate
+    int lb;      // low key bits sorted inside a bucket (xb <= lb <= 9)
+    int nbits;   // top digit bits: 2^nbits buckets
+};
+
+// One Gaussian's emitted slots [cum[g-1], cum[g]) below the capacity, as box
+// rows: the first nvalid slots are the box's tiles z -> y -> x (nvalid =
+// min(slots, box volume)); the remaining ninvalid slots (only when cum
+// disagrees with the box) carry no tile and sort last.
+struct GaussRows {
+    int mnx, mny, mnz, ex, ey;
+    int nvalid, ninvalid, nrows;
+};
+
+__device__ __forceinline__ GaussRows gauss_rows(int g, int n, int64_t cap,
+                                                const int *__restrict__ tile_min,
+                                                const int *__restrict__ tile_max,
+                                                const int *__restrict__ cum) {
+    GaussRows r{};
+    if (g >= n) return r;
+    const int64_t s0 = g > 0 ? cum[g - 1] : 0;
+    const int64_t s1 = min<int64_t>(cum[g], cap);
+    const int64_t ns = s1 > s0 ? s1 - s0 : 0;
+    r.mnx = tile_min[3 * g]; r.mny = tile_min[3 * g + 1]; r.mnz = tile_min[3 * g + 2];
+    r.ex = tile_max[3 * g] - r.mnx;
+    r.ey = tile_max[3 * g + 1] - r.mny;
+    const int ez = tile_max[3 * g + 2] - r.mnz;
+    const int64_t vol = (r.ex > 0 && r.ey > 0 && ez > 0) ? (int64_t)r.ex * r.ey * ez : 0;
+    const int64_t nv = min(ns, vol);
+    r.nvalid = (int)nv;
+    r.ninvalid = (int)(ns - nv);
+    r.nrows = nv > 0 ? (int)((nv + r.ex - 1) / r.ex) : 0;
+    return r;
+}
+
+// Padded key of the first tile of box row (dz, dy); unsigned arithmetic, so a
+// box outside the grid gives a wrong but in-range digit, never a fault.
+__device__ __forceinline__ unsigned row_key(const BucketGeom &G, int mnx, int mny, int mnz, int dz,
+                                            int dy) {
+    const unsigned row = (unsigned)(mnz + dz) * (unsigned)G.Ty + (unsigned)(mny + dy);
+    return (row << G.xb) | (unsigned)mnx;
+}
+
+constexpr int kSplitThreads = 256;  // Gaussians per chunk of the bucket split
+constexpr int kSplitWaves = kSplitThreads / kWave;
+constexpr int kPiece = 512;  // entries a split wave lists at a time
+
+// Adds the lane's Gaussian's pairs to h[top digit]: one atomic per run of
+// rows with one digit (a run of 2^(lb - xb) rows at most), plus the slots
+// past the box to the last digit.
+__device__ __forceinline__ void add_row_counts(const BucketGeom &G, const GaussRows &r, int nb,
+                                               int *h) {
+    int cur = 0, acc = 0, dz = 0, dy = 0;
+    for (int q = 0; q < r.nrows; ++q) {
+        const int d = (int)((row_key(G, r.mnx, r.mny, r.mnz, dz, dy) >> G.lb) & (unsigned)(nb - 1));
+        if (d != cur && acc) {
+            atomicAdd(&h[cur], acc);
+            acc = 0;
+        }
+        cur = d;
+        acc += min(r.ex, r.nvalid - q * r.ex);
+        if (++dy == r.ey) { dy = 0; ++dz; }
+    }
+    if (acc) atomicAdd(&h[cur], acc);
+    if (r.ninvalid) atomicAdd(&h[nb - 1], r.ninvalid);
+}
+
+// Pass 1: chunk c = the kSplitThreads Gaussians from kSplitThreads * c, one
+// lane each; the chunk's pair count per top digit, hist[d * hstride + c]
+// (digit-major, as k_digit_scan takes it).
+template <int Bt>
+__global__ __launch_bounds__(kSplitThreads) void k_bucket_hist(
+    int n, int64_t cap, const int *__restrict__ tile_min, const int *__restrict__ tile_max,
+    const int *__restrict__ cum, BucketGeom G, int *__restrict__ hist, int hstride) {
+    __shared__ int s_h[1 << Bt];
+    const int t = threadIdx.x, nb = 1 << G.nbits;
+    for (int d = t; d < nb; d += kSplitThreads) s_h[d] = 0;
+    __syncthreads();
+    const GaussRows r = gauss_rows(blockIdx.x * kSplitThreads + t, n, cap, tile_min, tile_max, cum);
+    add_row_counts(G, r, nb, s_h);
+    __syncthreads();
+    for (int d = t; d < nb; d += kSplitThreads) hist[(int64_t)d * hstride + blockIdx.x] = s_h[d];
+}
+
+// Pass 2: the stable split of chunk c.  Each wave counts its 64 Gaussians'
+// pairs per digit again, and one counter per (wave, digit) starts at the
+// digit's start, plus the chunk's prefix (k_digit_scan turned hist into the
+// prefix over chunks and wrote the digit totals), plus the earlier waves'
+// counts.  A wave lists its Gaussians' rows in emission order in LDS
+// (lane-major, kPiece at a time) and walks the list 64 rows a round: each row
+// takes its digit's counter plus the pairs of the lower lanes of the round
+// with the same digit (weights summed from bit-sliced ballots), the lowest
+// such lane advances the counter by the round's total, and each lane writes
+// its row's words, (gaussian << lb) | the key's low lb bits.  Slots past a box
+// get the all-ones key.
+template <int Bt>
+__global__ __launch_bounds__(kSplitThreads) void k_bucket_split(
+    int n, int64_t cap, const int *__restrict__ tile_min, const int *__restrict__ tile_max,
+    const int *__restrict__ cum, BucketGeom G, const int *__restrict__ hist, int hstride,
+    const int *__restrict__ totals, unsigned *__restrict__ words) {
+    __shared__ int s_cnt[kSplitWaves][1 << Bt];
+    __shared__ int2 s_list[kSplitWaves][kPiece];
+    __shared__ int s_info[kSplitWaves][7][kWave];
+    __shared__ int s_wtot[kSplitWaves];
+    const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
+    const int chunk = blockIdx.x, nb = 1 << G.nbits;
+    const unsigned lmask = (1u << G.lb) - 1u;
+    for (int d = t; d < nb; d += kSplitThreads)
+#pragma unroll
+        for (int w = 0; w < kSplitWaves; ++w) s_cnt[w][d] = 0;
+    __syncthreads();
+    const int g0 = chunk * kSplitThreads + wave * kWave;
+    const GaussRows r = gauss_rows(g0 + lane, n, cap, tile_min, tile_max, cum);
+    add_row_counts(G, r, nb, s_cnt[wave]);
+    __syncthreads();
+    {   // counter (w, d) = start of d + chunk prefix of d + counts of waves < w
+        int carry = 0;
+#pragma unroll
+        for (int j = 0; j < (1 << Bt) / kSplitThreads; ++j) {
+            const int d = j * kSplitThreads + t;
+            int tot;
+            const int dstart =
+                carry + block_scan_total<kSplitThreads>(d < nb ? totals[d] : 0, s_wtot, &tot);
+            carry += tot;
+            if (d < nb) {
+                unsigned run = (unsigned)dstart + (unsigned)hist[(int64_t)d * hstride + chunk];
+#pragma unroll
+                for (int w = 0; w < kSplitWaves; ++w) {
+                    const unsigned c = (unsigned)s_cnt[w][d];
+                    s_cnt[w][d] = (int)run;
+                    run += c;
+                }
+            }
+            __syncthreads();  // s_wtot is rewritten by the next round; counters final
+        }
+    }
+    int *cnt = s_cnt[wave];
+    int *info = &s_info[wave][0][0];
+    info[0 * kWave + lane] = r.mnx;
+    info[1 * kWave + lane] = r.mny;
+    info[2 * kWave + lane] = r.mnz;
+    info[3 * kWave + lane] = r.ex;
+    info[4 * kWave + lane] = r.ey;
+    info[5 * kWave + lane] = r.nvalid;
+    info[6 * kWave + lane] = r.ninvalid;
+    const int nent = r.nrows + (r.ninvalid > 0 ? 1 : 0);
+    int ent_inc = nent;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(ent_inc, o, kWave);
+        if (lane >= o) ent_inc += v;
+    }
+    const int base = ent_inc - nent;
+    const int E = __shfl(ent_inc, kWave - 1, kWave);
+    const uint64_t lt = lanemask_lt();
+    for (int p0 = 0; p0 < E; p0 += kPiece) {
+        {   // this lane's entries in [p0, p0 + kPiece): (lane | dy << 6, dz), or (lane, -1)
+            const int a = max(base, p0), b = min(base + nent, p0 + kPiece);
+            if (a < b) {
+                int q = a - base;
+                int dz = q < r.nrows ? q / r.ey : 0;
+                int dy = q < r.nrows ? q - dz * r.ey : 0;
+                for (int e = a; e < b; ++e, ++q) {
+                    if (q < r.nrows) {
+                        s_list[wave][e - p0] = make_int2(lane | (dy << 6), dz);
+                        if (++dy == r.ey) { dy = 0; ++dz; }
+                    } else {
+                        s_list[wave][e - p0] = make_int2(lane, -1);
+                    }
+                }
+            }
+        }
+        const int ne = min(kPiece, E - p0);
+        for (int r0 = 0; r0 < ne; r0 += kWave) {
+            const bool valid = r0 + lane < ne;
+            int d = nb - 1, len = 0, src = 0;
+            unsigned low = lmask, step = 0;
+            if (valid) {
+                const int2 en = s_list[wave][r0 + lane];
+                src = en.x & (kWave - 1);
+                if (en.y >= 0) {
+                    const int dy = en.x >> 6, dz = en.y;
+                    const int ex = info[3 * kWave + src];
+                    const int q = dz * info[4 * kWave + src] + dy;
+                    len = min(ex, info[5 * kWave + src] - q * ex);
+                    const unsigned key = row_key(G, info[src], info[kWave + src],
+                                                 info[2 * kWave + src], dz, dy);
+                    d = (int)((key >> G.lb) & (unsigned)(nb - 1));
+                    low = key & lmask;
+                    step = 1;
+                } else {
+                    len = info[6 * kWave + src];
+                }
+            }
+            // lanes of the round with the same digit
+            const uint64_t vm = __ballot(valid);
+            uint32_t plo = (uint32_t)vm, phi = (uint32_t)(vm >> 32);
+            for (int bit = 0; bit < G.nbits; ++bit) {
+                const uint32_t x = (uint32_t)__builtin_amdgcn_sbfe(d, bit, 1);
+                const uint64_t m = __ballot(x != 0u);
+                plo &= ~((uint32_t)m ^ x);
+                phi &= ~((uint32_t)(m >> 32) ^ x);
+            }
+            const uint64_t peers = ((uint64_t)phi << 32) | plo;
+            // their pairs below this lane (pre) and in all (tot), from as many
+            // weight bits as the round's longest row needs (3 for box rows of up
+            // to 7 tiles)
+            const int wbits = __ballot(len > 7) ? (__ballot(len > 31) ? 31 : 5) : 3;
+            int64_t pre = 0, tot = 0;
+            for (int bit = 0; bit < wbits; ++bit) {
+                const uint64_t m = __ballot((len >> bit) & 1) & peers;
+                pre += (int64_t)__popcll(m & lt) << bit;
+                tot += (int64_t)__popcll(m) << bit;
+            }
+            const unsigned off = (unsigned)cnt[d];  // the wave's own counter: LDS keeps read-then-write order
+            if (valid && __popcll(peers & lt) == 0) cnt[d] = (int)(off + (unsigned)tot);
+            const int64_t pos = (int64_t)(int)off + pre;
+            const unsigned gw = (unsigned)(g0 + src) << G.lb;
+            for (int k = 0; k < len; ++k) {
+                const int64_t i = pos + k;
+                if (i >= 0 && i < cap) words[i] = gw | ((low + step * (unsigned)k) & lmask);
+            }
+        }
+    }
+}
+
+// Second stage of the bucket path: every bucket of 2^lb consecutive padded
+// keys is one contiguous run of words (gaussian << lb | the key's low lb bits)
+// in emission order; block b sorts bucket b by its low bits in LDS and writes
+// the ids, the tiles (optional) and tile_bins of its tiles.
+//   1. wave w counts the words of its contiguous segment per key in its own
 //      row of LDS counters;
-//   2. one thread per tile turns the rows into per-(wave, tile) offsets and the
+//   2. one thread per key turns the rows into per-(wave, key) offsets and the
 //      tile's [start, end) (tiles without pairs get [0, 0), as the reference's
-//      zero-initialised tile_bins has them);
+//      zero-initialised tile_bins has them; padding keys name no tile);
 //   3. each wave walks its segment in order, 64 words a round: ballot-ranked
-//      among the round's lanes with the same tile, plus the wave's running
+//      among the round's lanes with the same key, plus the wave's running
 //      counter, which gives the stable position directly.
 // A wave loads up to kBatch rounds at once (all in flight), and keeps them in
 // registers from step 1 to step 3 when its segment is one batch (buckets of
 // up to 18,432 pairs).  Sorted words go to LDS when the bucket fits (then
 // copied out coalesced: unstaged, scattered 4-byte stores cost 22 us more at
 // 256^3 / 200k), else straight to global memory (an outsized bucket of a
-// clustered scene: slower, same result).  A slot with an invalid key
-// (cum inconsistent with the boxes) falls in the last bucket at the all-ones
-// low digit, as in the LSD path, and its tile reads 2^bits - 1.
+// clustered scene: slower, same result).  Words with the all-ones key (slots
+// past a box) sort last in the last bucket.
 constexpr int kBucketThreads = 1024;
 constexpr int kBucketWaves = kBucketThreads / kWave;
 constexpr int kBatch = 18;  // rounds of 64 words per wave and batch
-static_assert((1 << kRadixBitsMax) <= kBucketThreads, "one tile per thread in the offset step");
+static_assert((1 << kRadixBitsMax) <= kBucketThreads, "one key per thread in the offset step");
 
-// LB: the widest low digit served (8 with an 8-bit top digit, 9 with a 9-bit
-// one).  The staging area takes what the 160 KiB of LDS leave beside the
-// counters: 140 KiB (LB = 8) or 120 KiB (LB = 9), one workgroup per CU.
+// LB: the widest low digit served (8, or 9 for 18-bit keys).  The staging
+// area takes what the 160 KiB of LDS leave beside the counters: 140 KiB
+// (LB = 8) or 120 KiB (LB = 9), one workgroup per CU.
 template <int LB>
 constexpr int kStageWords = (LB <= 8 ? 140 : 120) * 1024 / 4;
+
+// The tile of padded key k, or kInvalidKey for a padding key.
+__device__ __forceinline__ int padded_tile(const BucketGeom &G, unsigned k) {
+    const unsigned row = k >> G.xb, tx = k & ((1u << G.xb) - 1u);
+    return (tx < (unsigned)G.Tx && row < (unsigned)G.rows) ? (int)(row * (unsigned)G.Tx + tx)
+                                                          : kInvalidKey;
+}
 
 template <int LB>
 __global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
     const unsigned *__restrict__ pin, int *__restrict__ kout, int *__restrict__ vout,
-    const int *__restrict__ totals, int lb, int64_t T, int2 *__restrict__ tile_bins) {
+    const int *__restrict__ totals, BucketGeom G, int64_t cap, int2 *__restrict__ tile_bins) {
     __shared__ int s_cnt[kBucketWaves << LB];
     __shared__ int s_wtot[kBucketWaves];
     __shared__ unsigned s_stage[kStageWords<LB>];
     const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
-    const int b = blockIdx.x, nb = 1 << lb;
+    const int b = blockIdx.x, lb = G.lb, nb = 1 << lb;
     const unsigned lmask = (unsigned)nb - 1u;
     int start;
     {
@@ -577,7 +823,8 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
         block_scan_total<kBucketThreads>(t < b ? totals[t] : 0, s_wtot, &tot);
         start = tot;
     }
-    const int size = totals[b];
+    // the words below the capacity (all of them unless the counts disagree with it)
+    const int size = start < cap ? (int)min<int64_t>(totals[b], cap - start) : 0;
     for (int i = t; i < kBucketWaves * nb; i += kBucketThreads) s_cnt[i] = 0;
     // segments of whole 64-word rounds, in bucket order; batches of kBatch rounds
     const int seg = (size + kBucketWaves * kWave - 1) / (kBucketWaves * kWave) * kWave;
@@ -601,6 +848,7 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
             if (s0 + (j * kBatch + q) * kWave + lane < s1) atomicAdd(&cnt[w[q] & lmask], 1);
     }
     __syncthreads();
+    const unsigned key0 = (unsigned)b << lb;
     {
         int run = 0;
         if (t < nb) {
@@ -616,14 +864,13 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
         if (t < nb) {
 #pragma unroll 4
             for (int v = 0; v < kBucketWaves; ++v) s_cnt[v * nb + t] += kstart;
-            const int64_t tile = (int64_t)b * nb + t;
-            if (tile < T)
+            const int tile = padded_tile(G, key0 | (unsigned)t);
+            if (tile != kInvalidKey)
                 tile_bins[tile] = run > 0 ? make_int2(start + kstart, start + kstart + run)
                                           : make_int2(0, 0);
         }
     }
     const bool staged = size <= kStageWords<LB>;
-    const int tile0 = b << lb;
     __syncthreads();
     const uint64_t lt = lanemask_lt();
     for (int j = 0; j < nbatch; ++j) {
@@ -652,7 +899,7 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
                     s_stage[pos] = w[q];
                 } else {
                     vout[start + pos] = (int)(w[q] >> lb);
-                    if (kout) kout[start + pos] = tile0 | d;
+                    if (kout) kout[start + pos] = padded_tile(G, key0 | (unsigned)d);
                 }
             }
         }
@@ -662,50 +909,76 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
         for (int i = t; i < size; i += kBucketThreads) {
             const unsigned x = s_stage[i];
             vout[start + i] = (int)(x >> lb);
-            if (kout) kout[start + i] = tile0 | (int)(x & lmask);
+            if (kout) kout[start + i] = padded_tile(G, key0 | (x & lmask));
         }
     }
 }
 
 struct BinLayout {
     size_t keys_a, vals_a, keys_b, hist, totals, total;
-    int bits, passes, nblocks, hstride;  // digit width; hist row stride, a multiple of 4
-    bool bucket;  // one scatter on the top digit + k_bucket_sort, instead of LSD passes
-    int lb;       // bucket path: low bits sorted inside a bucket
+    int bits, passes, nblocks, hstride;  // LSD digit width; hist row stride, a multiple of 4
+    bool bucket;     // the bucket path (box rows split by bucket + k_bucket_sort)
+    BucketGeom geom; // its padded-key geometry
+    int nchunks, bstride;  // its chunks of kSplitThreads Gaussians and their hist row stride
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-// The bucket path serves keys of up to 18 bits while the buckets stay small
-// enough for one workgroup each (mean below kBucketMeanMax pairs); heavier
-// scenes (e.g. 118M pairs on 2^15 tiles) keep the LSD passes, whose every
-// pass spreads over all CUs.  GSV_BINNING=lsd or =bucket overrides the
-// choice (bucket only where the key width allows it), so that tests can run
-// both paths on one scene; the workspace is the same either way.
+// The bucket path serves padded keys of up to 18 bits (at most 9 low bits per
+// bucket) while the buckets stay small enough for one workgroup each (mean
+// below kBucketMeanMax pairs); heavier scenes (e.g. 118M pairs on 2^15 tiles)
+// keep the LSD passes, whose every pass spreads over all CUs.  GSV_BINNING=lsd
+// or =bucket overrides the choice (bucket only where the key width allows it),
+// so that tests can run both paths on one scene; the workspace is the same
+// either way (its hist region fits both paths' histograms).  allow_bucket =
+// false leaves the bucket path out of the layout altogether.
 constexpr int64_t kBucketMeanMax = 24576;
 
-BinLayout bin_layout(int64_t cap, int64_t n_tiles, int64_t n) {
+BinLayout bin_layout(int64_t cap, int Tx, int Ty, int Tz, int64_t n, bool allow_bucket = true) {
     BinLayout L{};
+    const int64_t n_tiles = (int64_t)Tx * Ty * Tz;
     int bits = 0;
     while (bits < 31 && ((int64_t)1 << bits) < n_tiles) ++bits;
     L.bits = (bits == 17 || bits == 18) ? 9 : 8;
     L.passes = (bits + L.bits - 1) / L.bits;
-    L.lb = bits > L.bits ? bits - L.bits : 0;
-    // low digit of at most 9 bits, and gaussian ids that fit beside it in a word
-    const bool allow = bits <= 18 && n <= ((int64_t)1 << (32 - L.lb));
+    // padded keys: xb bits of x, rb bits of the Ty * Tz rows; the top digit
+    // takes at most rb bits, so that the low bits hold whole rows
+    int xb = 0, rb = 0;
+    while (xb < 31 && (1 << xb) < Tx) ++xb;
+    while (rb < 31 && ((int64_t)1 << rb) < (int64_t)Ty * Tz) ++rb;
+    const int pbits = xb + rb;
+    L.geom.Tx = Tx;
+    L.geom.Ty = Ty;
+    L.geom.rows = Ty * Tz;  // <= n_tiles, checked below 2^31 by the caller
+    L.geom.xb = xb;
+    L.geom.nbits = rb < (pbits >= 17 ? 9 : 8) ? rb : (pbits >= 17 ? 9 : 8);
+    L.geom.lb = pbits - L.geom.nbits;
+    // gaussian ids must fit beside the low bits in a word
+    const bool allow = allow_bucket && pbits <= 18 && L.geom.lb <= kRadixBitsMax &&
+                       n <= ((int64_t)1 << (32 - L.geom.lb));
     const char *force = getenv("GSV_BINNING");
     if (force && strcmp(force, "lsd") == 0) L.bucket = false;
     else if (force && strcmp(force, "bucket") == 0) L.bucket = allow;
-    else L.bucket = allow && cap <= ((int64_t)1 << L.bits) * kBucketMeanMax;
+    else L.bucket = allow && cap <= ((int64_t)1 << L.geom.nbits) * kBucketMeanMax;
     L.nblocks = (int)((cap + kChunk - 1) / kChunk);
     L.hstride = (imax64(L.nblocks, 1) + 3) / 4 * 4;
+    L.nchunks = (int)((n + kSplitThreads - 1) / kSplitThreads);
+    L.bstride = (imax64(L.nchunks, 1) + 3) / 4 * 4;
     const size_t arr = align256((size_t)cap * sizeof(int));
+    size_t hist_bytes = ((size_t)1 << L.bits) * L.hstride * sizeof(int);
+    size_t tot_bytes = ((size_t)1 << L.bits) * sizeof(int);
+    if (allow) {
+        const size_t bh = ((size_t)1 << L.geom.nbits) * L.bstride * sizeof(int);
+        hist_bytes = bh > hist_bytes ? bh : hist_bytes;
+        const size_t bt = ((size_t)1 << L.geom.nbits) * sizeof(int);
+        tot_bytes = bt > tot_bytes ? bt : tot_bytes;
+    }
     size_t off = 0;
     L.keys_a = off; off += arr;
     L.vals_a = off; off += arr;
     L.keys_b = off; off += arr;
-    L.hist = off; off += align256(((size_t)1 << L.bits) * L.hstride * sizeof(int));
-    L.totals = off; off += align256(((size_t)1 << L.bits) * sizeof(int));
+    L.hist = off; off += align256(hist_bytes);
+    L.totals = off; off += align256(tot_bytes);
     L.total = off;
     return L;
 }
@@ -740,7 +1013,7 @@ int emit_and_sort(const BinLayout &L, int32_t n, int64_t cap, const int64_t *d_c
         hipLaunchKernelGGL(k_radix_scatter<B>,
                            dim3((unsigned)(remap ? kXcds * xcd_per(L.nblocks) : L.nblocks)),
                            dim3(kSortThreads), 0, s, kin, vin, kout, vout, cap, d_count, shift,
-                           hist, totals, L.nblocks, L.hstride, remap, -1);
+                           hist, totals, L.nblocks, L.hstride, remap);
         if (int st = check_launch()) return st;
         kin = kout;
         vin = vout;
@@ -749,32 +1022,35 @@ int emit_and_sort(const BinLayout &L, int32_t n, int64_t cap, const int64_t *d_c
     return GSV_OK;
 }
 
-// The bucket path with a B-bit top digit: emission into (ka, ids_out), one
-// stable scatter on bits [lb, lb + B) into va as packed words, then
-// k_bucket_sort into (tiles_out, ids_out) and tile_bins.  Four launches.
-template <int B>
-int emit_and_bucket_sort(const BinLayout &L, int32_t n, int64_t cap, const int64_t *d_count,
-                         const int32_t *tile_min, const int32_t *tile_max, const int32_t *cum,
-                         int Tx, int Ty, int64_t T, int *ka, int *va, int *hist, int *totals,
-                         int32_t *ids_out, int32_t *tiles_out, int32_t *tile_bins,
+// The bucket path: box rows counted per chunk of Gaussians and top digit,
+// the prefix over chunks, the stable split of the rows into buckets of packed
+// words (in ka), then k_bucket_sort into (tiles_out, ids_out) and tile_bins.
+// Four launches; Bt sizes the top digit's LDS arrays (8 or 9 bits).
+template <int Bt>
+int rows_and_bucket_sort(const BinLayout &L, int32_t n, int64_t cap, const int32_t *tile_min,
+                         const int32_t *tile_max, const int32_t *cum, int *ka, int *hist,
+                         int *totals, int32_t *ids_out, int32_t *tiles_out, int32_t *tile_bins,
                          hipStream_t s) {
-    hipLaunchKernelGGL(k_emit_chunk<B>, dim3(L.nblocks), dim3(kEmitThreads), 0, s, n, cap,
-                       d_count, tile_min, tile_max, cum, Tx, Ty, T, ka, ids_out, hist, L.hstride,
-                       L.lb, static_cast<int2 *>(nullptr));
+    const unsigned blocks = (unsigned)L.nchunks;
+    unsigned *words = reinterpret_cast<unsigned *>(ka);
+    hipLaunchKernelGGL(k_bucket_hist<Bt>, dim3(blocks), dim3(kSplitThreads), 0, s, n, cap,
+                       tile_min, tile_max, cum, L.geom, hist, L.bstride);
     if (int st = check_launch()) return st;
-    hipLaunchKernelGGL(k_digit_scan, dim3(1u << B), dim3(kDigitScanThreads), 0, s, hist,
-                       L.nblocks, L.hstride, totals);
+    hipLaunchKernelGGL(k_digit_scan, dim3(1u << L.geom.nbits), dim3(kDigitScanThreads), 0, s,
+                       hist, L.nchunks, L.bstride, totals);
     if (int st = check_launch()) return st;
-    const int remap = L.nblocks > kRemapChunks ? 1 : 0;
-    hipLaunchKernelGGL(k_radix_scatter<B>,
-                       dim3((unsigned)(remap ? kXcds * xcd_per(L.nblocks) : L.nblocks)),
-                       dim3(kSortThreads), 0, s, ka, ids_out, static_cast<int *>(nullptr), va, cap,
-                       d_count, L.lb, hist, totals, L.nblocks, L.hstride, remap, L.lb);
+    hipLaunchKernelGGL(k_bucket_split<Bt>, dim3(blocks), dim3(kSplitThreads), 0, s, n, cap,
+                       tile_min, tile_max, cum, L.geom, hist, L.bstride, totals, words);
     if (int st = check_launch()) return st;
-    // every tile of [0, 2^bits) lies in one of the 2^B buckets
-    hipLaunchKernelGGL(k_bucket_sort<B>, dim3(1u << B), dim3(kBucketThreads), 0, s,
-                       reinterpret_cast<const unsigned *>(va), tiles_out, ids_out, totals, L.lb,
-                       T, reinterpret_cast<int2 *>(tile_bins));
+    // every padded key of [0, 2^(nbits + lb)) lies in one of the 2^nbits buckets
+    if (L.geom.lb <= 8)
+        hipLaunchKernelGGL(k_bucket_sort<8>, dim3(1u << L.geom.nbits), dim3(kBucketThreads), 0, s,
+                           words, tiles_out, ids_out, totals, L.geom, cap,
+                           reinterpret_cast<int2 *>(tile_bins));
+    else
+        hipLaunchKernelGGL(k_bucket_sort<9>, dim3(1u << L.geom.nbits), dim3(kBucketThreads), 0, s,
+                           words, tiles_out, ids_out, totals, L.geom, cap,
+                           reinterpret_cast<int2 *>(tile_bins));
     return check_launch();
 }
 
@@ -784,7 +1060,7 @@ int emit_and_bucket_sort(const BinLayout &L, int32_t n, int64_t cap, const int64
 int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *tile_min,
                  const int32_t *tile_max, const int32_t *cum, int32_t D, int32_t H, int32_t W,
                  void *workspace, size_t workspace_bytes, int32_t *ids_out, int32_t *tile_bins,
-                 int32_t *tiles_out, hipStream_t s) {
+                 int32_t *tiles_out, hipStream_t s, bool allow_bucket = true) {
     if (n < 0 || D <= 0 || H <= 0 || W <= 0 || !tile_bins) return GSV_ERR_INVALID_ARGUMENT;
     if (cap > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
@@ -794,7 +1070,7 @@ int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *
     if (!tile_min || !tile_max || !cum || !ids_out || !workspace) return GSV_ERR_INVALID_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(ids_out) & 15) != 0) return GSV_ERR_INVALID_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(tiles_out) & 15) != 0) return GSV_ERR_INVALID_ARGUMENT;
-    const BinLayout L = bin_layout(cap, T, n);
+    const BinLayout L = bin_layout(cap, Tx, Ty, Tz, n, allow_bucket);
     if (workspace_bytes < L.total + 256) return GSV_ERR_WORKSPACE_TOO_SMALL;
     char *ws = static_cast<char *>(workspace);
     ws += (256 - (reinterpret_cast<uintptr_t>(ws) & 255)) & 255;  // 16-byte vector access
@@ -802,13 +1078,12 @@ int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *
     int *va = reinterpret_cast<int *>(ws + L.vals_a);
     int *hist = reinterpret_cast<int *>(ws + L.hist);
     int *totals = reinterpret_cast<int *>(ws + L.totals);
-    if (L.bucket) {
-        return L.bits == 9 ? emit_and_bucket_sort<9>(L, n, cap, d_count, tile_min, tile_max, cum,
-                                                     Tx, Ty, T, ka, va, hist, totals, ids_out,
-                                                     tiles_out, tile_bins, s)
-                           : emit_and_bucket_sort<8>(L, n, cap, d_count, tile_min, tile_max, cum,
-                                                     Tx, Ty, T, ka, va, hist, totals, ids_out,
-                                                     tiles_out, tile_bins, s);
+    if (L.bucket) {  // works from cum and the capacity alone: no pair count needed
+        return L.geom.nbits == 9
+                   ? rows_and_bucket_sort<9>(L, n, cap, tile_min, tile_max, cum, ka, hist, totals,
+                                             ids_out, tiles_out, tile_bins, s)
+                   : rows_and_bucket_sort<8>(L, n, cap, tile_min, tile_max, cum, ka, hist, totals,
+                                             ids_out, tiles_out, tile_bins, s);
     }
     int *kb = tiles_out ? tiles_out : reinterpret_cast<int *>(ws + L.keys_b);
     int *vb = ids_out;
@@ -882,8 +1157,9 @@ extern "C" int gsv_bin_workspace_bytes(int32_t n, int64_t num_intersects, int32_
                                        int32_t W, size_t *bytes) {
     if (!bytes || n < 0 || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
     if (num_intersects > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
-    const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
-    const BinLayout L = bin_layout(num_intersects > 0 ? num_intersects : 0, T, n);
+    const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
+    if ((int64_t)Tx * Ty * Tz > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
+    const BinLayout L = bin_layout(num_intersects > 0 ? num_intersects : 0, Tx, Ty, Tz, n);
     *bytes = L.total + 256;
     return GSV_OK;
 }
@@ -918,13 +1194,17 @@ extern "C" int gsv_bin_and_sort_noalloc(int32_t n, int64_t num_intersects,
                                         int32_t *tile_bins, int32_t *tiles_sorted, void *stream) {
     if (num_intersects > kNoAllocMaxPairs) return GSV_ERR_SCRATCH_TOO_SMALL;
     if (n < 0 || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
-    const int64_t T = (int64_t)gsv_tiles_along(W) * gsv_tiles_along(H) * gsv_tiles_along(D);
-    if (T > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
-    if (bin_layout(num_intersects > 0 ? num_intersects : 0, T, n).total + 256 > kNoAllocScratchBytes)
+    const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
+    if ((int64_t)Tx * Ty * Tz > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
+    // the bucket path's histogram grows with the Gaussian count: where it would
+    // not fit the scratch array, the LSD passes (sized by the pair count) serve
+    const int64_t np = num_intersects > 0 ? num_intersects : 0;
+    bool bucket = bin_layout(np, Tx, Ty, Tz, n).total + 256 <= kNoAllocScratchBytes;
+    if (!bucket && bin_layout(np, Tx, Ty, Tz, n, false).total + 256 > kNoAllocScratchBytes)
         return GSV_ERR_SCRATCH_TOO_SMALL;
     void *ws = nullptr;
     if (int st = noalloc_scratch(&ws)) return st;
     return bin_and_sort(n, num_intersects, nullptr, tile_min, tile_max, cum_tiles_hit, D, H, W,
                         ws, kNoAllocScratchBytes, gaussian_ids_sorted, tile_bins, tiles_sorted,
-                        as_stream(stream));
+                        as_stream(stream), bucket);
 }
