@@ -628,12 +628,13 @@ __global__ __launch_bounds__(kSplitThreads) void k_bucket_hist(
     for (int d = t; d < nb; d += kSplitThreads) hist[(int64_t)d * hstride + blockIdx.x] = s_h[d];
 }
 
-// Pass 2: the stable split of chunk c.  Each wave counts its 64 Gaussians'
-// pairs per digit again, and one counter per (wave, digit) starts at the
-// digit's start, plus the chunk's prefix (k_digit_scan turned hist into the
-// prefix over chunks and wrote the digit totals), plus the earlier waves'
-// counts.  A wave lists its Gaussians' rows in emission order in LDS
-// (lane-major, kPiece at a time) and walks the list 64 rows a round: each row
+// Pass 2: the stable split of chunk c.  Each wave walks its 64 Gaussians'
+// rows once, counting their pairs per digit again and listing the rows in
+// emission order in LDS (lane-major, kPiece at a time; later pieces are listed
+// when reached).  One counter per (wave, digit) starts at the digit's start,
+// plus the chunk's prefix (k_digit_scan turned hist into the prefix over
+// chunks and wrote the digit totals), plus the earlier waves' counts.  The
+// wave then walks its list 64 rows a round: each row
 // takes its digit's counter plus the pairs of the lower lanes of the round
 // with the same digit (weights summed from bit-sliced ballots), the lowest
 // such lane advances the counter by the round's total, and each lane writes
@@ -651,35 +652,20 @@ __global__ __launch_bounds__(kSplitThreads) void k_bucket_split(
     const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
     const int chunk = blockIdx.x, nb = 1 << G.nbits;
     const unsigned lmask = (1u << G.lb) - 1u;
+    // the digit totals and this chunk's prefix, loaded ahead of the counting
+    constexpr int kPer = (1 << Bt) / kSplitThreads;
+    int tv[kPer], hv[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int d = j * kSplitThreads + t;
+        tv[j] = d < nb ? totals[d] : 0;
+        hv[j] = d < nb ? hist[(int64_t)d * hstride + chunk] : 0;
+    }
     for (int d = t; d < nb; d += kSplitThreads)
 #pragma unroll
         for (int w = 0; w < kSplitWaves; ++w) s_cnt[w][d] = 0;
-    __syncthreads();
     const int g0 = chunk * kSplitThreads + wave * kWave;
     const GaussRows r = gauss_rows(g0 + lane, n, cap, tile_min, tile_max, cum);
-    add_row_counts(G, r, nb, s_cnt[wave]);
-    __syncthreads();
-    {   // counter (w, d) = start of d + chunk prefix of d + counts of waves < w
-        int carry = 0;
-#pragma unroll
-        for (int j = 0; j < (1 << Bt) / kSplitThreads; ++j) {
-            const int d = j * kSplitThreads + t;
-            int tot;
-            const int dstart =
-                carry + block_scan_total<kSplitThreads>(d < nb ? totals[d] : 0, s_wtot, &tot);
-            carry += tot;
-            if (d < nb) {
-                unsigned run = (unsigned)dstart + (unsigned)hist[(int64_t)d * hstride + chunk];
-#pragma unroll
-                for (int w = 0; w < kSplitWaves; ++w) {
-                    const unsigned c = (unsigned)s_cnt[w][d];
-                    s_cnt[w][d] = (int)run;
-                    run += c;
-                }
-            }
-            __syncthreads();  // s_wtot is rewritten by the next round; counters final
-        }
-    }
     int *cnt = s_cnt[wave];
     int *info = &s_info[wave][0][0];
     info[0 * kWave + lane] = r.mnx;
@@ -698,9 +684,53 @@ __global__ __launch_bounds__(kSplitThreads) void k_bucket_split(
     }
     const int base = ent_inc - nent;
     const int E = __shfl(ent_inc, kWave - 1, kWave);
+    __syncthreads();  // counters zeroed
+    {   // one walk over the lane's rows: the wave's count per digit (one atomic
+        // per run of rows with one digit) and the first piece of the list,
+        // (lane | dy << 6, dz) per row and (lane, -1) for the slots past the box
+        int cur = 0, acc = 0, dz = 0, dy = 0;
+        for (int q = 0; q < r.nrows; ++q) {
+            const int d =
+                (int)((row_key(G, r.mnx, r.mny, r.mnz, dz, dy) >> G.lb) & (unsigned)(nb - 1));
+            if (d != cur && acc) {
+                atomicAdd(&cnt[cur], acc);
+                acc = 0;
+            }
+            cur = d;
+            acc += min(r.ex, r.nvalid - q * r.ex);
+            if (base + q < kPiece) s_list[wave][base + q] = make_int2(lane | (dy << 6), dz);
+            if (++dy == r.ey) { dy = 0; ++dz; }
+        }
+        if (acc) atomicAdd(&cnt[cur], acc);
+        if (r.ninvalid) {
+            atomicAdd(&cnt[nb - 1], r.ninvalid);
+            if (base + r.nrows < kPiece) s_list[wave][base + r.nrows] = make_int2(lane, -1);
+        }
+    }
+    __syncthreads();
+    {   // counter (w, d) = start of d + chunk prefix of d + counts of waves < w
+        int carry = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int d = j * kSplitThreads + t;
+            int tot;
+            const int dstart = carry + block_scan_total<kSplitThreads>(tv[j], s_wtot, &tot);
+            carry += tot;
+            if (d < nb) {
+                unsigned run = (unsigned)dstart + (unsigned)hv[j];
+#pragma unroll
+                for (int w = 0; w < kSplitWaves; ++w) {
+                    const unsigned c = (unsigned)s_cnt[w][d];
+                    s_cnt[w][d] = (int)run;
+                    run += c;
+                }
+            }
+            __syncthreads();  // s_wtot is rewritten by the next round; counters final
+        }
+    }
     const uint64_t lt = lanemask_lt();
     for (int p0 = 0; p0 < E; p0 += kPiece) {
-        {   // this lane's entries in [p0, p0 + kPiece): (lane | dy << 6, dz), or (lane, -1)
+        if (p0 > 0) {  // this lane's entries in [p0, p0 + kPiece), as above
             const int a = max(base, p0), b = min(base + nent, p0 + kPiece);
             if (a < b) {
                 int q = a - base;
@@ -751,20 +781,33 @@ __global__ __launch_bounds__(kSplitThreads) void k_bucket_split(
             // their pairs below this lane (pre) and in all (tot), from as many
             // weight bits as the round's longest row needs (3 for box rows of up
             // to 7 tiles)
-            const int wbits = __ballot(len > 7) ? (__ballot(len > 31) ? 31 : 5) : 3;
-            int64_t pre = 0, tot = 0;
-            for (int bit = 0; bit < wbits; ++bit) {
-                const uint64_t m = __ballot((len >> bit) & 1) & peers;
-                pre += (int64_t)__popcll(m & lt) << bit;
-                tot += (int64_t)__popcll(m) << bit;
+            unsigned pre = 0, tot = 0;  // sums below 2^31: the round's pairs are at most 64 * 2^30
+            if (!__ballot(len > 7)) {
+#pragma unroll
+                for (int bit = 0; bit < 3; ++bit) {
+                    const uint64_t m = __ballot((len >> bit) & 1) & peers;
+                    pre += (unsigned)__popcll(m & lt) << bit;
+                    tot += (unsigned)__popcll(m) << bit;
+                }
+            } else {
+                for (int bit = 0; bit < 31; ++bit) {
+                    const uint64_t m = __ballot((len >> bit) & 1) & peers;
+                    pre += (unsigned)__popcll(m & lt) << bit;
+                    tot += (unsigned)__popcll(m) << bit;
+                }
             }
             const unsigned off = (unsigned)cnt[d];  // the wave's own counter: LDS keeps read-then-write order
-            if (valid && __popcll(peers & lt) == 0) cnt[d] = (int)(off + (unsigned)tot);
-            const int64_t pos = (int64_t)(int)off + pre;
+            if (valid && __popcll(peers & lt) == 0) cnt[d] = (int)(off + tot);
+            const int64_t pos = (int64_t)(int)off + (int64_t)pre;
             const unsigned gw = (unsigned)(g0 + src) << G.lb;
-            for (int k = 0; k < len; ++k) {
-                const int64_t i = pos + k;
-                if (i >= 0 && i < cap) words[i] = gw | ((low + step * (unsigned)k) & lmask);
+            if (pos >= 0 && pos + len <= cap) {  // always, unless cum disagrees with the counts
+                unsigned *dst = words + pos;
+                for (int k = 0; k < len; ++k) dst[k] = gw | ((low + step * (unsigned)k) & lmask);
+            } else {
+                for (int k = 0; k < len; ++k) {
+                    const int64_t i = pos + k;
+                    if (i >= 0 && i < cap) words[i] = gw | ((low + step * (unsigned)k) & lmask);
+                }
             }
         }
     }
@@ -849,26 +892,35 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
     }
     __syncthreads();
     const unsigned key0 = (unsigned)b << lb;
-    {
-        int run = 0;
-        if (t < nb) {
-#pragma unroll 4
-            for (int v = 0; v < kBucketWaves; ++v) {
-                const int c = s_cnt[v * nb + t];
-                s_cnt[v * nb + t] = run;
-                run += c;
-            }
+    {   // counters -> positions: one exclusive scan over (key, wave) order, the
+        // 16 * 2^lb counters spread evenly over the block's threads
+        static_assert(kBucketWaves == 16, "(key, wave) index = key * 16 + wave");
+        const int ne = kBucketWaves * nb;
+        const int P = (ne + kBucketThreads - 1) / kBucketThreads;
+        const int i0 = t * P;
+        int loc = 0;
+        for (int k = 0; k < P; ++k) {
+            const int i = i0 + k;
+            if (i < ne) loc += s_cnt[(i & 15) * nb + (i >> 4)];
         }
         int tot;
-        const int kstart = block_scan_total<kBucketThreads>(run, s_wtot, &tot);
-        if (t < nb) {
-#pragma unroll 4
-            for (int v = 0; v < kBucketWaves; ++v) s_cnt[v * nb + t] += kstart;
-            const int tile = padded_tile(G, key0 | (unsigned)t);
-            if (tile != kInvalidKey)
-                tile_bins[tile] = run > 0 ? make_int2(start + kstart, start + kstart + run)
-                                          : make_int2(0, 0);
+        int run = block_scan_total<kBucketThreads>(loc, s_wtot, &tot);  // (its barrier orders the reads above before the writes below)
+        for (int k = 0; k < P; ++k) {
+            const int i = i0 + k;
+            if (i < ne) {
+                int &c = s_cnt[(i & 15) * nb + (i >> 4)];
+                const int v = c;
+                c = run;
+                run += v;
+            }
         }
+    }
+    __syncthreads();
+    if (t < nb) {  // key t's run: from its wave-0 position to the next key's
+        const int ks = s_cnt[t], ke = t + 1 < nb ? s_cnt[t + 1] : size;
+        const int tile = padded_tile(G, key0 | (unsigned)t);
+        if (tile != kInvalidKey)
+            tile_bins[tile] = ke > ks ? make_int2(start + ks, start + ke) : make_int2(0, 0);
     }
     const bool staged = size <= kStageWords<LB>;
     __syncthreads();
