@@ -50,6 +50,26 @@ __device__ __forceinline__ int64_t xcd_runs(int64_t b) {
 __host__ __device__ inline int64_t xcd_runs_grid(int64_t T) {
     return (T + kRunSpan - 1) / kRunSpan * kRunSpan;
 }
+// floor(x / d) for 0 <= x < 2^31 and 1 <= d < 2^31 as a multiply and a shift:
+// with 2^(s-1) < d <= 2^s and m = floor(2^(31+s) / d) + 1 (below 2^32), the
+// error m*d - 2^(31+s) lies in (0, d], so x * (m*d - 2^(31+s)) < 2^(31+s) and
+// (x * m) >> (31 + s) is exact (Granlund and Montgomery, "Division by invariant
+// integers using multiplication", 1994).
+struct FastDiv {
+    uint32_t m;
+    int s;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f;
+    f.s = 0;
+    while ((1u << f.s) < d) ++f.s;
+    f.m = (uint32_t)(((uint64_t)1 << (31 + f.s)) / d + 1);
+    return f;
+}
+__device__ __forceinline__ uint32_t fastdiv(uint32_t x, FastDiv f) {
+    return (uint32_t)(((uint64_t)x * f.m) >> (31 + f.s));
+}
+
 __host__ __device__ inline int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
 __host__ __device__ inline int64_t imax64(int64_t a, int64_t b) { return a > b ? a : b; }
 

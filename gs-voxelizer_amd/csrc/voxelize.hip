@@ -74,12 +74,12 @@ __device__ __forceinline__ Gate make_gate(float mean) {
         g.t2 = t2;
         g.shift = 0.5f * t2;
         g.half = -0.5f * t2;
-        g.scale = exp2f(g.shift);
+        g.scale = __builtin_amdgcn_exp2f(g.shift);  // shift >= -75 for a finite mean: a normal result
         g.live = t2 <= 0.f;  // mean < 1e-6: alpha <= 1 can never reach the threshold
         g.bounded = true;
         if (g.live && t2 >= -60.f) {
             g.off = -(t2 + kExpFlush);
-            g.fscale = exp2f(-g.off);  // of the rounded offset, so the two cancel
+            g.fscale = __builtin_amdgcn_exp2f(-g.off);  // of the rounded offset (66..126), so the two cancel
         }
     } else if (mean > 0.f || mean != mean) {
         // +inf or NaN mean: the reference's `alpha * mean < 1e-6` never holds,
@@ -167,6 +167,21 @@ __device__ __forceinline__ TileGeom tile_geom(int tile, int Tx, int Ty, int D, i
     const int tx = (int)((unsigned)tile - q * (unsigned)Tx);
     const int ty = (int)(q % (unsigned)Ty), tz = (int)(q / (unsigned)Ty);
     t.x0 = tx * GSV_TILE; t.y0 = ty * GSV_TILE; t.z0 = tz * GSV_TILE;
+    t.xlo = (float)t.x0 + 0.5f; t.xhi = (float)min(t.x0 + GSV_TILE - 1, W - 1) + 0.5f;
+    t.ylo = (float)t.y0 + 0.5f; t.yhi = (float)min(t.y0 + GSV_TILE - 1, H - 1) + 0.5f;
+    t.zlo = (float)t.z0 + 0.5f; t.zhi = (float)min(t.z0 + GSV_TILE - 1, D - 1) + 0.5f;
+    return t;
+}
+
+// The same from a per-lane tile id, with the two divisions as multiply-shifts.
+__device__ __forceinline__ TileGeom tile_geom(int tile, FastDiv fx, int Tx, FastDiv fy, int Ty,
+                                              int D, int H, int W) {
+    TileGeom t;
+    const unsigned q = fastdiv((unsigned)tile, fx);
+    const int tx = (int)((unsigned)tile - q * (unsigned)Tx);
+    const unsigned tz = fastdiv(q, fy);
+    const int ty = (int)(q - tz * (unsigned)Ty);
+    t.x0 = tx * GSV_TILE; t.y0 = ty * GSV_TILE; t.z0 = (int)tz * GSV_TILE;
     t.xlo = (float)t.x0 + 0.5f; t.xhi = (float)min(t.x0 + GSV_TILE - 1, W - 1) + 0.5f;
     t.ylo = (float)t.y0 + 0.5f; t.yhi = (float)min(t.y0 + GSV_TILE - 1, H - 1) + 0.5f;
     t.zlo = (float)t.z0 + 0.5f; t.zhi = (float)min(t.z0 + GSV_TILE - 1, D - 1) + 0.5f;
@@ -605,6 +620,7 @@ constexpr int64_t kVerySparsePairs = 24;
 
 struct BwdArgs {
     int D, H, W, Tx, Ty, n, n_isect;
+    FastDiv fx, fy;  // division by Tx and by Ty
     int64_t T;
     const int *ids, *pair_tiles;
     const float4 *pos_radii;
@@ -662,18 +678,24 @@ struct BwdLane {
 // (gaussian-major, tiles z->y->x), so each Gaussian's partials are contiguous
 // for the reduction pass.  -1 when g or the tile is out of range or the slot
 // lies outside [cum[g-1], cum[g]) or past the pair count.
-__device__ __forceinline__ int64_t emission_slot(int g, int tile, int n, int Tx, int Ty,
-                                                 const int *tile_min, const int *tile_max,
-                                                 const int *cum, int n_isect) {
-    if ((unsigned)g >= (unsigned)n || tile < 0) return -1;
-    const unsigned qt = (unsigned)tile / (unsigned)Tx;
-    const int tx = (int)((unsigned)tile - qt * (unsigned)Tx);
-    const int ty = (int)(qt % (unsigned)Ty), tz = (int)(qt / (unsigned)Ty);
+__device__ __forceinline__ int64_t emission_slot_at(int g, int tx, int ty, int tz, int n,
+                                                    const int *tile_min, const int *tile_max,
+                                                    const int *cum, int n_isect) {
+    if ((unsigned)g >= (unsigned)n) return -1;
     const int mnx = tile_min[3 * g], mny = tile_min[3 * g + 1], mnz = tile_min[3 * g + 2];
     const int nxb = tile_max[3 * g] - mnx, nyb = tile_max[3 * g + 1] - mny;
     const int64_t base = g == 0 ? 0 : cum[g - 1];
     const int64_t e = base + ((int64_t)(tz - mnz) * nyb + (ty - mny)) * nxb + (tx - mnx);
     return (e >= base && e < (int64_t)cum[g] && e < n_isect) ? e : -1;
+}
+
+__device__ __forceinline__ int64_t emission_slot(int g, int tile, const BwdArgs &a) {
+    if ((unsigned)g >= (unsigned)a.n || tile < 0) return -1;
+    const unsigned qt = fastdiv((unsigned)tile, a.fx);
+    const int tx = (int)((unsigned)tile - qt * (unsigned)a.Tx);
+    const unsigned tz = fastdiv(qt, a.fy);
+    const int ty = (int)(qt - tz * (unsigned)a.Ty);
+    return emission_slot_at(g, tx, ty, (int)tz, a.n, a.tile_min, a.tile_max, a.cum, a.n_isect);
 }
 
 // The forward's tile culling (pair_live: one byte per sorted pair) as the
@@ -820,7 +842,7 @@ __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
 #pragma unroll
     for (int c = 0; c < C; ++c) L.I[c] = 0.f;
     L.gt = make_gate(0.f);
-    L.tg = tile_geom(L.valid ? L.tile : 0, a.Tx, a.Ty, a.D, a.H, a.W);
+    L.tg = tile_geom(L.valid ? L.tile : 0, a.fx, a.Tx, a.fy, a.Ty, a.D, a.H, a.W);
     if (!L.valid) return;
     const int g = a.ids[L.p];
     L.g = g;
@@ -1044,8 +1066,9 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
     const int g = L.g;
     if (a.partial != nullptr) {
         // Deterministic path: this pair's partial goes to its emission slot
-        const int64_t e = emission_slot(g, L.tile, a.n, a.Tx, a.Ty, a.tile_min, a.tile_max, a.cum,
-                                        a.n_isect);
+        const int64_t e = emission_slot_at(g, L.tg.x0 / GSV_TILE, L.tg.y0 / GSV_TILE,
+                                           L.tg.z0 / GSV_TILE, a.n, a.tile_min, a.tile_max, a.cum,
+                                           a.n_isect);
         if (e >= 0) {
             float *dst = a.partial + e * (9 + C);
 #pragma unroll
@@ -1077,8 +1100,7 @@ __device__ __forceinline__ void bwd_zero_culled(const BwdArgs &a, int64_t wv, in
         const int p = a.order[a.n_isect - 1 - q];
         const int t = a.pair_tiles[p];
         if (t < 0 || t >= a.T) continue;
-        const int64_t e = emission_slot(a.ids[p], t, a.n, a.Tx, a.Ty, a.tile_min, a.tile_max,
-                                        a.cum, a.n_isect);
+        const int64_t e = emission_slot(a.ids[p], t, a);
         if (e < 0) continue;
         float *dst = a.partial + e * (9 + C);
 #pragma unroll
@@ -1376,6 +1398,8 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     const float numel = (float)((int64_t)D * H * W * channels);
     BwdArgs args;
     args.D = D; args.H = H; args.W = W; args.Tx = Tx; args.Ty = Ty; args.n = n; args.n_isect = ni;
+    args.fx = make_fastdiv((uint32_t)Tx);
+    args.fy = make_fastdiv((uint32_t)Ty);
     args.T = T;
     args.ids = gaussian_ids_sorted; args.pair_tiles = pair_tiles;
     args.pos_radii = reinterpret_cast<const float4 *>(pos3d_radii);
