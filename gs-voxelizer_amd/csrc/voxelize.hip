@@ -131,10 +131,10 @@ __device__ __forceinline__ bool may_touch(float mx, float my, float mz, float a,
     const float det = a * cfx - b * (b * f - c * e) + c * (b * e - c * d);
     if (!(a > 0.f && cfz > 0.f && det > 0.f)) return true;
     const float k2 = -2.0f * kLn2 * t2;
-    const float inv = 1.0f / det;
-    const float hx = sqrtf(k2 * cfx * inv) * 1.001f + 0.01f;
-    const float hy = sqrtf(k2 * cfy * inv) * 1.001f + 0.01f;
-    const float hz = sqrtf(k2 * cfz * inv) * 1.001f + 0.01f;
+    const float inv = __builtin_amdgcn_rcpf(det);
+    const float hx = __builtin_amdgcn_sqrtf(k2 * cfx * inv) * 1.001f + 0.01f;
+    const float hy = __builtin_amdgcn_sqrtf(k2 * cfy * inv) * 1.001f + 0.01f;
+    const float hz = __builtin_amdgcn_sqrtf(k2 * cfz * inv) * 1.001f + 0.01f;
     const bool miss = (mx + hx < xlo) || (mx - hx > xhi) || (my + hy < ylo) || (my - hy > yhi) ||
                       (mz + hz < zlo) || (mz - hz > zhi);
     if (miss) return false;
@@ -147,7 +147,7 @@ __device__ __forceinline__ bool may_touch(float mx, float my, float mz, float a,
     const double nz = (double)c * dx + (double)e * dy + (double)f * dz;
     const float m = (float)(dx * nx + dy * ny + dz * nz);
     const float r = (float)(fabs(nx) * ex + fabs(ny) * ey + fabs(nz) * ez);
-    const float K = sqrtf(k2) * 1.001f + 0.01f, sm = sqrtf(m);
+    const float K = __builtin_amdgcn_sqrtf(k2) * 1.001f + 0.01f, sm = __builtin_amdgcn_sqrtf(m);
     return !(sm * (sm - K) > r * 1.001f + 0.01f);  // NaN anywhere -> comparisons false -> keep
 }
 
