@@ -8,14 +8,14 @@
 // step is stable, the result is the reference's exact order: ascending tile,
 // then ascending gaussian id.  Two paths give the same bits:
 //
-// Bucket path (padded keys of up to 18 bits, up to ~24k pairs per bucket on
-// average: 256^3 / 200k, 512^3 up to ~12M pairs), four launches.  It sorts
+// Bucket path (padded keys of up to 18 bits, up to ~40k pairs of capacity per
+// bucket on average: 256^3 / 200k, 512^3 / 1M), four launches.  It sorts
 // padded keys (tile row << xb | tx, 2^xb >= Tx), which order the pairs as the
 // tile ids do, and whose low bits hold whole tile rows, so that each row of a
 // Gaussian's box falls in one bucket:
 //   k_bucket_hist    per chunk of 256 Gaussians, its pair count per top digit
-//                    (8 bits, or 9 for 17- and 18-bit keys), from the boxes'
-//                    rows (no pair is emitted);
+//                    (8 bits, 9 for 17-bit keys, 10 for 18-bit ones), from the
+//                    boxes' rows (no pair is emitted);
 //   k_digit_scan     one block per digit: exclusive prefix of the per-chunk
 //                    counts over chunks, plus the digit total;
 //   k_bucket_split   stable split of the chunk's box rows by top digit, each
@@ -978,13 +978,13 @@ size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 // The bucket path serves padded keys of up to 18 bits (at most 9 low bits per
 // bucket) while the buckets stay small enough for one workgroup each (mean
-// below kBucketMeanMax pairs); heavier scenes (e.g. 118M pairs on 2^15 tiles)
+// capacity below kBucketMeanMax pairs); heavier scenes (e.g. 118M pairs on 2^15 tiles)
 // keep the LSD passes, whose every pass spreads over all CUs.  GSV_BINNING=lsd
 // or =bucket overrides the choice (bucket only where the key width allows it),
 // so that tests can run both paths on one scene; the workspace is the same
 // either way (its hist region fits both paths' histograms).  allow_bucket =
 // false leaves the bucket path out of the layout altogether.
-constexpr int64_t kBucketMeanMax = 24576;
+constexpr int64_t kBucketMeanMax = 40000;  // ~1.1 x the 35,840 words a bucket sort stages
 
 BinLayout bin_layout(int64_t cap, int Tx, int Ty, int Tz, int64_t n, bool allow_bucket = true) {
     BinLayout L{};
@@ -1003,7 +1003,10 @@ BinLayout bin_layout(int64_t cap, int Tx, int Ty, int Tz, int64_t n, bool allow_
     L.geom.Ty = Ty;
     L.geom.rows = Ty * Tz;  // <= n_tiles, checked below 2^31 by the caller
     L.geom.xb = xb;
-    L.geom.nbits = rb < (pbits >= 17 ? 9 : 8) ? rb : (pbits >= 17 ? 9 : 8);
+    // top digit: 8 bits, 9 for 17-bit keys, 10 for 18-bit ones, so that a bucket
+    // holds at most 2^8 keys and its sort stages in the 140 KiB LDS variant
+    const int want = pbits >= 18 ? 10 : (pbits >= 17 ? 9 : 8);
+    L.geom.nbits = rb < want ? rb : want;
     L.geom.lb = pbits - L.geom.nbits;
     // gaussian ids must fit beside the low bits in a word
     const bool allow = allow_bucket && pbits <= 18 && L.geom.lb <= kRadixBitsMax &&
@@ -1131,6 +1134,9 @@ int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *
     int *hist = reinterpret_cast<int *>(ws + L.hist);
     int *totals = reinterpret_cast<int *>(ws + L.totals);
     if (L.bucket) {  // works from cum and the capacity alone: no pair count needed
+        if (L.geom.nbits == 10)
+            return rows_and_bucket_sort<10>(L, n, cap, tile_min, tile_max, cum, ka, hist, totals,
+                                            ids_out, tiles_out, tile_bins, s);
         return L.geom.nbits == 9
                    ? rows_and_bucket_sort<9>(L, n, cap, tile_min, tile_max, cum, ka, hist, totals,
                                              ids_out, tiles_out, tile_bins, s)
