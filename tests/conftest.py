@@ -29,8 +29,8 @@ def device():
 @pytest.fixture(params=["auto", "lsd", "bucket"])
 def binning_path(request, monkeypatch):
     """Binning through each of the library's two sort paths (GSV_BINNING: the
-    LSD passes, or one top-digit scatter plus per-bucket sorts) and through
-    its own choice; both must give the same bits."""
+    LSD passes, or the split of the boxes' rows into buckets plus per-bucket
+    sorts) and through its own choice; both must give the same bits."""
     if request.param == "auto":
         monkeypatch.delenv("GSV_BINNING", raising=False)
     else:

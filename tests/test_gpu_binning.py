@@ -41,6 +41,12 @@ def _bin_cases():
     yield "bits18", S.make_gaussians(small_config(3, 30000, vol=(512, 512, 512)), seed=10)
     yield "three_passes", S.make_gaussians(small_config(3, 30000, vol=(520, 520, 520)), seed=6)
     yield "clustered_heavy", S.make_gaussians(small_config(5, 40000), seed=7)
+    # extreme aspect ratios: 375 tiles along x (9 padded x bits, 8 buckets of
+    # 512 keys), 375 tile layers along z with 2 tiles per row, and 625 tiles
+    # along x (10 x bits: the bucket path steps aside for the LSD passes)
+    yield "wide_x", S.make_gaussians(small_config(3, 20000, vol=(16, 24, 3000)), seed=12)
+    yield "tall_z", S.make_gaussians(small_config(3, 20000, vol=(3000, 24, 16)), seed=13)
+    yield "wider_x", S.make_gaussians(small_config(3, 8000, vol=(8, 8, 5000)), seed=14)
 
 
 @pytest.mark.parametrize("name,work", list(_bin_cases()), ids=lambda v: v if isinstance(v, str) else "")
