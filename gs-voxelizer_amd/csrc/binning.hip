@@ -25,7 +25,12 @@
 //   k_bucket_sort    one 1024-thread block per bucket sorts it by the low bits
 //                    in LDS and writes ids, tiles and tile_bins.
 // These read cum and the boxes, never the pair count: slots at or above the
-// capacity are left out.
+// capacity are left out.  Emission slots past a Gaussian's box (a cum that
+// disagrees with the boxes; the reference writes past its arrays then) get the
+// all-ones key on both paths and sort after the valid pairs; the LSD path
+// leaves them out of tile_bins, and so does the bucket path unless the
+// all-ones padded key is a real tile (Tx, Ty * Tz powers of two), whose range
+// then takes them in at its end or among its pairs.
 // LSD path (wider keys, heavier buckets), 7 launches for two passes:
 //   k_emit_chunk     block b writes emission slots [4096 b, 4096 b + 4096) and
 //                    that chunk's histogram of the lowest digit; it also
