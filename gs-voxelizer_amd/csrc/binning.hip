@@ -26,11 +26,10 @@
 //                    in LDS and writes ids, tiles and tile_bins.
 // These read cum and the boxes, never the pair count: slots at or above the
 // capacity are left out.  Emission slots past a Gaussian's box (a cum that
-// disagrees with the boxes; the reference writes past its arrays then) get the
-// all-ones key on both paths and sort after the valid pairs; the LSD path
-// leaves them out of tile_bins, and so does the bucket path unless the
-// all-ones padded key is a real tile (Tx, Ty * Tz powers of two), whose range
-// then takes them in at its end or among its pairs.
+// disagrees with the boxes, which the reference does not guard against either)
+// carry the all-ones key and no tile on both paths; the sorts order only the
+// significant key bits, so where those name a real tile (all key bits in use)
+// such slots fall among or after that tile's pairs.
 // LSD path (wider keys, heavier buckets), 7 launches for two passes:
 //   k_emit_chunk     block b writes emission slots [4096 b, 4096 b + 4096) and
 //                    that chunk's histogram of the lowest digit; it also
