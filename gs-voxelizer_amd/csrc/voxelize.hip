@@ -22,6 +22,16 @@
 //    Gaussians outside that domain (indefinite or non-finite conic, mean
 //    beyond 2^60 * 1e-6, intensities far above the mean) take the exact
 //    |s| <= h path.
+//  * This file is compiled in binary32 flush-to-zero mode
+//    (-fgpu-flush-denormals-to-zero): v_mul_f32 then also returns 0 below
+//    2^-126, so the forward can form most of a row's exp2 values as products
+//    with the same gate: two or three v_exp_f32 per 8-voxel row instead of
+//    eight.  A v_exp_f32 occupies the SIMD four times as long as an FMA (16
+//    against 4 cycles per wave64, measured), so the eight-exp row spent more
+//    time in them than in its 28 other instructions.  Elsewhere the kernels
+//    keep every binary32 value they rely on in
+//    the normal range (the backward's power-of-two staging of vol_grad), so
+//    the mode changes no result beyond denormal magnitudes.
 //  * Along a voxel row (fixed y, z) the quadratic form is
 //    s(dx) = R0 + dx*(R1 + A2*dx): two FMAs per voxel once R0, R1 are set up.
 //  * Forward: one 64-lane wave per tile, lane = one x-row of 8 voxels.  Per
@@ -195,7 +205,20 @@ __device__ __forceinline__ TileGeom tile_geom(int tile, FastDiv fx, int Tx, Fast
 // and the target.  An unordered difference (a NaN volume or target element)
 // stores 0: torch's sign of NaN is 0, so its l1_loss backward passes
 // grad * 0 there (NaN only when grad itself is not finite, as here).
-__device__ __forceinline__ int8_t l1_sign(float d) { return d > 0.f ? 1 : (d < 0.f ? -1 : 0); }
+// The sign is that of v - t in IEEE arithmetic with denormals (torch's), decided
+// on the bit patterns: this file runs in binary32 flush-to-zero mode, where a
+// denormal operand would read as 0.  For non-NaN v, t, IEEE v - t is positive
+// iff v > t (a difference of distinct floats is never rounded to 0 with
+// gradual underflow), and inf - inf is NaN, sign 0, as for equal keys.
+__device__ __forceinline__ int order_key(float x) {  // monotone in x; -0 and +0 alike
+    const int b = __float_as_int(x);
+    return b >= 0 ? b : -(b & 0x7fffffff);
+}
+__device__ __forceinline__ int8_t l1_sign(float v, float t) {
+    if (v != v || t != t) return 0;
+    const int kv = order_key(v), kt = order_key(t);
+    return kv > kt ? 1 : (kv < kt ? -1 : 0);
+}
 
 // float4 slots of one prepared Gaussian record: 13 + C floats (gate-free
 // layout) or 12 + C (exact layout).
@@ -233,7 +256,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
 
     for (int b0 = range.x; b0 < range.y; b0 += kWave) {
         const int idx = b0 + lane;
-        bool live = false, fast = false;
+        bool live = false, fast = false, chain = false, one_way = false;
         if (idx < range.y) {
             const int g = ids[idx];
             if ((unsigned)g < (unsigned)n) {
@@ -276,16 +299,40 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                         const double a2 = A2, bb = q1.x, cc = q1.y, dd = q1.z, ee = q1.w, ff = F;
                         rec[0] = (float)(2.0 * a2 * X + bb * Y + cc * Z);
                         rec[1] = -q1.x; rec[2] = -q1.y;
-                        rec[3] = (float)(X * (a2 * X + bb * Y + cc * Z) + Y * (dd * Y + ee * Z) +
-                                         ff * Z * Z);
+                        const double t0 = X * (a2 * X + bb * Y + cc * Z) + Y * (dd * Y + ee * Z) +
+                                          ff * Z * Z;
                         rec[4] = (float)(-(bb * X + 2.0 * dd * Y + ee * Z));
                         rec[5] = (float)(-(cc * X + ee * Y + 2.0 * ff * Z));
                         rec[6] = q1.z; rec[7] = q1.w;
                         rec[8] = F;
+                        // Chained rows (the first two loops below) split s(u) into
+                        //   E(uc) = T0 + off + K - T1 uc   and   G(uc) = A2 uc^2 - K
+                        // and form 2^E by products: from uc = -3.5 to +3.5 (one-way
+                        // chain, span 7) or from uc = +0.5 outwards both ways (its
+                        // first step left gives uc = -0.5; span 4).  With
+                        // M >= |T1| on every row of the tile and an integer
+                        // K >= span * M + 2, K + 12.25 |A2| <= 120:
+                        //  - every 2^G is a normal number (G >= -120);
+                        //  - 2^E <= 2^(-66 + 12.25 |A2| + K) < 2^54 (s <= off <= -66):
+                        //    no overflow on any row, live or not;
+                        //  - at a voxel with s >= -126, E >= -126 + K, and E is linear
+                        //    in uc, so every product of the chain up to it is at
+                        //    least 2^(-126 + K - span * M) > 2^-126: no factor is
+                        //    flushed early, and a product flushes only where s < -126.
+                        const float bound_t1 =
+                            (fabsf(rec[0]) + 3.5f * (fabsf(rec[1]) + fabsf(rec[2]))) * 1.001f;
+                        const float span_g = 12.25f * fabsf(A2);
+                        const float K7 = ceilf(7.0f * bound_t1) + 2.0f;
+                        const float K4 = ceilf(4.0f * bound_t1) + 2.0f;
+                        one_way = K7 + span_g <= 120.0f;
+                        chain = one_way || K4 + span_g <= 120.0f;
+                        const float K = one_way ? K7 : K4;
+                        rec[3] = (float)(chain ? t0 + (double)gt.off + (double)K : t0);
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const float uc = 0.5f + (float)k;
-                            rec[9 + k] = fmaf(A2, uc * uc, gt.off);
+                            rec[9 + k] = chain ? __builtin_amdgcn_exp2f(fmaf(A2, uc * uc, -K))
+                                               : fmaf(A2, uc * uc, gt.off);
                         }
 #pragma unroll
                         for (int c = 0; c < C; ++c) rec[13 + c] = I[c] * gt.fscale;
@@ -306,11 +353,75 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
             if (pair_live != nullptr) pair_live[idx] = live ? 1 : 0;
         }
         const uint64_t live_mask = __ballot(live);
-        uint64_t fmask = __ballot(fast);  // fast implies live
-        uint64_t smask = live_mask & ~fmask;
+        const uint64_t fast_mask = __ballot(fast);    // fast implies live
+        const uint64_t chain_mask = __ballot(chain);  // chain implies fast
+        uint64_t omask = __ballot(one_way);           // one_way implies chain
+        uint64_t cmask = chain_mask & ~omask;
+        uint64_t fmask = fast_mask & ~chain_mask;
+        uint64_t smask = live_mask & ~fast_mask;
         __syncthreads();
-        // Gate-free Gaussians first, then the exact-gate ones of the batch: two
-        // single-path loops keep the accumulators in place (no copies per trip).
+        // One-way and centre-out chained Gaussians, then the other gate-free
+        // ones, then the exact-gate ones of the batch: single-path loops keep the
+        // accumulators in place (no copies per trip).
+        while (omask) {
+            const int j = __builtin_ctzll(omask);
+            omask &= omask - 1;
+            const float4 r0 = s_rec[j][0], r1 = s_rec[j][1], r2 = s_rec[j][2], r3 = s_rec[j][3];
+            float iw[4];  // entries >= C are unused
+            iw[0] = r3.y;
+            if (C > 1) iw[1] = r3.z;
+            if (C > 2) iw[2] = r3.w;
+            if (C > 3) iw[3] = s_rec[j][kRecF4<C> - 1].x;
+            const float T1 = fmaf(r0.y, py, fmaf(r0.z, pz, r0.x));
+            const float T0 =
+                fmaf(r2.x, pz2, fmaf(r1.w, pyz, fmaf(r1.z, py2, fmaf(r1.y, pz, fmaf(r1.x, py, r0.w)))));
+            const float G[4] = {r2.y, r2.z, r2.w, r3.x};  // 2^(A2 uc^2 - K), |uc| = 0.5 .. 3.5
+            // two v_exp_f32 per row: 2^E at uc = -3.5 and the step 2^-T1 towards
+            // +x; every product below 2^-126 is 0 (binary32 flush-to-zero mode),
+            // which is the gate, as v_exp_f32's own flush is on the other paths
+            const float step = __builtin_amdgcn_exp2f(-T1);
+            float e = __builtin_amdgcn_exp2f(fmaf(3.5f, T1, T0));
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u) {
+                const float a = e * G[u < 4 ? 3 - u : u - 4];
+#pragma unroll
+                for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
+                if (u + 1 < GSV_TILE) e *= step;
+            }
+        }
+        while (cmask) {
+            const int j = __builtin_ctzll(cmask);
+            cmask &= cmask - 1;
+            const float4 r0 = s_rec[j][0], r1 = s_rec[j][1], r2 = s_rec[j][2], r3 = s_rec[j][3];
+            float iw[4];  // entries >= C are unused
+            iw[0] = r3.y;
+            if (C > 1) iw[1] = r3.z;
+            if (C > 2) iw[2] = r3.w;
+            if (C > 3) iw[3] = s_rec[j][kRecF4<C> - 1].x;
+            const float T1 = fmaf(r0.y, py, fmaf(r0.z, pz, r0.x));
+            const float T0 =
+                fmaf(r2.x, pz2, fmaf(r1.w, pyz, fmaf(r1.z, py2, fmaf(r1.y, pz, fmaf(r1.x, py, r0.w)))));
+            const float G[4] = {r2.y, r2.z, r2.w, r3.x};  // 2^(A2 uc^2 - K), |uc| = 0.5 .. 3.5
+            // three v_exp_f32 per row: 2^E at uc = +0.5 and the steps 2^-T1
+            // (towards +x) and 2^T1 (towards -x); uc = -0.5 is the first step
+            // left of it, so the chain spans 4 units of uc on the left
+            const float step_r = __builtin_amdgcn_exp2f(-T1), step_l = __builtin_amdgcn_exp2f(T1);
+            float er = __builtin_amdgcn_exp2f(fmaf(-0.5f, T1, T0));
+            float el = er * step_l;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float ar = er * G[k], al = el * G[k];
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    acc[4 + k][c] = fmaf(ar, iw[c], acc[4 + k][c]);
+                    acc[3 - k][c] = fmaf(al, iw[c], acc[3 - k][c]);
+                }
+                if (k < 3) {
+                    er *= step_r;
+                    el *= step_l;
+                }
+            }
+        }
         while (fmask) {
             const int j = __builtin_ctzll(fmask);
             fmask &= fmask - 1;
@@ -393,7 +504,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                     for (int b = 0; b < 4; ++b) {
                         const float d = v[4 * q + b] - tq[b];
                         lsum += fabsf(d);
-                        const int8_t sb = l1_sign(d);
+                        const int8_t sb = l1_sign(v[4 * q + b], tq[b]);
                         wd |= (uint32_t)(uint8_t)sb << (8 * b);
                     }
                     words[q] = wd;
@@ -418,7 +529,7 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                         for (int c = 0; c < C; ++c) {
                             const float d = acc[u][c] - tt[u * C + c];
                             lsum += fabsf(d);
-                            sg[u * C + c] = l1_sign(d);
+                            sg[u * C + c] = l1_sign(acc[u][c], tt[u * C + c]);
                         }
             }
         }
