@@ -49,6 +49,8 @@
 //    centre of a tile contributes exactly nothing there in the reference; such
 //    (tile, Gaussian) pairs are skipped with a conservative axis-aligned test.
 #include <float.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include "gsv_device.h"
 #include "gsv_scan.h"
@@ -331,7 +333,8 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const float uc = 0.5f + (float)k;
-                            rec[9 + k] = chain ? __builtin_amdgcn_exp2f(fmaf(A2, uc * uc, -K))
+                            // 2^-K applied exactly: the exp2 argument stays small
+                            rec[9 + k] = chain ? ldexpf(__builtin_amdgcn_exp2f(A2 * (uc * uc)), -(int)K)
                                                : fmaf(A2, uc * uc, gt.off);
                         }
 #pragma unroll
@@ -607,31 +610,45 @@ struct Moments {
 //              the voxels u and 7 - u share S0 + P_k (at C = 2 the four P_k
 //              cost a wave per SIMD, 5 -> 4, and still gain ~6 %; at C >= 3
 //              the staged tiles' LDS limits occupancy first);
+//   kChain (gate-free too): a row's a from three v_exp_f32 instead of eight,
+//              as products, which the binary32 flush-to-zero mode gates like
+//              v_exp_f32: E = S0 + bound + K - p' S1 from 2^E at p' = -3.5 and
+//              p' = +0.5, each stepped three times by 2^-S1, times the lane's
+//              2^(A2 p'^2 - K).  K (chain_shift) keeps every product of a chain
+//              up to a passing voxel above 2^-126 and every factor finite;
 //   otherwise: a = exp2(s) if |s| <= bound, s = sigma2 - shift.
-template <int C, bool kGateFree>
+template <int C, bool kGateFree, bool kChain = false>
 __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int nz,
                                              float mxl, float myl, float mzl, float A2, float Bn,
                                              float Cn, float Dn, float En, float Fn, float shift,
-                                             float bound, const float (&I)[C], Moments<C> &M) {
+                                             float bound, float K, const float (&I)[C],
+                                             Moments<C> &M) {
+    static_assert(kGateFree || !kChain, "the chained rows are gate-free");
     float dxu[GSV_TILE], dxu2[GSV_TILE];
 #pragma unroll
     for (int u = 0; u < GSV_TILE; ++u) {
         dxu[u] = mxl - ((float)u - 3.5f);
         dxu2[u] = dxu[u] * dxu[u];
     }
-    constexpr bool kSym = kGateFree;
-    float P[4];
+    constexpr bool kSym = kGateFree && !kChain;
+    float P[4];  // kSym: A2 p'^2 + bound;  kChain: 2^(A2 p'^2 - K), both at |p'| = k + 1/2
     const float A2m = A2 * mxl, Bm = Bn * mxl, Cm = Cn * mxl;
     if (kSym) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) P[k] = fmaf(A2, (0.5f + k) * (0.5f + k), bound);
     }
+    if (kChain) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)  // 2^-K applied exactly: the exp2 argument stays small
+            P[k] = ldexpf(__builtin_amdgcn_exp2f(A2 * ((0.5f + k) * (0.5f + k))), -(int)K);
+    }
+    const float K0base = kChain ? fmaf(A2m, mxl, bound + K) : A2m * mxl;
     for (int lz = 0; lz < nz; ++lz) {
         const float dz = mzl - ((float)lz - 3.5f);
         const float Cdz = Cn * dz, Edz = En * dz;
         // gate-free: S1 = Bn dy + K1, S0 = dy (Dn dy + L1) + K0
         const float K1 = fmaf(2.0f, A2m, Cdz), L1 = Bm + Edz;
-        const float K0 = fmaf(dz, fmaf(Fn, dz, Cm), A2m * mxl);
+        const float K0 = fmaf(dz, fmaf(Fn, dz, Cm), K0base);
         const float R0z = kGateFree ? (Fn * dz) * dz : fmaf(Fn * dz, dz, -shift);
         float Q0 = 0.f, Qx = 0.f, Qxx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
 #pragma unroll
@@ -645,9 +662,24 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                 gv[4 * q] = t4.x; gv[4 * q + 1] = t4.y; gv[4 * q + 2] = t4.z; gv[4 * q + 3] = t4.w;
             }
             const float dy = myl - ((float)ly - 3.5f);
-            float sv[GSV_TILE];  // kSym: the row's exponents
+            float sv[GSV_TILE];  // kSym: the row's exponents; kChain: its a
             float R1 = 0.f, R0 = 0.f;
-            if (kSym) {
+            if (kChain) {
+                const float S1 = fmaf(Bn, dy, K1);
+                const float S0 = fmaf(dy, fmaf(Dn, dy, L1), K0);  // + bound + K
+                const float step = __builtin_amdgcn_exp2f(-S1);
+                float e1 = __builtin_amdgcn_exp2f(fmaf(3.5f, S1, S0));   // p' = -3.5
+                float e2 = __builtin_amdgcn_exp2f(fmaf(-0.5f, S1, S0));  // p' = +0.5
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    sv[k] = e1 * P[3 - k];
+                    sv[4 + k] = e2 * P[k];
+                    if (k < 3) {
+                        e1 *= step;
+                        e2 *= step;
+                    }
+                }
+            } else if (kSym) {
                 const float S1 = fmaf(Bn, dy, K1);
                 const float S0 = fmaf(dy, fmaf(Dn, dy, L1), K0);
 #pragma unroll
@@ -664,12 +696,16 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
             float W0 = 0.f, W1 = 0.f, W2 = 0.f;
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
-                const float s = kSym ? sv[u] : fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
                 float a;
-                if (kGateFree)
-                    a = __builtin_amdgcn_exp2f(s);
-                else
-                    a = (fabsf(s) <= bound) ? __builtin_amdgcn_exp2f(s) : 0.f;
+                if (kChain) {
+                    a = sv[u];
+                } else {
+                    const float s = kSym ? sv[u] : fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
+                    if (kGateFree)
+                        a = __builtin_amdgcn_exp2f(s);
+                    else
+                        a = (fabsf(s) <= bound) ? __builtin_amdgcn_exp2f(s) : 0.f;
+                }
                 float h;
                 if (C == 1) {
                     h = a * gv[u];
@@ -732,6 +768,11 @@ constexpr int64_t kVerySparsePairs = 24;
 struct BwdArgs {
     int D, H, W, Tx, Ty, n, n_isect;
     FastDiv fx, fy;  // division by Tx and by Ty
+    // Chained rows allowed (GSV_BWD_CHAIN=0 turns them off).  A group takes them
+    // when every one of its pairs qualifies, so a pair's rounding can depend on
+    // the pairs it shares a wave with (as for exact-gate pairs, which take the
+    // whole group to the exact path); without them it never does.
+    int chain;
     int64_t T;
     const int *ids, *pair_tiles;
     const float4 *pos_radii;
@@ -987,6 +1028,38 @@ __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
     }
 }
 
+// Shift K of the chained row evaluation of one pair (pair_moments, kChain), or
+// -1 when the pair's rows are too steep for it: K = ceil(3M) + 2 with M >= |S1|
+// on every row that can hold a passing voxel, and K + 12.25 |A2| <= 120 (so
+// 2^(A2 p'^2 - K) >= 2^-120, and 2^E <= 2^(-66 + 12.25 |A2| + K) < 2^54 since
+// sigma2 + off <= off <= -66).  S1 = 2 A2 mx + Bn dy + Cn dz is linear in the
+// row's offsets (dy, dz) from the centre: over the tile's rows it stays within
+// 3.5 (|Bn| + |Cn|) of its value at the tile's centre row; rows outside the
+// projection onto (y, z) of the gate ellipsoid d^T Q d <= k2 hold no passing
+// voxel, and over that ellipse Bn dy + Cn dz stays within sqrt(k2 g^T S g),
+// g = (Bn, Cn), S the (y, z) block of Q^-1.  Also, on a row whose gate interval
+// (half-width <= sqrt(k2 / Q_xx)) meets the voxel centres |p'| <= 3.5, the
+// form's peak lies within 3.5 + sqrt(k2 / Q_xx) of the row centre, where the
+// slope is 2 |A2| times that distance.  Along a chain (three steps of p'), E
+// then falls by at most 3M before a passing voxel, where E >= -126 + K: no
+// product flushes early.
+template <int C>
+__device__ __forceinline__ float chain_shift(const BwdLane<C> &L, float A2, float Bn, float Cn) {
+    const float m_tile = fabsf(fmaf(2.0f * A2, L.mxl, fmaf(Bn, L.myl, Cn * L.mzl))) +
+                         3.5f * (fabsf(Bn) + fabsf(Cn));
+    const double a = L.ca, b = L.cb, c = L.cc, d = L.cd, e = L.ce, f = L.cf;
+    const double syy = a * f - c * c, szz = a * d - b * b, syz = b * c - a * e;
+    const double det = a * (d * f - e * e) - b * (b * f - c * e) + c * (b * e - c * d);
+    const double gb = Bn, gc = Cn;
+    const double q = (gb * gb * syy + 2.0 * gb * gc * syz + gc * gc * szz) / det;
+    const double k2 = -2.0 * (double)kLn2 * (double)L.gt.t2;
+    const float m_ell = (float)(fabs(2.0 * (double)A2 * (double)L.mxl) + sqrt(fmax(k2 * q, 0.0)));
+    const float m_reach = (float)(fabs(2.0 * (double)A2) * (3.5 + sqrt(fmax(k2 / a, 0.0))));
+    const float M = fminf(m_tile, fminf(m_ell, m_reach)) * 1.001f + 0.01f;
+    const float K = ceilf(3.0f * M) + 2.0f;
+    return K + 12.25f * fabsf(A2) <= 120.0f ? K : -1.0f;
+}
+
 // Exponent e such that m * 2^e lies in [2^(kGradScaleExp-1), 2^kGradScaleExp);
 // 0 for m = 0, infinite or NaN.
 __device__ __forceinline__ int grad_scale_exp(float m) {
@@ -1144,12 +1217,19 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
         const float Cn = in_grp ? -kLog2e * L.cc : 0.f, Dn = in_grp ? -0.5f * kLog2e * L.cd : 0.f;
         const float En = in_grp ? -kLog2e * L.ce : 0.f, Fn = in_grp ? -0.5f * kLog2e * L.cf : 0.f;
         const float gx = in_grp ? L.mxl : 0.f, gy = in_grp ? L.myl : 0.f, gz = in_grp ? L.mzl : 0.f;
-        if (wave_fast)
-            pair_moments<C, true>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn, Cn, Dn,
-                                  En, Fn, 0.f, in_grp ? L.gt.off : kDeadOffset, L.I, M);
-        else
+        if (wave_fast) {
+            const float off = in_grp ? L.gt.off : kDeadOffset;
+            const float kshift = in_grp ? chain_shift(L, A2, Bn, Cn) : 2.0f;
+            if (a.chain && __all(kshift >= 0.f))
+                pair_moments<C, true, true>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn,
+                                            Cn, Dn, En, Fn, 0.f, off, kshift, L.I, M);
+            else
+                pair_moments<C, true>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn, Cn,
+                                      Dn, En, Fn, 0.f, off, 0.f, L.I, M);
+        } else {
             pair_moments<C, false>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn, Cn,
-                                   Dn, En, Fn, L.gt.shift, in_grp ? L.gt.half : -1.f, L.I, M);
+                                   Dn, En, Fn, L.gt.shift, in_grp ? L.gt.half : -1.f, 0.f, L.I, M);
+        }
         __syncthreads();  // a later group restages the slots
     }
     if (!mine) return;
@@ -1511,6 +1591,10 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     args.D = D; args.H = H; args.W = W; args.Tx = Tx; args.Ty = Ty; args.n = n; args.n_isect = ni;
     args.fx = make_fastdiv((uint32_t)Tx);
     args.fy = make_fastdiv((uint32_t)Ty);
+    {
+        const char *chain = getenv("GSV_BWD_CHAIN");
+        args.chain = !(chain && strcmp(chain, "0") == 0);
+    }
     args.T = T;
     args.ids = gaussian_ids_sorted; args.pair_tiles = pair_tiles;
     args.pos_radii = reinterpret_cast<const float4 *>(pos3d_radii);

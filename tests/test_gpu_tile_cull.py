@@ -14,7 +14,11 @@ ellipsoid, and reports its decision per sorted pair (pair_live).  Checked here:
 - the backward given the flags (evaluating only the kept pairs, zero partials
   for the culled ones) returns the same bits as without them, for vol_grad and
   fused-L1 sources, in host-count and capacity (device-count) modes, including
-  sparse scenes whose waves span more tiles than one wave stages.
+  sparse scenes whose waves span more tiles than one wave stages.  That holds
+  with the backward's chained rows off (GSV_BWD_CHAIN=0): with them on, a
+  group of pairs takes them only when all of its pairs qualify, and the flags
+  change which pairs share a wave, so there the two agree to rounding
+  (rel 1e-4 / abs 1e-6) instead.
 """
 import dataclasses
 
@@ -23,7 +27,7 @@ import pytest
 import torch
 
 from gs_voxelizer import synthetic as S
-from helpers import l1_vol_grad, np32, small_config
+from helpers import l1_vol_grad, np32, report_close, small_config
 
 pytestmark = pytest.mark.gpu
 
@@ -110,9 +114,19 @@ def test_culled_pairs_have_no_passing_voxel(device, name, work):
         assert culled.size > 0.03 * R["I"], (name, culled.size, R["I"])
 
 
+def _agree(what, a, b, exact):
+    if exact:
+        assert torch.equal(a, b), what
+    else:
+        report_close(what, np32(a), np32(b), 1e-4, 1e-6)
+
+
+@pytest.mark.parametrize("chain", ["0", "1"], ids=["chain_off", "chain_on"])
 @pytest.mark.parametrize("name,work", CASES, ids=IDS)
-def test_backward_with_cull_flags_is_bitwise_equal(device, name, work):
+def test_backward_with_cull_flags_is_bitwise_equal(device, monkeypatch, name, work, chain):
     import gs_voxelizer.cuda as _C
+    monkeypatch.setenv("GSV_BWD_CHAIN", chain)
+    exact = chain == "0"
     R = _run(work, device)
     cfg, w = work.cfg, R["w"]
     args = (cfg.vol, R["ids"], R["bins"], R["pr"], R["cn"], w.intensities)
@@ -124,7 +138,7 @@ def test_backward_with_cull_flags_is_bitwise_equal(device, name, work):
     culled = _C.voxelize_backward_per_gaussian(*args, gd, *boxes, tiles_sorted=R["tiles"],
                                                pair_live=R["live"])
     for a, b in zip(plain, culled):
-        assert torch.equal(a, b)
+        _agree(f"{name} vol_grad", a, b, exact)
     # fused L1 source
     tgt = torch.from_numpy(np.ascontiguousarray(np.broadcast_to(target, tuple(R["vol"].shape))))
     vol, loss, sign = _C.voxelize_forward_l1(*args, tgt.to(device).float())
@@ -133,7 +147,7 @@ def test_backward_with_cull_flags_is_bitwise_equal(device, name, work):
     culled = _C.voxelize_backward_l1(*args, sign, gl, None, *boxes, tiles_sorted=R["tiles"],
                                      pair_live=R["live"])
     for a, b in zip(plain, culled):
-        assert torch.equal(a, b)
+        _agree(f"{name} fused L1", a, b, exact)
     # capacity-sized arrays with the live count on the device
     cap = R["I"] + 777
     ids_c, bins_c, tiles_c = _C.bin_and_sort_gaussians_device_count(
@@ -147,4 +161,4 @@ def test_backward_with_cull_flags_is_bitwise_equal(device, name, work):
                                             count_dev=R["total"], pair_live=live_c)
     plain = _C.voxelize_backward_per_gaussian(*args, gd, *boxes, tiles_sorted=R["tiles"])
     for a, b in zip(plain, got):
-        assert torch.equal(a, b)
+        _agree(f"{name} capacity", a, b, exact)
