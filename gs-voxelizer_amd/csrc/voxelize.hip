@@ -313,7 +313,9 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                         // chain, span 7) or from uc = +0.5 outwards both ways (its
                         // first step left gives uc = -0.5; span 4).  With
                         // M >= |T1| on every row of the tile and an integer
-                        // K >= span * M + 2, K + 12.25 |A2| <= 120:
+                        // K >= span * M + 2, K + 12.25 |A2| <= 120 (K is the largest
+                        // such integer: it brings the exp2 arguments of the passing
+                        // voxels nearest to 0, where their rounding costs least):
                         //  - every 2^G is a normal number (G >= -120);
                         //  - 2^E <= 2^(-66 + 12.25 |A2| + K) < 2^54 (s <= off <= -66):
                         //    no overflow on any row, live or not;
@@ -324,11 +326,9 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                         const float bound_t1 =
                             (fabsf(rec[0]) + 3.5f * (fabsf(rec[1]) + fabsf(rec[2]))) * 1.001f;
                         const float span_g = 12.25f * fabsf(A2);
-                        const float K7 = ceilf(7.0f * bound_t1) + 2.0f;
-                        const float K4 = ceilf(4.0f * bound_t1) + 2.0f;
-                        one_way = K7 + span_g <= 120.0f;
-                        chain = one_way || K4 + span_g <= 120.0f;
-                        const float K = one_way ? K7 : K4;
+                        const float K = floorf(120.0f - span_g);
+                        one_way = ceilf(7.0f * bound_t1) + 2.0f <= K;
+                        chain = one_way || ceilf(4.0f * bound_t1) + 2.0f <= K;
                         rec[3] = (float)(chain ? t0 + (double)gt.off + (double)K : t0);
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
@@ -1029,10 +1029,12 @@ __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
 }
 
 // Shift K of the chained row evaluation of one pair (pair_moments, kChain), or
-// -1 when the pair's rows are too steep for it: K = ceil(3M) + 2 with M >= |S1|
-// on every row that can hold a passing voxel, and K + 12.25 |A2| <= 120 (so
-// 2^(A2 p'^2 - K) >= 2^-120, and 2^E <= 2^(-66 + 12.25 |A2| + K) < 2^54 since
-// sigma2 + off <= off <= -66).  S1 = 2 A2 mx + Bn dy + Cn dz is linear in the
+// -1 when the pair's rows are too steep for it: the largest integer K with
+// K + 12.25 |A2| <= 120 (so 2^(A2 p'^2 - K) >= 2^-120, and
+// 2^E <= 2^(-66 + 12.25 |A2| + K) < 2^54 since sigma2 + off <= off <= -66),
+// provided K >= 3M + 2 for an M >= |S1| on every row that can hold a passing
+// voxel.  The largest K brings the exp2 arguments of passing voxels nearest to
+// 0, where their rounding costs least.  S1 = 2 A2 mx + Bn dy + Cn dz is linear in the
 // row's offsets (dy, dz) from the centre: over the tile's rows it stays within
 // 3.5 (|Bn| + |Cn|) of its value at the tile's centre row; rows outside the
 // projection onto (y, z) of the gate ellipsoid d^T Q d <= k2 hold no passing
@@ -1056,8 +1058,8 @@ __device__ __forceinline__ float chain_shift(const BwdLane<C> &L, float A2, floa
     const float m_ell = (float)(fabs(2.0 * (double)A2 * (double)L.mxl) + sqrt(fmax(k2 * q, 0.0)));
     const float m_reach = (float)(fabs(2.0 * (double)A2) * (3.5 + sqrt(fmax(k2 / a, 0.0))));
     const float M = fminf(m_tile, fminf(m_ell, m_reach)) * 1.001f + 0.01f;
-    const float K = ceilf(3.0f * M) + 2.0f;
-    return K + 12.25f * fabsf(A2) <= 120.0f ? K : -1.0f;
+    const float K = floorf(120.0f - 12.25f * fabsf(A2));
+    return ceilf(3.0f * M) + 2.0f <= K ? K : -1.0f;
 }
 
 // Exponent e such that m * 2^e lies in [2^(kGradScaleExp-1), 2^kGradScaleExp);
