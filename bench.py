@@ -258,13 +258,13 @@ def main():
         achieved = bw["fp32_flops"] / (bwd_ms * 1e-3) / 1e12
         roof.update(achieved=round(achieved, 3), frac=round(achieved / FP32_PEAK_TFLOPS, 4),
                     fp32_flops_per_launch=bw["fp32_flops"],
-                    valu_issue_nontrans=bw["valu_issue_nontrans"],
+                    valu_insts_per_simd_cycle=bw["valu_insts_per_simd_cycle"],
                     counters=f"profiles/valu_{cfg.name}.json")
         fw = counters["per_launch"].get("voxelize_forward")
         if fw is not None:
             roof["forward"] = {"kernel": "k_vox_fwd", "duration_ms": round(fwd_ms, 4),
                                "achieved": round(fw["fp32_flops"] / (fwd_ms * 1e-3) / 1e12, 3),
-                               "valu_issue_nontrans": fw["valu_issue_nontrans"]}
+                               "valu_insts_per_simd_cycle": fw["valu_insts_per_simd_cycle"]}
             roof["forward"]["frac"] = round(roof["forward"]["achieved"] / FP32_PEAK_TFLOPS, 4)
     if traffic is not None and traffic.get("evals") == evals:
         roof["traffic"] = traffic.get("voxelize_backward_hbm_bytes_per_launch")
