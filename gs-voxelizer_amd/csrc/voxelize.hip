@@ -303,8 +303,8 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                         rec[1] = -q1.x; rec[2] = -q1.y;
                         const double t0 = X * (a2 * X + bb * Y + cc * Z) + Y * (dd * Y + ee * Z) +
                                           ff * Z * Z;
-                        rec[4] = (float)(-(bb * X + 2.0 * dd * Y + ee * Z));
-                        rec[5] = (float)(-(cc * X + ee * Y + 2.0 * ff * Z));
+                        const double ty = -(bb * X + 2.0 * dd * Y + ee * Z);
+                        const double tz = -(cc * X + ee * Y + 2.0 * ff * Z);
                         rec[6] = q1.z; rec[7] = q1.w;
                         rec[8] = F;
                         // Chained rows (the first two loops below) split s(u) into
@@ -323,13 +323,19 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
                         //    in uc, so every product of the chain up to it is at
                         //    least 2^(-126 + K - span * M) > 2^-126: no factor is
                         //    flushed early, and a product flushes only where s < -126.
+                        // The record's (t0, ty, tz) then hold the anchor's exponent,
+                        // E at uc = -3.5 or +0.5: T0 - uc T1 in the same polynomial.
                         const float bound_t1 =
                             (fabsf(rec[0]) + 3.5f * (fabsf(rec[1]) + fabsf(rec[2]))) * 1.001f;
                         const float span_g = 12.25f * fabsf(A2);
                         const float K = floorf(120.0f - span_g);
                         one_way = ceilf(7.0f * bound_t1) + 2.0f <= K;
                         chain = one_way || ceilf(4.0f * bound_t1) + 2.0f <= K;
-                        rec[3] = (float)(chain ? t0 + (double)gt.off + (double)K : t0);
+                        const double at = one_way ? -3.5 : (chain ? 0.5 : 0.0);  // anchor uc
+                        const double t1 = 2.0 * a2 * X + bb * Y + cc * Z;
+                        rec[3] = (float)(t0 - at * t1 + (chain ? (double)gt.off + (double)K : 0.0));
+                        rec[4] = (float)(ty - at * (double)rec[1]);
+                        rec[5] = (float)(tz - at * (double)rec[2]);
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const float uc = 0.5f + (float)k;
@@ -376,14 +382,14 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
             if (C > 2) iw[2] = r3.w;
             if (C > 3) iw[3] = s_rec[j][kRecF4<C> - 1].x;
             const float T1 = fmaf(r0.y, py, fmaf(r0.z, pz, r0.x));
-            const float T0 =
+            const float E0 =  // E at uc = -3.5
                 fmaf(r2.x, pz2, fmaf(r1.w, pyz, fmaf(r1.z, py2, fmaf(r1.y, pz, fmaf(r1.x, py, r0.w)))));
             const float G[4] = {r2.y, r2.z, r2.w, r3.x};  // 2^(A2 uc^2 - K), |uc| = 0.5 .. 3.5
             // two v_exp_f32 per row: 2^E at uc = -3.5 and the step 2^-T1 towards
             // +x; every product below 2^-126 is 0 (binary32 flush-to-zero mode),
             // which is the gate, as v_exp_f32's own flush is on the other paths
             const float step = __builtin_amdgcn_exp2f(-T1);
-            float e = __builtin_amdgcn_exp2f(fmaf(3.5f, T1, T0));
+            float e = __builtin_amdgcn_exp2f(E0);
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
                 const float a = e * G[u < 4 ? 3 - u : u - 4];
@@ -402,14 +408,14 @@ __global__ __launch_bounds__(kWave) void k_vox_fwd(
             if (C > 2) iw[2] = r3.w;
             if (C > 3) iw[3] = s_rec[j][kRecF4<C> - 1].x;
             const float T1 = fmaf(r0.y, py, fmaf(r0.z, pz, r0.x));
-            const float T0 =
+            const float E0 =  // E at uc = +0.5
                 fmaf(r2.x, pz2, fmaf(r1.w, pyz, fmaf(r1.z, py2, fmaf(r1.y, pz, fmaf(r1.x, py, r0.w)))));
             const float G[4] = {r2.y, r2.z, r2.w, r3.x};  // 2^(A2 uc^2 - K), |uc| = 0.5 .. 3.5
             // three v_exp_f32 per row: 2^E at uc = +0.5 and the steps 2^-T1
             // (towards +x) and 2^T1 (towards -x); uc = -0.5 is the first step
             // left of it, so the chain spans 4 units of uc on the left
             const float step_r = __builtin_amdgcn_exp2f(-T1), step_l = __builtin_amdgcn_exp2f(T1);
-            float er = __builtin_amdgcn_exp2f(fmaf(-0.5f, T1, T0));
+            float er = __builtin_amdgcn_exp2f(E0);
             float el = er * step_l;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -649,6 +655,9 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
         // gate-free: S1 = Bn dy + K1, S0 = dy (Dn dy + L1) + K0
         const float K1 = fmaf(2.0f, A2m, Cdz), L1 = Bm + Edz;
         const float K0 = fmaf(dz, fmaf(Fn, dz, Cm), K0base);
+        // kChain: the exponent at p' = -3.5, S0 + 3.5 S1 = dy (Dn dy + L1a) + K0a
+        const float L1a = kChain ? fmaf(3.5f, Bn, L1) : 0.f;
+        const float K0a = kChain ? fmaf(3.5f, K1, K0) : 0.f;
         const float R0z = kGateFree ? (Fn * dz) * dz : fmaf(Fn * dz, dz, -shift);
         float Q0 = 0.f, Qx = 0.f, Qxx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
 #pragma unroll
@@ -666,10 +675,10 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
             float R1 = 0.f, R0 = 0.f;
             if (kChain) {
                 const float S1 = fmaf(Bn, dy, K1);
-                const float S0 = fmaf(dy, fmaf(Dn, dy, L1), K0);  // + bound + K
+                const float Ea = fmaf(dy, fmaf(Dn, dy, L1a), K0a);  // E at p' = -3.5 (+ bound + K)
                 const float step = __builtin_amdgcn_exp2f(-S1);
-                float e1 = __builtin_amdgcn_exp2f(fmaf(3.5f, S1, S0));   // p' = -3.5
-                float e2 = __builtin_amdgcn_exp2f(fmaf(-0.5f, S1, S0));  // p' = +0.5
+                float e1 = __builtin_amdgcn_exp2f(Ea);                    // p' = -3.5
+                float e2 = __builtin_amdgcn_exp2f(fmaf(-4.0f, S1, Ea));  // p' = +0.5
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     sv[k] = e1 * P[3 - k];
