@@ -298,7 +298,7 @@ def voxelize_forward_l1(vol_size, gaussian_ids_sorted, tile_bins, pos3d, conics,
                         target, pair_live=None):
     """voxelize_forward fused with torch.nn.functional.l1_loss(volume, target) (mean).
     Returns (volume (D, H, W, C), loss (0-d device tensor), sign): sign is
-    sgn(volume - target) as int8 (2 where the difference is NaN), kept for
+    sgn(volume - target) as int8 (0 where the difference is NaN, as torch's sign), kept for
     voxelize_backward_l1.  pair_live as in voxelize_forward."""
     _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities)
     channels = _channels(intensities)

@@ -117,3 +117,35 @@ def test_fused_l1_nan_and_inf_targets_match_unfused(device, per_gaussian):
     for nm, a, b in zip(("pos3d", "scale3d", "quat", "intensity"), grads, ref_grads):
         assert torch.isfinite(b).all(), nm
         assert torch.equal(a, b), f"grad {nm}"
+
+
+def test_fused_l1_sign_bytes_keep_denormal_differences(device):
+    """The stored sign bytes are torch's sign(volume - target) element for
+    element, also where the difference is a denormal number (targets of
+    +-1e-40 where the volume is 0).  The library's voxelize code runs in
+    binary32 flush-to-zero mode,
+    where a denormal operand reads as 0; the sign is decided on the bit
+    patterns, as IEEE arithmetic with denormals (torch's) decides it."""
+    import gs_voxelizer.cuda as _C
+    from helpers import gpu_bin
+    work = S.make_gaussians(small_config(1, 2000), seed=10)
+    cfg, n = work.cfg, work.cfg.n
+    w = work.to(device)
+    pr, cn, tmin, tmax, nt = _C.optim_to_render_forward(n, w.pos3d, w.scale3d, w.quat,
+                                                        w.intensities, cfg.vol, cfg.world,
+                                                        cfg.center)
+    _, _, ids, bins = gpu_bin(n, tmin, tmax, nt, cfg.vol)
+    vol0 = _C.voxelize_forward(cfg.vol, ids, bins, pr, cn, w.intensities).reshape(-1)
+    target = S.phantom(work, device=device).clone().reshape(-1)
+    g = torch.Generator(device="cpu").manual_seed(11)
+    zero = torch.nonzero(vol0 == 0).view(-1).cpu()
+    zi = zero[torch.randperm(zero.numel(), generator=g)[:400]].to(device)
+    target[zi[:200]] = 1e-40
+    target[zi[200:]] = -1e-40
+    assert bool((target[zi].abs() < 1.2e-38).all()) and bool((target[zi] != 0).all())
+    vol, loss, sign = _C.voxelize_forward_l1(cfg.vol, ids, bins, pr, cn, w.intensities,
+                                             target.view(cfg.vol))
+    assert torch.equal(vol.reshape(-1), vol0)
+    ref = torch.sign(vol.reshape(-1) - target)
+    assert torch.equal(ref[zi], -torch.sign(target[zi]))  # torch keeps the denormal difference
+    assert torch.equal(sign.reshape(-1).to(torch.float32), ref)
