@@ -1293,23 +1293,21 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
 
 // The zero partials of the pairs the forward culled, spread over the W work
 // waves: wave wv writes those of culled items [wv*c, (wv+1)*c), c =
-// ceil(culled / W), one lane per pair.
+// ceil(culled / W), one lane per pair.  culled_slot looks up one item's slot
+// (-1: none); the kernel looks up each lane's first item before its own work
+// and writes the zeros after it, so those loads overlap the work.
+__device__ __forceinline__ int64_t culled_slot(const BwdArgs &a, int64_t q) {
+    const int p = a.order[a.n_isect - 1 - q];
+    const int t = a.pair_tiles[p];
+    if (t < 0 || t >= a.T) return -1;
+    return emission_slot(a.ids[p], t, a);
+}
+
 template <int C>
-__device__ __forceinline__ void bwd_zero_culled(const BwdArgs &a, int64_t wv, int64_t W) {
-    const int64_t culled = (int64_t)a.n_isect - a.n_work;
-    if (culled <= 0) return;
-    const int64_t c = (culled + W - 1) / W;
-    const int64_t q1 = min<int64_t>(culled, (wv + 1) * c);
-    for (int64_t q = wv * c + threadIdx.x; q < q1; q += kWave) {
-        const int p = a.order[a.n_isect - 1 - q];
-        const int t = a.pair_tiles[p];
-        if (t < 0 || t >= a.T) continue;
-        const int64_t e = emission_slot(a.ids[p], t, a);
-        if (e < 0) continue;
-        float *dst = a.partial + e * (9 + C);
+__device__ __forceinline__ void zero_partial(const BwdArgs &a, int64_t e) {
+    float *dst = a.partial + e * (9 + C);
 #pragma unroll
-        for (int k = 0; k < 9 + C; ++k) dst[k] = 0.f;
-    }
+    for (int k = 0; k < 9 + C; ++k) dst[k] = 0.f;
 }
 
 // One wave per 64 consecutive (tile, Gaussian) pairs of the sorted list (or of
@@ -1331,19 +1329,33 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
     const int64_t per = xcd_per(W);
     if ((int64_t)(blockIdx.x / kXcds) >= per) return;
     const int64_t wv = xcd_remap(blockIdx.x, per);
-    if (zeros) bwd_zero_culled<C>(a, wv, W);
+    int64_t zq = 0, zq1 = 0, ze = -1;  // this lane's culled items [zq, zq1), step kWave
+    if (zeros) {
+        const int64_t culled = (int64_t)a.n_isect - a.n_work;
+        const int64_t c = culled > 0 ? (culled + W - 1) / W : 0;
+        zq = wv * c + threadIdx.x;
+        zq1 = min<int64_t>(culled, (wv + 1) * c);
+        if (zq < zq1) ze = culled_slot(a, zq);
+    }
     const int64_t p0 = wv * kWave;
-    if (p0 >= a.n_work) return;
-    BwdLane<C> L;
-    uint64_t starts;
-    int nslots;
-    if (!bwd_slots(a, p0, L, starts, nslots)) return;
-    bwd_gaussian(a, L);
-    // one wave-uniform choice: gate-free unless a live lane needs the exact gate
-    const bool wave_fast = __all(!L.live || L.fast);
-    const bool any_live = __any(L.live);
-    if (!any_live && a.partial == nullptr) return;
-    bwd_group<C, K>(a, L, starts, 0, wave_fast, any_live, s_g);
+    if (p0 < a.n_work) {
+        BwdLane<C> L;
+        uint64_t starts;
+        int nslots;
+        if (bwd_slots(a, p0, L, starts, nslots)) {
+            bwd_gaussian(a, L);
+            // one wave-uniform choice: gate-free unless a live lane needs the exact gate
+            const bool wave_fast = __all(!L.live || L.fast);
+            const bool any_live = __any(L.live);
+            if (any_live || a.partial != nullptr)
+                bwd_group<C, K>(a, L, starts, 0, wave_fast, any_live, s_g);
+        }
+    }
+    if (ze >= 0) zero_partial<C>(a, ze);
+    for (int64_t q = zq + kWave; q < zq1; q += kWave) {
+        const int64_t e = culled_slot(a, q);
+        if (e >= 0) zero_partial<C>(a, e);
+    }
 }
 
 // The pairs that k_vox_bwd left: those of the waves spanning more than K tiles,
