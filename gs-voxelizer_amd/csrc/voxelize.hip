@@ -63,6 +63,16 @@ constexpr float kLn2 = 0.693147180559945309f;
 constexpr float kLog2MinContrib = -19.9315685693241741f;  // log2(1e-6)
 
 constexpr float kExpFlush = 126.0f;     // v_exp_f32 results below 2^-126 are 0
+
+// The forward at C = 1 accumulates I * alpha / kAccUnit, kAccUnit = fl(1e-6) * 2^126:
+// a term then falls below 2^-126, and a product that forms it is flushed to 0,
+// exactly when I * alpha < fl(1e-6), the reference's gate.  The chained rows fold
+// the weight I * 2^-off / kAccUnit (1 up to the rounding of off) into their
+// per-Gaussian factors, so each voxel's gated product is added with a
+// two-operand v_add_f32 instead of a three-operand FMA against the weight; the
+// other paths scale their weights alike, and the epilogue multiplies once.
+constexpr float kAccUnit = 1e-6f * 0x1p126f;
+constexpr double kInvAccUnit = 1.0 / (double)kAccUnit;
 constexpr float kDeadOffset = -1000.0f;  // exponent offset that zeroes a lane
 
 struct Gate {
@@ -161,6 +171,13 @@ __device__ __forceinline__ bool may_touch(float mx, float my, float mz, float a,
     const float r = (float)(fabs(nx) * ex + fabs(ny) * ey + fabs(nz) * ez);
     const float K = __builtin_amdgcn_sqrtf(k2) * 1.001f + 0.01f, sm = __builtin_amdgcn_sqrtf(m);
     return !(sm * (sm - K) > r * 1.001f + 0.01f);  // NaN anywhere -> comparisons false -> keep
+}
+
+// x + y, never contracted with a product that feeds it: the operand is a
+// separately rounded (and, below 2^-126, flushed) binary32 product.
+__device__ __forceinline__ float add_nc(float x, float y) {
+#pragma clang fp contract(off)
+    return x + y;
 }
 
 __host__ __device__ inline bool aligned_to(const void *p, uintptr_t a) {
@@ -338,22 +355,28 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(C == 1 ? 
                         rec[3] = (float)(t0 - at * t1 + (chain ? (double)gt.off + (double)K : 0.0));
                         rec[4] = (float)(ty - at * (double)rec[1]);
                         rec[5] = (float)(tz - at * (double)rec[2]);
+                        // C = 1: the weight I * 2^-off in units of kAccUnit, ~1 (see
+                        // kAccUnit); the chains carry it in their factors
+                        const double rho = C == 1 ? (double)I[0] * (double)gt.fscale * kInvAccUnit : 1.0;
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const float uc = 0.5f + (float)k;
                             // 2^-K applied exactly: the exp2 argument stays small
-                            rec[9 + k] = chain ? ldexpf(__builtin_amdgcn_exp2f(A2 * (uc * uc)), -(int)K)
+                            const float Gk = ldexpf(__builtin_amdgcn_exp2f(A2 * (uc * uc)), -(int)K);
+                            rec[9 + k] = chain ? (C == 1 ? (float)((double)Gk * rho) : Gk)
                                                : fmaf(A2, uc * uc, gt.off);
                         }
 #pragma unroll
-                        for (int c = 0; c < C; ++c) rec[13 + c] = I[c] * gt.fscale;
+                        for (int c = 0; c < C; ++c) rec[13 + c] = C == 1 ? (float)rho : I[c] * gt.fscale;
                     } else {
                         // (cx, cy, cz, A2 | B, C, D, E | F, shift, half, A2 cx | I*2^shift)
                         rec[0] = cx; rec[1] = cy; rec[2] = cz; rec[3] = A2;
                         rec[4] = q1.x; rec[5] = q1.y; rec[6] = q1.z; rec[7] = q1.w;
                         rec[8] = F; rec[9] = gt.shift; rec[10] = gt.half; rec[11] = A2 * cx;
 #pragma unroll
-                        for (int c = 0; c < C; ++c) rec[12 + c] = I[c] * gt.scale;
+                        for (int c = 0; c < C; ++c)
+                            rec[12 + c] = C == 1 ? (float)((double)I[0] * (double)gt.scale * kInvAccUnit)
+                                                 : I[c] * gt.scale;
                     }
 #pragma unroll
                     for (int q = 0; q < kRecF4<C>; ++q)
@@ -395,8 +418,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(C == 1 ? 
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
                 const float a = e * G[u < 4 ? 3 - u : u - 4];
+                if (C == 1) {
+                    acc[u][0] = add_nc(acc[u][0], a);  // a = I alpha / kAccUnit, gated
+                } else {
 #pragma unroll
-                for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
+                    for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
+                }
                 if (u + 1 < GSV_TILE) e *= step;
             }
         }
@@ -422,10 +449,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(C == 1 ? 
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const float ar = er * G[k], al = el * G[k];
+                if (C == 1) {
+                    acc[4 + k][0] = add_nc(acc[4 + k][0], ar);
+                    acc[3 - k][0] = add_nc(acc[3 - k][0], al);
+                } else {
 #pragma unroll
-                for (int c = 0; c < C; ++c) {
-                    acc[4 + k][c] = fmaf(ar, iw[c], acc[4 + k][c]);
-                    acc[3 - k][c] = fmaf(al, iw[c], acc[3 - k][c]);
+                    for (int c = 0; c < C; ++c) {
+                        acc[4 + k][c] = fmaf(ar, iw[c], acc[4 + k][c]);
+                        acc[3 - k][c] = fmaf(al, iw[c], acc[3 - k][c]);
+                    }
                 }
                 if (k < 3) {
                     er *= step_r;
@@ -478,6 +510,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(C == 1 ? 
             }
         }
         __syncthreads();
+    }
+    if (C == 1) {
+#pragma unroll
+        for (int u = 0; u < GSV_TILE; ++u) acc[u][0] *= kAccUnit;
     }
     const int y = tg.y0 + (lane & 7), z = tg.z0 + (lane >> 3);
     float lsum = 0.f;  // fused L1: sum of |volume - target| over the lane's row
@@ -704,7 +740,7 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                 R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
                 if (kGateFree) R0 += bound;  // the offset enters after the small terms
             }
-            float W0 = 0.f, W1 = 0.f, W2 = 0.f;
+            float W1 = 0.f, W2 = 0.f, h[GSV_TILE];
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
                 float a;
@@ -717,9 +753,8 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                     else
                         a = (fabsf(s) <= bound) ? __builtin_amdgcn_exp2f(s) : 0.f;
                 }
-                float h;
                 if (C == 1) {
-                    h = a * gv[u];
+                    h[u] = a * gv[u];
                 } else {
                     float G = 0.f;
 #pragma unroll
@@ -727,12 +762,15 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                         G = fmaf(I[c], gv[u * C + c], G);
                         M.dI[c] = fmaf(a, gv[u * C + c], M.dI[c]);
                     }
-                    h = a * G;
+                    h[u] = a * G;
                 }
-                W0 += h;
-                W1 = fmaf(h, dxu[u], W1);
-                W2 = fmaf(h, dxu2[u], W2);
+                W1 = fmaf(h[u], dxu[u], W1);
+                W2 = fmaf(h[u], dxu2[u], W2);
             }
+            // the row sum of the h already formed: 7 two-operand adds, which
+            // issue faster than the 8 three-operand FMAs a contracted a*g sum takes
+            const float W0 = add_nc(add_nc(add_nc(h[0], h[1]), add_nc(h[2], h[3])),
+                                    add_nc(add_nc(h[4], h[5]), add_nc(h[6], h[7])));
             Q0 += W0;
             Qx += W1;
             Qxx += W2;
