@@ -654,12 +654,13 @@ struct Moments {
 //              the voxels u and 7 - u share S0 + P_k (at C = 2 the four P_k
 //              cost a wave per SIMD, 5 -> 4, and still gain ~6 %; at C >= 3
 //              the staged tiles' LDS limits occupancy first);
-//   kChain (gate-free too): a row's a from three v_exp_f32 instead of eight,
+//   kChain (gate-free too): a row's a from two v_exp_f32 instead of eight,
 //              as products, which the binary32 flush-to-zero mode gates like
 //              v_exp_f32: E = S0 + bound + K - p' S1 from 2^E at p' = -3.5 and
 //              p' = +0.5, each stepped three times by 2^-S1, times the lane's
-//              2^(A2 p'^2 - K).  K (chain_shift) keeps every product of a chain
-//              up to a passing voxel above 2^-126 and every factor finite;
+//              2^(A2 p'^2 - K); the step itself is the previous row's times
+//              2^Bn.  K (chain_shift) keeps every product of a chain up to a
+//              passing voxel above 2^-126 and every factor finite;
 //   otherwise: a = exp2(s) if |s| <= bound, s = sigma2 - shift.
 template <int C, bool kGateFree, bool kChain = false>
 __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int nz,
@@ -687,6 +688,10 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
             P[k] = ldexpf(__builtin_amdgcn_exp2f(A2 * ((0.5f + k) * (0.5f + k))), -(int)K);
     }
     const float K0base = kChain ? fmaf(A2m, mxl, bound + K) : A2m * mxl;
+    // kChain: a row's step 2^-S1 is the previous row's times 2^Bn (S1 falls by
+    // Bn per row), one v_mul_f32 instead of a v_exp_f32; the first row of each
+    // plane takes its own exp2
+    const float rB = kChain ? __builtin_amdgcn_exp2f(Bn) : 0.f;
     for (int lz = 0; lz < nz; ++lz) {
         const float dz = mzl - ((float)lz - 3.5f);
         const float Cdz = Cn * dz, Edz = En * dz;
@@ -697,6 +702,7 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
         const float L1a = kChain ? fmaf(3.5f, Bn, L1) : 0.f;
         const float K0a = kChain ? fmaf(3.5f, K1, K0) : 0.f;
         const float R0z = kGateFree ? (Fn * dz) * dz : fmaf(Fn * dz, dz, -shift);
+        float stp = kChain ? __builtin_amdgcn_exp2f(-fmaf(Bn, myl + 3.5f, K1)) : 0.f;  // ly = 0
         float Q0 = 0.f, Qx = 0.f, Qxx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
 #pragma unroll
         for (int ly = 0; ly < GSV_TILE; ++ly) {
@@ -714,7 +720,8 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
             if (kChain) {
                 const float S1 = fmaf(Bn, dy, K1);
                 const float Ea = fmaf(dy, fmaf(Dn, dy, L1a), K0a);  // E at p' = -3.5 (+ bound + K)
-                const float step = __builtin_amdgcn_exp2f(-S1);
+                const float step = stp;  // 2^-S1
+                stp *= rB;
                 float e1 = __builtin_amdgcn_exp2f(Ea);                    // p' = -3.5
                 float e2 = __builtin_amdgcn_exp2f(fmaf(-4.0f, S1, Ea));  // p' = +0.5
 #pragma unroll
@@ -1108,7 +1115,10 @@ __device__ __forceinline__ float chain_shift(const BwdLane<C> &L, float A2, floa
     const float m_reach = (float)(fabs(2.0 * (double)A2) * (3.5 + sqrt(fmax(k2 / a, 0.0))));
     const float M = fminf(m_tile, fminf(m_ell, m_reach)) * 1.001f + 0.01f;
     const float K = floorf(120.0f - 12.25f * fabsf(A2));
-    return ceilf(3.0f * M) + 2.0f <= K ? K : -1.0f;
+    // Rows outside the gate ellipse are bounded by m_tile alone: below 120 every
+    // row's step 2^-S1 (and 2^Bn, the ratio of neighbouring rows' steps) is a
+    // finite normal number, so no product of a dead row is inf * 0.
+    return ceilf(3.0f * M) + 2.0f <= K && m_tile < 120.0f ? K : -1.0f;
 }
 
 // Exponent e such that m * 2^e lies in [2^(kGradScaleExp-1), 2^kGradScaleExp);

@@ -184,7 +184,9 @@ def _backward_chains(P):
     m_reach = (np.abs(2.0 * A2.astype(np.float64)) * (3.5 + np.sqrt(np.maximum(k2 / a, 0)))).astype(np.float32)
     M = np.minimum(m_tile, np.minimum(m_ell, m_reach)) * F32(1.001) + F32(0.01)
     K = np.floor(F32(120.0) - F32(12.25) * np.abs(A2))
-    qualifies = np.ceil(F32(3.0) * M) + 2 <= K
+    span_ok = np.ceil(F32(3.0) * M) + 2 <= K
+    # every row of the tile, dead ones included, keeps |S1| below 120
+    qualifies = span_ok & (m_tile < F32(120.0))
     k = (np.arange(4) + 0.5).astype(np.float32)
     with np.errstate(over="ignore"):  # K < 0 only for pairs that do not qualify
         Pk = _ftz(np.ldexp(_exp2(A2[:, None] * (k * k)), -K.astype(np.int64)[:, None]))
@@ -199,7 +201,15 @@ def _backward_chains(P):
           + Fd * dz * dz)
     Ea = (S0 + 3.5 * S1.astype(np.float64) + off.astype(np.float64)[:, None]
           + K.astype(np.float64)[:, None]).astype(np.float32)            # E at p' = -3.5
-    step = _exp2(-S1)
+    # the step 2^-S1 of row (ly, lz) is row (0, lz)'s times (2^Bn)^ly
+    rB = _exp2(Bn)
+    step = np.zeros_like(S1)
+    for lz in range(8):
+        rows = slice(8 * lz, 8 * lz + 8)
+        st = _exp2(-S1[:, 8 * lz])
+        for ly in range(8):
+            step[:, 8 * lz + ly] = st
+            st = _mul(st, rB)
     e1 = _exp2(Ea)
     e2 = _exp2((Ea.astype(np.float64) - 4.0 * S1).astype(np.float32))  # p' = +0.5
     out = np.zeros(Ea.shape + (8,), np.float32)
@@ -207,7 +217,7 @@ def _backward_chains(P):
         out[..., kk] = _mul(e1, Pk[:, 3 - kk][:, None])
         out[..., 4 + kk] = _mul(e2, Pk[:, kk][:, None])
         e1, e2 = _mul(e1, step), _mul(e2, step)
-    return out, qualifies
+    return out, qualifies, span_ok & ~qualifies
 
 
 def _random_pairs(n, seed):
@@ -223,6 +233,28 @@ def _random_pairs(n, seed):
     Q = np.einsum("nij,nj,nkj->nik", q, 1.0 / sig ** 2, q)
     con = np.stack([Q[:, 0, 0], Q[:, 0, 1], Q[:, 0, 2], Q[:, 1, 1], Q[:, 1, 2], Q[:, 2, 2]], 1)
     P = np.concatenate([g.uniform(-7, 7, (n, 3)), con.astype(np.float32),
+                        g.uniform(-40, -14, (n, 1))], 1)
+    return P.astype(np.float32).astype(np.float64)
+
+
+def _needle_pairs(n, seed):
+    """Tilted needles: one long axis (1.2-3 voxels) within 0.05-0.35 rad of x,
+    two short ones (0.12-0.3 voxels).  Their conics couple x strongly to y and
+    z (large |b|, |c| against a small a): the x-slope S1 of a row varies by far
+    more over the tile than over the gate ellipse, and on rows away from the
+    ellipse it can exceed 128, where 2^-S1 overflows binary32."""
+    g = np.random.default_rng(seed)
+    th = g.uniform(0.05, 0.35, n)
+    ph = g.uniform(0, 2 * np.pi, n)
+    u = np.stack([np.cos(th), np.sin(th) * np.cos(ph), np.sin(th) * np.sin(ph)], 1)
+    v = np.cross(u, g.normal(size=(n, 3)))
+    v /= np.linalg.norm(v, axis=1, keepdims=True)
+    w = np.cross(u, v)
+    R = np.stack([u, v, w], 2)                                    # columns: axes
+    sig = np.stack([g.uniform(1.2, 3.0, n), g.uniform(0.12, 0.3, n), g.uniform(0.12, 0.3, n)], 1)
+    Q = np.einsum("nij,nj,nkj->nik", R, 1.0 / sig ** 2, R)
+    con = np.stack([Q[:, 0, 0], Q[:, 0, 1], Q[:, 0, 2], Q[:, 1, 1], Q[:, 1, 2], Q[:, 2, 2]], 1)
+    P = np.concatenate([g.uniform(-6, 6, (n, 3)), con.astype(np.float32),
                         g.uniform(-40, -14, (n, 1))], 1)
     return P.astype(np.float32).astype(np.float64)
 
@@ -254,7 +286,22 @@ def test_chained_rows_gate_like_exp2(name, make, npairs, share):
     fwd, fwd_ok = _forward_chains(P)
     n_f, live_f = _check(f"{name} forward", s_exact, fwd, fwd_ok)
     # the backward walks the same rows with the Gaussian-centred form
-    bwd, bwd_ok = _backward_chains(P)
+    bwd, bwd_ok, _ = _backward_chains(P)
     n_b, live_b = _check(f"{name} backward", s_exact, bwd, bwd_ok)
     assert n_f > share * len(P) and n_b > share * len(P), (name, n_f, n_b, len(P))
     assert live_f > 0 and live_b > 0
+
+
+def test_backward_chain_bounds_dead_rows():
+    """chain_shift's m_tile < 120 condition: needles whose live rows qualify
+    but whose dead rows reach |S1| >= 128 must take the exact path, and every
+    qualifying pair stays finite with the right gate."""
+    P = _needle_pairs(6000, seed=9)
+    s_exact = _exact_exponent(P)
+    bwd, ok, excluded = _backward_chains(P)
+    n_b, live_b = _check("needles backward", s_exact, bwd, ok)
+    assert n_b > 0.05 * len(P) and live_b > 0, (n_b, len(P))
+    # the scene exercises the condition: without it these pairs would take the
+    # chains and some of their products would overflow
+    assert excluded.sum() > 0.01 * len(P), int(excluded.sum())
+    assert not np.isfinite(bwd[excluded]).all()
