@@ -230,6 +230,7 @@ def main():
     # are queued back to back.
     timer = KernelTimer(_C, ["optim_to_render_forward", "cumsum_tiles_hit",
                              "bin_and_sort_gaussians", "bin_and_sort_gaussians_device_count",
+                             "cumsum_bin_and_sort_device_count",
                              "voxelize_forward", "voxelize_backward_per_gaussian",
                              "optim_to_render_backward"])
     timer.install()

@@ -51,6 +51,7 @@
 #include <mutex>
 
 #include "gsv_device.h"
+#include "gsv_scan.h"
 
 namespace gsv {
 namespace {
@@ -313,15 +314,15 @@ __device__ __forceinline__ int block_scan_total(int v, int *s_wtot, int *total) 
 // with two 16-byte stores, so every access is coalesced.
 constexpr int kDigitScanThreads = 1024;
 constexpr int kDigitScanItems = 8;
-constexpr int kDigitScanTile = kDigitScanThreads * kDigitScanItems;
 
-__global__ __launch_bounds__(kDigitScanThreads) void k_digit_scan(int *__restrict__ hist,
-                                                                  int nblocks, int hstride,
-                                                                  int *__restrict__ totals) {
-    __shared__ int s_wtot[kDigitScanThreads / kWave];
-    int *row = hist + (int64_t)blockIdx.x * hstride;
+// The scan of one digit's row by a workgroup of NT threads (s_wtot: NT / 64
+// ints), in tiles of NT * 8; *total_slot gets the row's total.
+template <int NT>
+__device__ __forceinline__ void digit_scan_row(int *__restrict__ row, int nblocks,
+                                               int *__restrict__ total_slot, int *s_wtot) {
+    constexpr int kTileItems = NT * kDigitScanItems;
     int carry = 0;
-    for (int base = 0; base < nblocks; base += kDigitScanTile) {
+    for (int base = 0; base < nblocks; base += kTileItems) {
         const int i0 = base + (int)threadIdx.x * kDigitScanItems;
         int v[kDigitScanItems];
         const bool whole = i0 + kDigitScanItems <= nblocks;
@@ -338,7 +339,7 @@ __global__ __launch_bounds__(kDigitScanThreads) void k_digit_scan(int *__restric
 #pragma unroll
         for (int k = 0; k < kDigitScanItems; ++k) s += v[k];
         int total;
-        int run = carry + block_scan_total<kDigitScanThreads>(s, s_wtot, &total);
+        int run = carry + block_scan_total<NT>(s, s_wtot, &total);
         int o[kDigitScanItems];
 #pragma unroll
         for (int k = 0; k < kDigitScanItems; ++k) {
@@ -356,7 +357,15 @@ __global__ __launch_bounds__(kDigitScanThreads) void k_digit_scan(int *__restric
         carry += total;
         __syncthreads();  // s_wtot is rewritten by the next tile's scan
     }
-    if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+    if (threadIdx.x == 0) *total_slot = carry;
+}
+
+__global__ __launch_bounds__(kDigitScanThreads) void k_digit_scan(int *__restrict__ hist,
+                                                                  int nblocks, int hstride,
+                                                                  int *__restrict__ totals) {
+    __shared__ int s_wtot[kDigitScanThreads / kWave];
+    digit_scan_row<kDigitScanThreads>(hist + (int64_t)blockIdx.x * hstride, nblocks,
+                                      totals + blockIdx.x, s_wtot);
 }
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
@@ -630,6 +639,80 @@ __global__ __launch_bounds__(kSplitThreads) void k_bucket_hist(
     add_row_counts(G, r, nb, s_h);
     __syncthreads();
     for (int d = t; d < nb; d += kSplitThreads) hist[(int64_t)d * hstride + blockIdx.x] = s_h[d];
+}
+
+// ------------------------------------ prefix sum and bucket counts fused --
+//
+// When one call runs the prefix sum of num_tiles_hit and the binning
+// (gsv_cumsum_bin_and_sort_device_count), the bucket path's two small passes
+// ride on the scan's two launches: the chunks' bucket counts beside the scan's
+// block sums (they need the boxes and the tile counts, not the prefix sum),
+// the prefix over chunks beside the scan's apply pass.  Four launches for the
+// prefix sum and the binning instead of six; the same words, ids and bins.
+
+// A Gaussian's rows from its tile count instead of cum: equal to gauss_rows
+// (ns = cum[g] - cum[g-1] = num_tiles_hit[g]) whenever the pairs fit the
+// capacity.  Past it the binning's output is incomplete whichever counts it
+// uses, and the caller runs it again; every store stays guarded by cap.
+__device__ __forceinline__ GaussRows gauss_rows_nth(int g, int n, const int *__restrict__ nth,
+                                                    const int *__restrict__ tile_min,
+                                                    const int *__restrict__ tile_max) {
+    GaussRows r{};
+    if (g >= n) return r;
+    const int64_t ns = nth[g] > 0 ? nth[g] : 0;
+    r.mnx = tile_min[3 * g]; r.mny = tile_min[3 * g + 1]; r.mnz = tile_min[3 * g + 2];
+    r.ex = tile_max[3 * g] - r.mnx;
+    r.ey = tile_max[3 * g + 1] - r.mny;
+    const int ez = tile_max[3 * g + 2] - r.mnz;
+    const int64_t vol = (r.ex > 0 && r.ey > 0 && ez > 0) ? (int64_t)r.ex * r.ey * ez : 0;
+    const int64_t nv = min(ns, vol);
+    r.nvalid = (int)nv;
+    r.ninvalid = (int)(ns - nv);
+    r.nrows = nv > 0 ? (int)((nv + r.ex - 1) / r.ex) : 0;
+    return r;
+}
+
+static_assert(kSplitThreads == scan_detail::kThreads, "one block size for both halves");
+
+// Blocks [0, nb_scan): the scan's block sums of num_tiles_hit; blocks
+// nb_scan + c: chunk c's bucket counts, as k_bucket_hist.
+template <int Bt>
+__global__ __launch_bounds__(kSplitThreads) void k_sums_hist(
+    const int32_t *__restrict__ nth, int n, int nb_scan, int32_t *__restrict__ part,
+    const int *__restrict__ tile_min, const int *__restrict__ tile_max, BucketGeom G,
+    int *__restrict__ hist, int hstride) {
+    __shared__ int s_h[1 << Bt];
+    __shared__ int lds_waves[kSplitThreads / kWave];
+    if ((int)blockIdx.x < nb_scan) {  // uniform per block
+        scan_detail::block_sums_body(LoadI32{nth}, (int64_t)n, part, (int)blockIdx.x, lds_waves);
+        return;
+    }
+    const int chunk = (int)blockIdx.x - nb_scan;
+    const int t = threadIdx.x, nb = 1 << G.nbits;
+    for (int d = t; d < nb; d += kSplitThreads) s_h[d] = 0;
+    __syncthreads();
+    const GaussRows r = gauss_rows_nth(chunk * kSplitThreads + t, n, nth, tile_min, tile_max);
+    add_row_counts(G, r, nb, s_h);
+    __syncthreads();
+    for (int d = t; d < nb; d += kSplitThreads) hist[(int64_t)d * hstride + chunk] = s_h[d];
+}
+
+// Blocks [0, nb_scan): the scan's apply pass (cum = inclusive prefix sum, the
+// total to *total_out and *total_host); blocks nb_scan + d: digit d's prefix
+// over the chunks and its total, as k_digit_scan.
+__global__ __launch_bounds__(kSplitThreads) void k_apply_digits(
+    const int32_t *__restrict__ nth, int32_t *__restrict__ cum, int n, int nb_scan,
+    const int32_t *__restrict__ part, int64_t *__restrict__ total_out, int64_t *total_host,
+    int *__restrict__ hist, int nchunks, int hstride, int *__restrict__ totals) {
+    __shared__ int lds_waves[kSplitThreads / kWave];
+    __shared__ long long lds_pre[kSplitThreads / kWave];
+    if ((int)blockIdx.x < nb_scan) {  // uniform per block
+        scan_detail::apply_body(LoadI32{nth}, StoreI32{cum, 1}, (int64_t)n, part, 1, total_out,
+                                total_host, (int)blockIdx.x, nb_scan, lds_waves, lds_pre);
+        return;
+    }
+    const int d = (int)blockIdx.x - nb_scan;
+    digit_scan_row<kSplitThreads>(hist + (int64_t)d * hstride, nchunks, totals + d, lds_waves);
 }
 
 // Pass 2: the stable split of chunk c.  Each wave walks its 64 Gaussians'
@@ -1081,23 +1164,17 @@ int emit_and_sort(const BinLayout &L, int32_t n, int64_t cap, const int64_t *d_c
     return GSV_OK;
 }
 
-// The bucket path: box rows counted per chunk of Gaussians and top digit,
-// the prefix over chunks, the stable split of the rows into buckets of packed
-// words (in ka), then k_bucket_sort into (tiles_out, ids_out) and tile_bins.
-// Four launches; Bt sizes the top digit's LDS arrays (8 or 9 bits).
+// The bucket path's last two launches: the stable split of the box rows into
+// buckets of packed words (in ka), then k_bucket_sort into (tiles_out, ids_out)
+// and tile_bins.  hist holds the chunks' prefixes per digit, totals the digit
+// totals.
 template <int Bt>
-int rows_and_bucket_sort(const BinLayout &L, int32_t n, int64_t cap, const int32_t *tile_min,
-                         const int32_t *tile_max, const int32_t *cum, int *ka, int *hist,
-                         int *totals, int32_t *ids_out, int32_t *tiles_out, int32_t *tile_bins,
-                         hipStream_t s) {
+int split_and_bucket_sort(const BinLayout &L, int32_t n, int64_t cap, const int32_t *tile_min,
+                          const int32_t *tile_max, const int32_t *cum, int *ka, const int *hist,
+                          const int *totals, int32_t *ids_out, int32_t *tiles_out,
+                          int32_t *tile_bins, hipStream_t s) {
     const unsigned blocks = (unsigned)L.nchunks;
     unsigned *words = reinterpret_cast<unsigned *>(ka);
-    hipLaunchKernelGGL(k_bucket_hist<Bt>, dim3(blocks), dim3(kSplitThreads), 0, s, n, cap,
-                       tile_min, tile_max, cum, L.geom, hist, L.bstride);
-    if (int st = check_launch()) return st;
-    hipLaunchKernelGGL(k_digit_scan, dim3(1u << L.geom.nbits), dim3(kDigitScanThreads), 0, s,
-                       hist, L.nchunks, L.bstride, totals);
-    if (int st = check_launch()) return st;
     hipLaunchKernelGGL(k_bucket_split<Bt>, dim3(blocks), dim3(kSplitThreads), 0, s, n, cap,
                        tile_min, tile_max, cum, L.geom, hist, L.bstride, totals, words);
     if (int st = check_launch()) return st;
@@ -1111,6 +1188,26 @@ int rows_and_bucket_sort(const BinLayout &L, int32_t n, int64_t cap, const int32
                            words, tiles_out, ids_out, totals, L.geom, cap,
                            reinterpret_cast<int2 *>(tile_bins));
     return check_launch();
+}
+
+// The bucket path: box rows counted per chunk of Gaussians and top digit,
+// the prefix over chunks, the stable split of the rows into buckets of packed
+// words (in ka), then k_bucket_sort into (tiles_out, ids_out) and tile_bins.
+// Four launches; Bt sizes the top digit's LDS arrays (8 or 9 bits).
+template <int Bt>
+int rows_and_bucket_sort(const BinLayout &L, int32_t n, int64_t cap, const int32_t *tile_min,
+                         const int32_t *tile_max, const int32_t *cum, int *ka, int *hist,
+                         int *totals, int32_t *ids_out, int32_t *tiles_out, int32_t *tile_bins,
+                         hipStream_t s) {
+    const unsigned blocks = (unsigned)L.nchunks;
+    hipLaunchKernelGGL(k_bucket_hist<Bt>, dim3(blocks), dim3(kSplitThreads), 0, s, n, cap,
+                       tile_min, tile_max, cum, L.geom, hist, L.bstride);
+    if (int st = check_launch()) return st;
+    hipLaunchKernelGGL(k_digit_scan, dim3(1u << L.geom.nbits), dim3(kDigitScanThreads), 0, s,
+                       hist, L.nchunks, L.bstride, totals);
+    if (int st = check_launch()) return st;
+    return split_and_bucket_sort<Bt>(L, n, cap, tile_min, tile_max, cum, ka, hist, totals, ids_out,
+                                     tiles_out, tile_bins, s);
 }
 
 // tiles_out (optional, 16-byte aligned, cap entries): the sorted keys, i.e. the
@@ -1161,6 +1258,87 @@ int bin_and_sort(int32_t n, int64_t cap, const int64_t *d_count, const int32_t *
     hipLaunchKernelGGL(k_tile_edges, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                        keys_sorted, cap, d_count, T, reinterpret_cast<int2 *>(tile_bins));
     return check_launch();
+}
+
+// The prefix sum of num_tiles_hit (cum, *total_out, *total_host_dev) and the
+// binning with the count left on the device, in one call.  The workspace holds
+// the scan's block sums (align256(scan_workspace_bytes(n)) bytes) and then the
+// binning's.  On the bucket path with a direct scan (at most kDirectBlocks
+// blocks) the bucket counts and their prefix ride on the scan's launches
+// (k_sums_hist, k_apply_digits); otherwise the scan and bin_and_sort run one
+// after the other.
+size_t cumsum_scan_bytes(int64_t n) { return align256(scan_workspace_bytes(n)); }
+
+template <int Bt>
+int fused_bucket_path(const BinLayout &L, int32_t n, int64_t cap, const int32_t *nth,
+                      const int32_t *tile_min, const int32_t *tile_max, int32_t *cum,
+                      int64_t *total_out, int64_t *total_host_dev, int32_t *part, int *ka,
+                      int *hist, int *totals, int32_t *ids_out, int32_t *tile_bins,
+                      int32_t *tiles_out, hipStream_t s) {
+    const int nb_scan = (int)((n + scan_detail::kTile - 1) / scan_detail::kTile);
+    hipLaunchKernelGGL(k_sums_hist<Bt>, dim3((unsigned)(nb_scan + L.nchunks)), dim3(kSplitThreads),
+                       0, s, nth, n, nb_scan, part, tile_min, tile_max, L.geom, hist, L.bstride);
+    if (int st = check_launch()) return st;
+    hipLaunchKernelGGL(k_apply_digits, dim3((unsigned)(nb_scan + (1 << L.geom.nbits))),
+                       dim3(kSplitThreads), 0, s, nth, cum, n, nb_scan, part, total_out,
+                       total_host_dev, hist, L.nchunks, L.bstride, totals);
+    if (int st = check_launch()) return st;
+    return split_and_bucket_sort<Bt>(L, n, cap, tile_min, tile_max, cum, ka, hist, totals, ids_out,
+                                     tiles_out, tile_bins, s);
+}
+
+int cumsum_bin_and_sort(int32_t n, int64_t cap, const int32_t *nth, const int32_t *tile_min,
+                        const int32_t *tile_max, int32_t D, int32_t H, int32_t W, int32_t *cum,
+                        int64_t *total_out, int64_t *total_host_dev, void *workspace,
+                        size_t workspace_bytes, int32_t *ids_out, int32_t *tile_bins,
+                        int32_t *tiles_out, hipStream_t s) {
+    if (n < 0 || D <= 0 || H <= 0 || W <= 0 || !tile_bins || !total_out || !workspace)
+        return GSV_ERR_INVALID_ARGUMENT;
+    if (n > 0 && (!nth || !cum)) return GSV_ERR_INVALID_ARGUMENT;
+    if (cap > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
+    const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
+    if ((int64_t)Tx * Ty * Tz > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
+    const size_t scan_bytes = cumsum_scan_bytes(n);
+    if (workspace_bytes < scan_bytes) return GSV_ERR_WORKSPACE_TOO_SMALL;
+    char *bin_ws = static_cast<char *>(workspace) + scan_bytes;
+    const size_t bin_bytes = workspace_bytes - scan_bytes;
+    const int64_t nb_scan = ((int64_t)n + scan_detail::kTile - 1) / scan_detail::kTile;
+    bool fused = cap > 0 && n > 0 && nb_scan <= scan_detail::kDirectBlocks && tile_min &&
+                 tile_max && ids_out;
+    BinLayout L{};
+    if (fused) {
+        L = bin_layout(cap, Tx, Ty, Tz, n);
+        fused = L.bucket;
+    }
+    if (!fused) {
+        if (int st = scan_i32(nth, cum, n, true, total_out, total_host_dev, workspace, scan_bytes, s))
+            return st;
+        return bin_and_sort(n, cap, total_out, tile_min, tile_max, cum, D, H, W, bin_ws, bin_bytes,
+                            ids_out, tile_bins, tiles_out, s);
+    }
+    // bin_and_sort's checks for the bucket path
+    if ((reinterpret_cast<uintptr_t>(ids_out) & 15) != 0) return GSV_ERR_INVALID_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(tiles_out) & 15) != 0) return GSV_ERR_INVALID_ARGUMENT;
+    if (bin_bytes < L.total + 256) return GSV_ERR_WORKSPACE_TOO_SMALL;
+    char *ws = bin_ws + ((256 - (reinterpret_cast<uintptr_t>(bin_ws) & 255)) & 255);
+    int32_t *part = static_cast<int32_t *>(workspace);
+    int *ka = reinterpret_cast<int *>(ws + L.keys_a);
+    int *hist = reinterpret_cast<int *>(ws + L.hist);
+    int *totals = reinterpret_cast<int *>(ws + L.totals);
+    switch (L.geom.nbits) {
+        case 10:
+            return fused_bucket_path<10>(L, n, cap, nth, tile_min, tile_max, cum, total_out,
+                                         total_host_dev, part, ka, hist, totals, ids_out,
+                                         tile_bins, tiles_out, s);
+        case 9:
+            return fused_bucket_path<9>(L, n, cap, nth, tile_min, tile_max, cum, total_out,
+                                        total_host_dev, part, ka, hist, totals, ids_out, tile_bins,
+                                        tiles_out, s);
+        default:
+            return fused_bucket_path<8>(L, n, cap, nth, tile_min, tile_max, cum, total_out,
+                                        total_host_dev, part, ka, hist, totals, ids_out, tile_bins,
+                                        tiles_out, s);
+    }
 }
 
 // ---------------------------------------------------- allocation-free entry --
@@ -1247,6 +1425,27 @@ extern "C" int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity,
     return bin_and_sort(n, capacity, num_intersects_dev, tile_min, tile_max, cum_tiles_hit, D, H,
                         W, workspace, workspace_bytes, gaussian_ids_sorted, tile_bins,
                         tiles_sorted, as_stream(stream));
+}
+
+extern "C" int gsv_cumsum_bin_workspace_bytes(int32_t n, int64_t capacity, int32_t D, int32_t H,
+                                              int32_t W, size_t *bytes) {
+    if (!bytes) return GSV_ERR_INVALID_ARGUMENT;
+    size_t bin = 0;
+    if (int st = gsv_bin_workspace_bytes(n, capacity, D, H, W, &bin)) return st;
+    *bytes = cumsum_scan_bytes(n) + bin;
+    return GSV_OK;
+}
+
+extern "C" int gsv_cumsum_bin_and_sort_device_count(
+    int32_t n, int64_t capacity, const int32_t *num_tiles_hit, const int32_t *tile_min,
+    const int32_t *tile_max, int32_t D, int32_t H, int32_t W, int32_t *cum_tiles_hit,
+    int64_t *total_out, int64_t *total_host, void *workspace, size_t workspace_bytes,
+    int32_t *gaussian_ids_sorted, int32_t *tile_bins, int32_t *tiles_sorted, void *stream) {
+    int64_t *host_dev = nullptr;
+    if (int st = pinned_int64_device_ptr(total_host, &host_dev)) return st;
+    return cumsum_bin_and_sort(n, capacity, num_tiles_hit, tile_min, tile_max, D, H, W,
+                               cum_tiles_hit, total_out, host_dev, workspace, workspace_bytes,
+                               gaussian_ids_sorted, tile_bins, tiles_sorted, as_stream(stream));
 }
 
 extern "C" int gsv_bin_and_sort_noalloc(int32_t n, int64_t num_intersects,

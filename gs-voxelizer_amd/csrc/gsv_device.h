@@ -92,6 +92,10 @@ uint64_t *wave_timeline_buffer(int *capacity);
 // Zero-fills n 32-bit words with a kernel (graph-capture safe, unlike memset).
 int fill_zero_u32(void *ptr, int64_t n_words, hipStream_t stream);
 
+// The device address of a pinned (device-visible) host int64, or nullptr for
+// host == nullptr; GSV_ERR_INVALID_ARGUMENT for memory that is not pinned.
+int pinned_int64_device_ptr(int64_t *host, int64_t **dev);
+
 // Exclusive / inclusive int32 scan of a device array (scan.hip; the functor
 // form and scan_workspace_bytes are in gsv_scan.h).
 int scan_i32(const int32_t *in, int32_t *out, int64_t n, bool inclusive, int64_t *total_out,

@@ -50,17 +50,24 @@ __device__ __forceinline__ int block_exclusive(int v, int *lds_waves, int *total
     return off + inc - v;
 }
 
+// Block b's sum of ld(b * kTile .. (b + 1) * kTile) into part[b] (a workgroup
+// of kThreads; lds_waves holds kThreads / kWave ints).
 template <class Load>
-__global__ __launch_bounds__(kThreads) void k_block_sums(Load ld, int64_t n, int32_t *part) {
-    __shared__ int lds_waves[kThreads / kWave];
-    const int64_t base = (int64_t)blockIdx.x * kTile + (int64_t)threadIdx.x * kItems;
+__device__ __forceinline__ void block_sums_body(Load ld, int64_t n, int32_t *part, int b,
+                                                int *lds_waves) {
+    const int64_t base = (int64_t)b * kTile + (int64_t)threadIdx.x * kItems;
     int s = 0;
 #pragma unroll
     for (int k = 0; k < kItems; ++k)
         if (base + k < n) s += ld(base + k);
     int total;
     (void)block_exclusive(s, lds_waves, &total);
-    if (threadIdx.x == 0) part[blockIdx.x] = total;
+    if (threadIdx.x == 0) part[b] = total;
+}
+template <class Load>
+__global__ __launch_bounds__(kThreads) void k_block_sums(Load ld, int64_t n, int32_t *part) {
+    __shared__ int lds_waves[kThreads / kWave];
+    block_sums_body(ld, n, part, (int)blockIdx.x, lds_waves);
 }
 
 // Writes the total to the device int64 and, when given, to pinned host memory
@@ -141,13 +148,12 @@ __global__ __launch_bounds__(kSumsThreads) void k_scan_block_sums(int32_t *part,
 // st(i, exclusive prefix of element i, element i) for every i < n.  direct:
 // part holds raw block sums and each block adds its predecessors' (the last
 // block then writes the total); otherwise part is already scanned.
+// Block b of nblocks (a workgroup of kThreads; LDS as k_apply declares it).
 template <class Load, class Store>
-__global__ __launch_bounds__(kThreads) void k_apply(Load ld, Store st, int64_t n,
-                                                    const int32_t *part, int direct,
-                                                    int64_t *total_out, int64_t *total_host) {
-    __shared__ int lds_waves[kThreads / kWave];
-    __shared__ long long lds_pre[kThreads / kWave];
-    const int b = blockIdx.x;
+__device__ __forceinline__ void apply_body(Load ld, Store st, int64_t n, const int32_t *part,
+                                           int direct, int64_t *total_out, int64_t *total_host,
+                                           int b, int nblocks, int *lds_waves,
+                                           long long *lds_pre) {
     long long prefix;
     if (direct) {
         long long s = 0;
@@ -177,8 +183,17 @@ __global__ __launch_bounds__(kThreads) void k_apply(Load ld, Store st, int64_t n
         if (base + k < n) st(base + k, run, v[k]);
         run += v[k];
     }
-    if (direct && b == (int)gridDim.x - 1 && threadIdx.x == 0)
+    if (direct && b == nblocks - 1 && threadIdx.x == 0)
         put_total(prefix + total, total_out, total_host);
+}
+template <class Load, class Store>
+__global__ __launch_bounds__(kThreads) void k_apply(Load ld, Store st, int64_t n,
+                                                    const int32_t *part, int direct,
+                                                    int64_t *total_out, int64_t *total_host) {
+    __shared__ int lds_waves[kThreads / kWave];
+    __shared__ long long lds_pre[kThreads / kWave];
+    apply_body(ld, st, n, part, direct, total_out, total_host, (int)blockIdx.x, (int)gridDim.x,
+               lds_waves, lds_pre);
 }
 
 }  // namespace scan_detail

@@ -102,6 +102,20 @@ int fill_zero_u32(void *ptr, int64_t n_words, hipStream_t stream) {
     return check_launch();
 }
 
+int pinned_int64_device_ptr(int64_t *host, int64_t **dev) {
+    *dev = nullptr;
+    if (!host) return GSV_OK;
+    void *p = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&p, host, 0);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();  // leave no error behind for the next launch check
+        (void)record_hip_error(e);
+        return GSV_ERR_INVALID_ARGUMENT;  // not pinned, device-visible host memory
+    }
+    *dev = static_cast<int64_t *>(p);
+    return GSV_OK;
+}
+
 int scan_i32(const int32_t *in, int32_t *out, int64_t n, bool inclusive, int64_t *total_out,
              int64_t *total_host, void *ws, size_t ws_bytes, hipStream_t stream) {
     if (n > 0 && (!in || !out)) return GSV_ERR_INVALID_ARGUMENT;
@@ -189,16 +203,7 @@ extern "C" int gsv_cumsum_tiles_hit(int32_t n, const int32_t *num_tiles_hit,
     if (n < 0) return GSV_ERR_INVALID_ARGUMENT;
     if (n > 0 && (!num_tiles_hit || !cum_tiles_hit)) return GSV_ERR_INVALID_ARGUMENT;
     int64_t *host_dev = nullptr;  // the kernels' address of the pinned host int64
-    if (total_host) {
-        void *p = nullptr;
-        const hipError_t e = hipHostGetDevicePointer(&p, total_host, 0);
-        if (e != hipSuccess) {
-            (void)hipGetLastError();  // leave no error behind for the next launch check
-            (void)record_hip_error(e);
-            return GSV_ERR_INVALID_ARGUMENT;  // not pinned, device-visible host memory
-        }
-        host_dev = static_cast<int64_t *>(p);
-    }
+    if (int st = pinned_int64_device_ptr(total_host, &host_dev)) return st;
     return scan_i32(num_tiles_hit, cum_tiles_hit, n, true, total_out, host_dev, workspace,
                     workspace_bytes, as_stream(stream));
 }

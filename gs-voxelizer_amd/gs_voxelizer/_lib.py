@@ -32,6 +32,10 @@ SIGNATURES = {
                          _P, _P, _P, _P],
     "gsv_bin_and_sort_device_count": [_c_int, _c_i64, _P, _P, _P, _P, _c_int, _c_int, _c_int, _P,
                                       _c_size_t, _P, _P, _P, _P],
+    "gsv_cumsum_bin_workspace_bytes": [_c_int, _c_i64, _c_int, _c_int, _c_int,
+                                       ctypes.POINTER(_c_size_t)],
+    "gsv_cumsum_bin_and_sort_device_count": [_c_int, _c_i64, _P, _P, _P, _c_int, _c_int, _c_int,
+                                             _P, _P, _P, _P, _c_size_t, _P, _P, _P, _P],
     "gsv_bin_and_sort_noalloc": [_c_int, _c_i64, _P, _P, _P, _c_int, _c_int, _c_int, _P, _P, _P,
                                  _P],
     "gsv_voxelize_fwd": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P, _P,

@@ -234,6 +234,48 @@ def bin_and_sort_gaussians_device_count(num_gaussians: int, capacity: int, num_i
     return (ids, tile_bins, tiles) if return_tiles else (ids, tile_bins)
 
 
+def cumsum_bin_and_sort_device_count(num_gaussians: int, capacity: int, num_tiles_hit, tile_min,
+                                     tile_max, vol_size, total_host=None,
+                                     return_tiles: bool = False):
+    """cumsum_tiles_hit followed by bin_and_sort_gaussians_device_count, in
+    one native call (voxelize.py:87-88 and the binning, without the host read
+    of the count).  Returns (cum_tiles_hit, total, gaussian_ids_sorted
+    (capacity,), tile_bins (T,2)) and, with return_tiles, the tile of each
+    sorted pair (capacity,); total_host as for cumsum_tiles_hit.  The binning
+    is complete only when total <= capacity, which the caller checks."""
+    for t, w in ((num_tiles_hit, "num_tiles_hit"), (tile_min, "tile_min"),
+                 (tile_max, "tile_max")):
+        _check_input(t, w)
+        _check_dtype(t, w, torch.int32)
+    if total_host is not None:
+        if (total_host.is_cuda or not total_host.is_pinned() or total_host.dtype != torch.int64
+                or total_host.numel() != 1):
+            raise RuntimeError("total_host must be a pinned (1,) int64 CPU tensor")
+    Tx, Ty, Tz = _tiles(vol_size)
+    D, H, W = (int(v) for v in vol_size)
+    dev = tile_min.device
+    n, cap = int(num_gaussians), max(int(capacity), 0)
+    _check_rows(n, ((tile_min, "tile_min", 3), (tile_max, "tile_max", 3),
+                    (num_tiles_hit, "num_tiles_hit", 1)))
+    i32 = dict(device=dev, dtype=torch.int32)
+    cum = torch.empty((n,), **i32)
+    total = torch.empty((1,), device=dev, dtype=torch.int64)
+    tile_bins = torch.empty((Tx * Ty * Tz, 2), **i32)
+    ids = torch.empty((cap,), **i32)
+    tiles = torch.empty((cap,), **i32) if return_tiles else None
+    nbytes = ctypes.c_size_t(0)
+    _call("cumsum_bin_workspace_bytes", n, cap, D, H, W, ctypes.byref(nbytes))
+    ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        _call("cumsum_bin_and_sort_device_count", n, cap, _ptr(num_tiles_hit), _ptr(tile_min),
+              _ptr(tile_max), D, H, W, _ptr(cum), _ptr(total),
+              _ptr(total_host) if total_host is not None else ctypes.c_void_p(0), _ptr(ws),
+              nbytes.value, _ptr(ids), _ptr(tile_bins),
+              _ptr(tiles) if tiles is not None else ctypes.c_void_p(0), _stream(dev))
+    out = (cum, total, ids, tile_bins)
+    return out + (tiles,) if return_tiles else out
+
+
 def _voxelize_inputs(gaussian_ids_sorted, tile_bins, pos3d, conics, intensities):
     for t, w in ((gaussian_ids_sorted, "gaussian_ids_sorted"), (tile_bins, "tile_bins"),
                  (pos3d, "pos3d"), (conics, "conics"), (intensities, "intensities")):

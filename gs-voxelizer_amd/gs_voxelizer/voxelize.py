@@ -162,10 +162,9 @@ def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tile
                 "(it checks every replay's intersection count), at most 16 forwards a step")
         host = free.pop()
         _capture.counts.append((host, cap))
-        cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous(), total_host=host)
-        ids_cap, tile_bins, tiles_cap = _C.bin_and_sort_gaussians_device_count(
-            num_gaussians, cap, total, tile_min, tile_max, cum_tiles_hit, vol_size_voxel,
-            return_tiles=True)
+        cum_tiles_hit, total, ids_cap, tile_bins, tiles_cap = _C.cumsum_bin_and_sort_device_count(
+            num_gaussians, cap, num_tiles_hit.contiguous(), tile_min, tile_max, vol_size_voxel,
+            total_host=host, return_tiles=True)
         return (cap, ids_cap, tile_bins, tiles_cap, cum_tiles_hit, fwd(ids_cap, tile_bins),
                 total)
     if cap is not None:
@@ -173,10 +172,11 @@ def _bin_and_forward(num_gaussians, vol_size_voxel, tile_min, tile_max, num_tile
         # memory meanwhile
         host = _count_slot(dev)
         host.fill_(-1)
-        cum_tiles_hit, total = _C.cumsum_tiles_hit(num_tiles_hit.contiguous(), total_host=host)
-        ids_cap, tile_bins, tiles_cap = _C.bin_and_sort_gaussians_device_count(
-            num_gaussians, cap, total, tile_min, tile_max, cum_tiles_hit, vol_size_voxel,
-            return_tiles=True)
+        # the prefix sum and the binning in one native call (four launches on
+        # the bucket path); the scan writes the count into pinned memory
+        cum_tiles_hit, total, ids_cap, tile_bins, tiles_cap = _C.cumsum_bin_and_sort_device_count(
+            num_gaussians, cap, num_tiles_hit.contiguous(), tile_min, tile_max, vol_size_voxel,
+            total_host=host, return_tiles=True)
         result = fwd(ids_cap, tile_bins)
         num_intersects = _await_count(host, dev)
         if num_intersects <= cap:

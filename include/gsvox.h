@@ -143,6 +143,30 @@ int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity, const int64_t *nu
                                   int32_t *tiles_sorted, void *stream);
 
 /*
+ * Prefix sum and binning in one call, with the pair count left on the device.
+ * Replaces voxelize.py:87-88 and bin_and_sort_gaussians_torch
+ * (bindings.cu:259-360): the same work and outputs as gsv_cumsum_tiles_hit
+ * (cum_tiles_hit, *total_out, *total_host as described there) followed by
+ * gsv_bin_and_sort_device_count with num_intersects_dev = total_out.
+ * total_out is required.  Workspace size from gsv_cumsum_bin_workspace_bytes
+ * (n, capacity, D, H, W).  Where the binning takes the bucket method with a
+ * single-pass scan of its block sums (n up to 4,194,304), the bucket counts
+ * are formed beside the scan's block sums and their prefix beside the scan's
+ * apply pass: four kernel launches instead of six, the same results.  When
+ * *total_out > capacity the binning's output is incomplete, as for
+ * gsv_bin_and_sort_device_count.
+ */
+int gsv_cumsum_bin_workspace_bytes(int32_t n, int64_t capacity, int32_t D, int32_t H, int32_t W,
+                                   size_t *bytes);
+int gsv_cumsum_bin_and_sort_device_count(int32_t n, int64_t capacity,
+                                         const int32_t *num_tiles_hit, const int32_t *tile_min,
+                                         const int32_t *tile_max, int32_t D, int32_t H, int32_t W,
+                                         int32_t *cum_tiles_hit, int64_t *total_out,
+                                         int64_t *total_host, void *workspace,
+                                         size_t workspace_bytes, int32_t *gaussian_ids_sorted,
+                                         int32_t *tile_bins, int32_t *tiles_sorted, void *stream);
+
+/*
  * Binning that allocates nothing.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory when they bin (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same

@@ -164,3 +164,61 @@ def test_binning_long_runs_of_empty_gaussians(device, binning_path):
     I2, ids2, bins2 = _device_count_bin(device, n, tmin, tmax, nt, vol, rI)
     np.testing.assert_array_equal(bins2, rbins)
     np.testing.assert_array_equal(ids2, rids)
+
+
+def _fused_bin(device, n, tmin, tmax, nt, vol, capacity):
+    import gs_voxelizer.cuda as _C
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    host = torch.full((1,), -1, dtype=torch.int64).pin_memory()
+    cum, total, ids, bins, tiles = _C.cumsum_bin_and_sort_device_count(
+        n, capacity, t(nt), t(tmin), t(tmax), vol, total_host=host, return_tiles=True)
+    torch.cuda.synchronize()
+    assert int(host.item()) == int(total.item())
+    return np32(cum), int(total.item()), np32(ids), np32(bins), np32(tiles)
+
+
+@pytest.mark.parametrize("name,work", [c for c in _bin_cases() if c[0] in
+                                       ("cfg1", "cfg2_full", "cfg3_full", "one_tile", "few_tiles",
+                                        "bits17", "bits18", "clustered_heavy", "wide_x", "tall_z",
+                                        "wider_x")],
+                         ids=lambda v: v if isinstance(v, str) else "")
+def test_fused_cumsum_binning_matches_oracle(device, binning_path, name, work):
+    """gsv_cumsum_bin_and_sort_device_count (the bucket counts and their prefix
+    formed beside the scan's two passes) gives the oracle's prefix sum, count,
+    ids, bins and sorted tiles bit for bit, on both sort paths."""
+    cfg = work.cfg
+    n = work.pos3d.shape[0]
+    _, _, rtmin, rtmax, rnt = oracle_project(work)
+    rcum = O.cumsum(rnt)
+    rI = int(rcum[-1])
+    rids, rbins = O.bin_and_sort(n, rI, rtmin, rtmax, rcum, cfg.vol)
+    rtiles = np.repeat(np.arange(rbins.shape[0]), rbins[:, 1] - rbins[:, 0])
+    cum, I, ids, bins, tiles = _fused_bin(device, n, rtmin, rtmax, rnt, cfg.vol, rI + 3000)
+    assert I == rI, (name, I, rI)
+    np.testing.assert_array_equal(cum, rcum, err_msg=f"{name}: cum_tiles_hit")
+    np.testing.assert_array_equal(bins, rbins, err_msg=f"{name}: tile_bins")
+    np.testing.assert_array_equal(ids[:rI], rids, err_msg=f"{name}: gaussian_ids_sorted")
+    np.testing.assert_array_equal(tiles[:rI], rtiles, err_msg=f"{name}: tiles_sorted")
+
+
+def test_fused_cumsum_binning_empty_and_over_capacity(device, binning_path):
+    """No Gaussians: a zero count and zeroed bins.  Capacity below the count:
+    the call returns, reports the full count, and a second call at that count
+    bins exactly (what voxelize.py does)."""
+    cum, I, ids, bins, tiles = _fused_bin(device, 0, np.zeros((0, 3), np.int32),
+                                          np.zeros((0, 3), np.int32), np.zeros(0, np.int32),
+                                          (16, 16, 24), 100)
+    assert I == 0 and cum.size == 0 and int(np.abs(bins).sum()) == 0
+    work = S.make_gaussians(small_config(1, 3000, vol=(40, 48, 56)), seed=3)
+    cfg = work.cfg
+    n = work.pos3d.shape[0]
+    _, _, rtmin, rtmax, rnt = oracle_project(work)
+    rcum = O.cumsum(rnt)
+    rI = int(rcum[-1])
+    rids, rbins = O.bin_and_sort(n, rI, rtmin, rtmax, rcum, cfg.vol)
+    cum, I, ids, bins, _ = _fused_bin(device, n, rtmin, rtmax, rnt, cfg.vol, rI // 2 + 17)
+    assert I == rI and ids.shape == (rI // 2 + 17,)
+    np.testing.assert_array_equal(cum, rcum)
+    cum, I, ids, bins, _ = _fused_bin(device, n, rtmin, rtmax, rnt, cfg.vol, rI)
+    np.testing.assert_array_equal(bins, rbins)
+    np.testing.assert_array_equal(ids, rids)
