@@ -249,3 +249,58 @@ def test_backward_power_of_two_gradient_scaling_is_exact(device, e):
     for x, y in zip(base, scaled):
         assert torch.equal(torch.ldexp(x, torch.tensor(float(e))), y)
     assert float(base[2].abs().sum()) > 0
+
+
+# A tilted needle (one long axis near x, two of ~0.15 voxel) whose rows inside
+# its gate ellipse admit the backward's chained rows (3M + 2 = 76 <= K = 95),
+# while on rows of its tile away from the ellipse the x-slope reaches
+# m_tile = 145: there 2^-S1 overflows binary32.  Found with the CPU restatement
+# of the chains in test_chain_cpu.py (needle scene, seed 9, pair 2300):
+# centre offset from the tile centre, conic (00, 01, 02, 11, 12, 22), and
+# t2 = log2(1e-6 / I).
+_NEEDLE = np.array([3.490655, 1.9826925, -3.301888, 2.745941, 9.987584, -5.312871, 52.159576,
+                    -15.002705, 25.211243, -14.04277], np.float32)
+
+
+def test_backward_chain_guard_on_needle_in_a_chained_wave(device):
+    """One tile, one backward wave: 63 round Gaussians that take the chained
+    rows and the needle above.  Without chain_shift's m_tile < 120 condition
+    the wave would take the chains and the needle's dead rows would turn into
+    inf / NaN; with it the wave takes the exact path, and every gradient
+    matches the oracle."""
+    import gs_voxelizer.cuda as _C
+    from test_chain_cpu import _backward_chains
+    P = _NEEDLE.astype(np.float64)[None, :]
+    _, qualifies, excluded = _backward_chains(P)
+    assert excluded[0] and not qualifies[0]  # the span rule alone would take it
+    rng = np.random.default_rng(1)
+    n, vol, centre = 64, (24, 24, 24), np.float32(12.0)  # tile (1, 1, 1): voxels 8..15
+    pr = np.zeros((n, 4), np.float32)
+    cn = np.zeros((n, 6), np.float32)
+    inten = np.full((n, 1), 0.5, np.float32)
+    sig = rng.uniform(1.0, 2.0, n - 1)
+    pr[:-1, :3] = centre + rng.uniform(-3, 3, (n - 1, 3))
+    pr[:, 3] = 3.0
+    cn[:-1, 0] = cn[:-1, 3] = cn[:-1, 5] = 1.0 / sig ** 2
+    pr[-1, :3] = centre + _NEEDLE[:3]
+    cn[-1] = _NEEDLE[3:9]
+    inten[-1, 0] = np.float32(2.0 ** (np.log2(1e-6) - float(_NEEDLE[9])))
+    tmin = np.ones((n, 3), np.int32)
+    tmax = np.full((n, 3), 2, np.int32)
+    nt = np.ones(n, np.int32)
+    cum = O.cumsum(nt)
+    rids, rbins = O.bin_and_sort(n, n, tmin, tmax, cum, vol)
+    g = rng.standard_normal(vol + (1,)).astype(np.float32)
+    ref, absum, amb = O.voxelize_bwd(vol, rids, rbins, pr, cn, inten, g, diagnostics=True)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    ids, bins = _C.bin_and_sort_gaussians(n, n, t(tmin), t(tmax), t(cum), vol)
+    for mode in MODES:
+        extra = (t(tmin), t(tmax), t(cum)) if mode == "pairs" else ()
+        got = _C.voxelize_backward_per_gaussian(vol, ids, bins, t(pr), t(cn), t(inten), t(g),
+                                                *extra)
+        torch.cuda.synchronize()
+        for nm, a, b, s, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, ref, absum,
+                                  amb):
+            a = np32(a)
+            assert np.isfinite(a).all(), f"needle {mode}: {nm} not finite"
+            report_close(f"needle guard {mode}: {nm}", a, b, RTOL, ATOL, bound=1e-5 * s + m)
