@@ -1105,20 +1105,36 @@ template <int C>
 __device__ __forceinline__ float chain_shift(const BwdLane<C> &L, float A2, float Bn, float Cn) {
     const float m_tile = fabsf(fmaf(2.0f * A2, L.mxl, fmaf(Bn, L.myl, Cn * L.mzl))) +
                          3.5f * (fabsf(Bn) + fabsf(Cn));
-    const double a = L.ca, b = L.cb, c = L.cc, d = L.cd, e = L.ce, f = L.cf;
-    const double syy = a * f - c * c, szz = a * d - b * b, syz = b * c - a * e;
-    const double det = a * (d * f - e * e) - b * (b * f - c * e) + c * (b * e - c * d);
-    const double gb = Bn, gc = Cn;
-    const double q = (gb * gb * syy + 2.0 * gb * gc * syz + gc * gc * szz) / det;
-    const double k2 = -2.0 * (double)kLn2 * (double)L.gt.t2;
-    const float m_ell = (float)(fabs(2.0 * (double)A2 * (double)L.mxl) + sqrt(fmax(k2 * q, 0.0)));
-    const float m_reach = (float)(fabs(2.0 * (double)A2) * (3.5 + sqrt(fmax(k2 / a, 0.0))));
-    const float M = fminf(m_tile, fminf(m_ell, m_reach)) * 1.001f + 0.01f;
     const float K = floorf(120.0f - 12.25f * fabsf(A2));
     // Rows outside the gate ellipse are bounded by m_tile alone: below 120 every
     // row's step 2^-S1 (and 2^Bn, the ratio of neighbouring rows' steps) is a
     // finite normal number, so no product of a dead row is inf * 0.
-    return ceilf(3.0f * M) + 2.0f <= K && m_tile < 120.0f ? K : -1.0f;
+    if (!(m_tile < 120.0f)) return -1.0f;
+    const float k2 = -2.0f * kLn2 * L.gt.t2;
+    const float m_reach = fabsf(2.0f * A2) *
+                          (3.5f + __builtin_amdgcn_sqrtf(fmaxf(k2 * __builtin_amdgcn_rcpf(L.ca), 0.f)));
+    // sqrt(k2 g^T S g) = sqrt(k2 w^T Q^-1 w), w = (0, Bn, Cn), from the Cholesky
+    // factor Q = L L^T in binary32: w^T Q^-1 w = y2^2 + y3^2 with y = L^-1 w.
+    // With both pivots above 1e-3 of their diagonal (condition number below
+    // ~1e3) the relative error stays near 1e-4, inside the margins below; a
+    // worse-conditioned conic leaves this bound out (M only grows).
+    float m_ell = __builtin_inff();
+    const float i11 = __builtin_amdgcn_rsqf(L.ca);
+    const float l21 = L.cb * i11, l31 = L.cc * i11;
+    const float t22 = fmaf(-l21, l21, L.cd);
+    if (t22 > 1e-3f * L.cd) {
+        const float i22 = __builtin_amdgcn_rsqf(t22);
+        const float l32 = fmaf(-l31, l21, L.ce) * i22;
+        const float t33 = fmaf(-l32, l32, fmaf(-l31, l31, L.cf));
+        if (t33 > 1e-3f * L.cf) {
+            const float y2 = Bn * i22;
+            const float y3 = fmaf(-l32, y2, Cn) * __builtin_amdgcn_rsqf(t33);
+            m_ell = fabsf(2.0f * A2 * L.mxl) +
+                    __builtin_amdgcn_sqrtf(fmaxf(k2 * fmaf(y2, y2, y3 * y3), 0.f));
+        }
+    }
+    const float M = fminf(m_tile, fminf(m_ell, m_reach)) * 1.001f + 0.01f;
+    return ceilf(3.0f * M) + 2.0f <= K ? K : -1.0f;
 }
 
 // Exponent e such that m * 2^e lies in [2^(kGradScaleExp-1), 2^kGradScaleExp);
@@ -1294,26 +1310,36 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
         __syncthreads();  // a later group restages the slots
     }
     if (!mine) return;
-    // sigma-gradient weight per unit of h (alpha = scale * a); binary64 keeps the
-    // 2^-gexp and 2^-off factors in range
-    double wscale = 0.0;
-    if (L.live) wscale = wave_fast ? ldexp((double)L.gt.fscale, -gexp) : (double)L.gt.scale;
-    const double w = (C == 1) ? wscale * (double)L.I[0] : wscale;
+    // sigma-gradient weight per unit of h (alpha = scale * a) as ws * 2^we: the
+    // 2^-gexp and 2^-off factors stay in the exponent, so each product below is
+    // a binary32 number in range (gate-free: ws < 1, I < 2^54, moments < 2^45),
+    // and ldexpf applies them exactly
+    float ws = 0.f;
+    int we = 0;
+    if (L.live) {
+        if (wave_fast) {
+            ws = frexpf(L.gt.fscale, &we);
+            we -= gexp;
+        } else {
+            ws = L.gt.scale;
+        }
+    }
+    const float w = (C == 1) ? ws * L.I[0] : ws;
     float out[9 + C];
-    out[0] = (float)(-0.5 * w * (double)M.Sxx);
-    out[1] = (float)(-w * (double)M.Sxy);
-    out[2] = (float)(-w * (double)M.Sxz);
-    out[3] = (float)(-0.5 * w * (double)M.Syy);
-    out[4] = (float)(-w * (double)M.Syz);
-    out[5] = (float)(-0.5 * w * (double)M.Szz);
-    out[6] = (float)(-w * ((double)L.ca * M.Sx + (double)L.cb * M.Sy + (double)L.cc * M.Sz));
-    out[7] = (float)(-w * ((double)L.cb * M.Sx + (double)L.cd * M.Sy + (double)L.ce * M.Sz));
-    out[8] = (float)(-w * ((double)L.cc * M.Sx + (double)L.ce * M.Sy + (double)L.cf * M.Sz));
+    out[0] = ldexpf(-w * M.Sxx, we - 1);
+    out[1] = ldexpf(-w * M.Sxy, we);
+    out[2] = ldexpf(-w * M.Sxz, we);
+    out[3] = ldexpf(-w * M.Syy, we - 1);
+    out[4] = ldexpf(-w * M.Syz, we);
+    out[5] = ldexpf(-w * M.Szz, we - 1);
+    out[6] = ldexpf(-w * fmaf(L.ca, M.Sx, fmaf(L.cb, M.Sy, L.cc * M.Sz)), we);
+    out[7] = ldexpf(-w * fmaf(L.cb, M.Sx, fmaf(L.cd, M.Sy, L.ce * M.Sz)), we);
+    out[8] = ldexpf(-w * fmaf(L.cc, M.Sx, fmaf(L.ce, M.Sy, L.cf * M.Sz)), we);
     if (C == 1) {
-        out[9] = (float)(wscale * (double)M.S0);
+        out[9] = ldexpf(ws * M.S0, we);
     } else {
 #pragma unroll
-        for (int c = 0; c < C; ++c) out[9 + c] = (float)(wscale * (double)M.dI[c]);
+        for (int c = 0; c < C; ++c) out[9 + c] = ldexpf(ws * M.dI[c], we);
     }
     const int g = L.g;
     if (a.partial != nullptr) {

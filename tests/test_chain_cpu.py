@@ -172,16 +172,26 @@ def _backward_chains(P):
     A2 = F32(-0.5 * L2E) * ca
     Bn, Cn = F32(-L2E) * cb, F32(-L2E) * cc_
     Dn, En, Fn = F32(-0.5 * L2E) * cd, F32(-L2E) * ce, F32(-0.5 * L2E) * cf
-    # chain_shift
+    # chain_shift (binary32): the tile bound, the gate interval's reach, and the
+    # slope bound over the gate ellipse from a Cholesky factor of the conic,
+    # left out when a pivot falls below 1e-3 of its diagonal
     m_tile = np.abs(2 * A2 * mx + Bn * my + Cn * mz) + F32(3.5) * (np.abs(Bn) + np.abs(Cn))
-    a, b, c, d, e, f = (v.astype(np.float64) for v in (ca, cb, cc_, cd, ce, cf))
-    syy, szz, syz = a * f - c * c, a * d - b * b, b * c - a * e
-    det = a * (d * f - e * e) - b * (b * f - c * e) + c * (b * e - c * d)
-    gb, gc = Bn.astype(np.float64), Cn.astype(np.float64)
-    q = (gb * gb * syy + 2 * gb * gc * syz + gc * gc * szz) / det
-    k2 = -2.0 * 0.693147180559945309 * t2.astype(np.float64)
-    m_ell = (np.abs(2.0 * A2.astype(np.float64) * mx) + np.sqrt(np.maximum(k2 * q, 0))).astype(np.float32)
-    m_reach = (np.abs(2.0 * A2.astype(np.float64)) * (3.5 + np.sqrt(np.maximum(k2 / a, 0)))).astype(np.float32)
+    k2 = (F32(-2.0 * 0.693147180559945309) * t2).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        m_reach = (np.abs(F32(2) * A2) * (F32(3.5) + np.sqrt(np.maximum(k2 / ca, F32(0))))
+                   ).astype(np.float32)
+        i11 = (F32(1) / np.sqrt(ca)).astype(np.float32)
+        l21, l31 = cb * i11, cc_ * i11
+        t22 = (cd - l21 * l21).astype(np.float32)
+        i22 = (F32(1) / np.sqrt(t22)).astype(np.float32)
+        l32 = ((ce - l31 * l21) * i22).astype(np.float32)
+        t33 = (cf - l31 * l31 - l32 * l32).astype(np.float32)
+        y2 = Bn * i22
+        y3 = ((Cn - l32 * y2) / np.sqrt(t33)).astype(np.float32)
+        ell = (np.abs(F32(2) * A2 * mx) + np.sqrt(np.maximum(k2 * (y2 * y2 + y3 * y3), F32(0)))
+               ).astype(np.float32)
+    ok = (t22 > F32(1e-3) * cd) & (t33 > F32(1e-3) * cf)
+    m_ell = np.where(ok, ell, np.float32(np.inf)).astype(np.float32)
     M = np.minimum(m_tile, np.minimum(m_ell, m_reach)) * F32(1.001) + F32(0.01)
     K = np.floor(F32(120.0) - F32(12.25) * np.abs(A2))
     span_ok = np.ceil(F32(3.0) * M) + 2 <= K
@@ -305,3 +315,37 @@ def test_backward_chain_bounds_dead_rows():
     # chains and some of their products would overflow
     assert excluded.sum() > 0.01 * len(P), int(excluded.sum())
     assert not np.isfinite(bwd[excluded]).all()
+
+
+def test_backward_ellipse_bound_in_binary32():
+    """chain_shift's slope bound over the gate ellipse, sqrt(k2 w^T Q^-1 w) with
+    w = (0, Bn, Cn), from a binary32 Cholesky factor of the conic: wherever both
+    pivots stay above 1e-3 of their diagonal it agrees with the binary64
+    cofactor formula to 2e-4 relative (the kernel's margin is 1e-3 + 0.01), on
+    random rotated conics, narrow ones and tilted needles."""
+    P = np.concatenate([_random_pairs(12000, seed=15), _needle_pairs(6000, seed=16)])
+    F = np.float32
+    ca, cb, cc_, cd, ce, cf = (P[:, 3 + i].astype(F) for i in range(6))
+    t2 = P[:, 9].astype(F)
+    Bn, Cn = F(-L2E) * cb, F(-L2E) * cc_
+    k2 = (F(-2.0 * 0.693147180559945309) * t2).astype(F)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        i11 = (F(1) / np.sqrt(ca)).astype(F)
+        l21, l31 = cb * i11, cc_ * i11
+        t22 = (cd - l21 * l21).astype(F)
+        i22 = (F(1) / np.sqrt(t22)).astype(F)
+        l32 = ((ce - l31 * l21) * i22).astype(F)
+        t33 = (cf - l31 * l31 - l32 * l32).astype(F)
+        y2 = Bn * i22
+        y3 = ((Cn - l32 * y2) / np.sqrt(t33)).astype(F)
+        got = np.sqrt(np.maximum(k2 * (y2 * y2 + y3 * y3), F(0))).astype(np.float64)
+    ok = (t22 > F(1e-3) * cd) & (t33 > F(1e-3) * cf)
+    a, b, c, d, e, f = (v.astype(np.float64) for v in (ca, cb, cc_, cd, ce, cf))
+    syy, szz, syz = a * f - c * c, a * d - b * b, b * c - a * e
+    det = a * (d * f - e * e) - b * (b * f - c * e) + c * (b * e - c * d)
+    gb, gc = Bn.astype(np.float64), Cn.astype(np.float64)
+    ref = np.sqrt(np.maximum(k2.astype(np.float64) *
+                             (gb * gb * syy + 2 * gb * gc * syz + gc * gc * szz) / det, 0))
+    assert ok.mean() > 0.9, ok.mean()
+    rel = np.abs(got[ok] - ref[ok]) / np.maximum(ref[ok], 1e-30)
+    assert rel.max() <= 2e-4, rel.max()
