@@ -72,7 +72,7 @@ constexpr float kExpFlush = 126.0f;     // v_exp_f32 results below 2^-126 are 0
 // two-operand v_add_f32 instead of a three-operand FMA against the weight; the
 // other paths scale their weights alike, and the epilogue multiplies once.
 constexpr float kAccUnit = 1e-6f * 0x1p126f;
-constexpr double kInvAccUnit = 1.0 / (double)kAccUnit;
+constexpr float kInvAccUnit = (float)(1.0 / (double)kAccUnit);  // rounded once: ~1e-7 overall
 constexpr float kDeadOffset = -1000.0f;  // exponent offset that zeroes a lane
 
 struct Gate {
@@ -357,17 +357,16 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(C == 1 ? 
                         rec[5] = (float)(tz - at * (double)rec[2]);
                         // C = 1: the weight I * 2^-off in units of kAccUnit, ~1 (see
                         // kAccUnit); the chains carry it in their factors
-                        const double rho = C == 1 ? (double)I[0] * (double)gt.fscale * kInvAccUnit : 1.0;
+                        const float rho = C == 1 ? (I[0] * gt.fscale) * kInvAccUnit : 1.f;
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const float uc = 0.5f + (float)k;
                             // 2^-K applied exactly: the exp2 argument stays small
                             const float Gk = ldexpf(__builtin_amdgcn_exp2f(A2 * (uc * uc)), -(int)K);
-                            rec[9 + k] = chain ? (C == 1 ? (float)((double)Gk * rho) : Gk)
-                                               : fmaf(A2, uc * uc, gt.off);
+                            rec[9 + k] = chain ? Gk * rho : fmaf(A2, uc * uc, gt.off);
                         }
 #pragma unroll
-                        for (int c = 0; c < C; ++c) rec[13 + c] = C == 1 ? (float)rho : I[c] * gt.fscale;
+                        for (int c = 0; c < C; ++c) rec[13 + c] = C == 1 ? rho : I[c] * gt.fscale;
                     } else {
                         // (cx, cy, cz, A2 | B, C, D, E | F, shift, half, A2 cx | I*2^shift)
                         rec[0] = cx; rec[1] = cy; rec[2] = cz; rec[3] = A2;
@@ -375,8 +374,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(C == 1 ? 
                         rec[8] = F; rec[9] = gt.shift; rec[10] = gt.half; rec[11] = A2 * cx;
 #pragma unroll
                         for (int c = 0; c < C; ++c)
-                            rec[12 + c] = C == 1 ? (float)((double)I[0] * (double)gt.scale * kInvAccUnit)
-                                                 : I[c] * gt.scale;
+                            rec[12 + c] = C == 1 ? (I[0] * gt.scale) * kInvAccUnit : I[c] * gt.scale;
                     }
 #pragma unroll
                     for (int q = 0; q < kRecF4<C>; ++q)
