@@ -640,8 +640,9 @@ struct Moments {
 
 // Adds to M the moments of h = a * G about the Gaussian's centre for one lane's pair:
 // S[..] = sum h * delta^k, delta = mu - p, G = sum_c I_c g_c (g_c alone for
-// C == 1; I folds into the final scale).  Per voxel: h, h*dx, h*dx^2 by FMAs
-// against the lane's hoisted dx_u and dx_u^2; rows fold in dy, planes in dz.
+// C == 1; I folds into the final scale).  Per voxel: h, h*dx by an FMA against
+// the lane's hoisted dx_u, and h into its column's sum (for Sxx); rows fold in
+// dy, planes in dz.
 // Taking moments about the Gaussian (not the tile) keeps every sum
 // well-conditioned: h is large only where |delta| is small.
 //   kGateFree: a = exp2(sigma2 + bound), zero below the threshold by the
@@ -667,11 +668,14 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                                              float bound, float K, const float (&I)[C],
                                              Moments<C> &M) {
     static_assert(kGateFree || !kChain, "the chained rows are gate-free");
-    float dxu[GSV_TILE], dxu2[GSV_TILE];
+    // Sxx is only needed whole: the loop sums h per voxel column (col[u], a
+    // two-operand add per voxel) and Sxx = sum_u dx_u^2 col[u] is formed once at
+    // the end, instead of an FMA chain against dx_u^2 in every row
+    float dxu[GSV_TILE], col[GSV_TILE];
 #pragma unroll
     for (int u = 0; u < GSV_TILE; ++u) {
         dxu[u] = mxl - ((float)u - 3.5f);
-        dxu2[u] = dxu[u] * dxu[u];
+        col[u] = 0.f;
     }
     constexpr bool kSym = kGateFree && !kChain;
     float P[4];  // kSym: A2 p'^2 + bound;  kChain: 2^(A2 p'^2 - K), both at |p'| = k + 1/2
@@ -701,7 +705,7 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
         const float K0a = kChain ? fmaf(3.5f, K1, K0) : 0.f;
         const float R0z = kGateFree ? (Fn * dz) * dz : fmaf(Fn * dz, dz, -shift);
         float stp = kChain ? __builtin_amdgcn_exp2f(-fmaf(Bn, myl + 3.5f, K1)) : 0.f;  // ly = 0
-        float Q0 = 0.f, Qx = 0.f, Qxx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
+        float Q0 = 0.f, Qx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
 #pragma unroll
         for (int ly = 0; ly < GSV_TILE; ++ly) {
             if (ly >= ny) break;
@@ -745,7 +749,7 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                 R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
                 if (kGateFree) R0 += bound;  // the offset enters after the small terms
             }
-            float W1 = 0.f, W2 = 0.f, h[GSV_TILE];
+            float W1 = 0.f, h[GSV_TILE];
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
                 float a;
@@ -770,7 +774,7 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                     h[u] = a * G;
                 }
                 W1 = fmaf(h[u], dxu[u], W1);
-                W2 = fmaf(h[u], dxu2[u], W2);
+                col[u] = add_nc(col[u], h[u]);
             }
             // the row sum of the h already formed: 7 two-operand adds, which
             // issue faster than the 8 three-operand FMAs a contracted a*g sum takes
@@ -778,14 +782,12 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                                     add_nc(add_nc(h[4], h[5]), add_nc(h[6], h[7])));
             Q0 += W0;
             Qx += W1;
-            Qxx += W2;
             Qy = fmaf(W0, dy, Qy);
             Qxy = fmaf(W1, dy, Qxy);
             Qyy = fmaf(W0, dy * dy, Qyy);
         }
         M.S0 += Q0;
         M.Sx += Qx;
-        M.Sxx += Qxx;
         M.Sy += Qy;
         M.Sxy += Qxy;
         M.Syy += Qyy;
@@ -794,6 +796,10 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
         M.Syz = fmaf(Qy, dz, M.Syz);
         M.Szz = fmaf(Q0, dz * dz, M.Szz);
     }
+    float sxx = 0.f;
+#pragma unroll
+    for (int u = 0; u < GSV_TILE; ++u) sxx = fmaf(dxu[u] * dxu[u], col[u], sxx);
+    M.Sxx += sxx;
 }
 
 // vol_grad of a tile is staged scaled by a power of two so that its largest
