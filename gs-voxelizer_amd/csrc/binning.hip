@@ -25,7 +25,10 @@
 //   k_bucket_sort    one 1024-thread block per bucket sorts it by the low bits
 //                    in LDS and writes ids, tiles and tile_bins.
 // These read cum and the boxes, never the pair count: slots at or above the
-// capacity are left out.  Emission slots past a Gaussian's box (a cum that
+// capacity are left out.  When one call also runs the prefix sum of
+// num_tiles_hit (gsv_cumsum_bin_and_sort_device_count), the first two become
+// extra blocks of the scan's two launches (k_sums_hist, k_apply_digits): the
+// prefix sum and the binning in four launches.  Emission slots past a Gaussian's box (a cum that
 // disagrees with the boxes, which the reference does not guard against either)
 // carry the all-ones key and no tile on both paths; the sorts order only the
 // significant key bits, so where those name a real tile (all key bits in use)
