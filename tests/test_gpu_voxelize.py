@@ -199,17 +199,20 @@ def _mixed_gate_inputs(work, P):
     indef, huge, spread, dead = k[:60], k[60:80], k[80:120], k[120:140]
     cn[indef, 5] = -0.05 * np.abs(cn[indef, 5])  # negative zz entry: indefinite form
     inten[huge] *= np.float32(1e14)               # log2(1e-6 / mean) < -60
-    inten[spread, 0] = 3e7                        # mean ~0.5, |I| ~ 2^25 * mean
-    inten[spread, 1] = -3e7 + 4  # binary32 spacing at 3e7 is 2: mean 2 exactly
+    if inten.shape[1] > 1:
+        inten[spread, 0] = 3e7                    # mean ~0.5, |I| ~ 2^25 * mean
+        inten[spread, 1] = -3e7 + 4  # binary32 spacing at 3e7 is 2: mean 2 exactly
     inten[dead] = 5e-7                            # alpha * mean < 1e-6 everywhere
     return pr, cn, inten
 
 
-def test_mixed_gate_paths_match_oracle(device):
+@pytest.mark.parametrize("channels", [2, 1])
+def test_mixed_gate_paths_match_oracle(device, channels):
     """Exact-gate Gaussians sharing tiles with gate-free ones, forward and both
-    backward reductions."""
+    backward reductions.  At C = 1 the forward accumulates in units of
+    1e-6 * 2^126 on every path, the exact one included."""
     import gs_voxelizer.cuda as _C
-    cfg = small_config(1, 1500, vol=(24, 32, 28), channels=2)
+    cfg = small_config(1, 1500, vol=(24, 32, 28), channels=channels)
     work = S.make_gaussians(cfg, seed=12)
     P = _prepare(work, device)
     pr, cn, inten = _mixed_gate_inputs(work, P)
@@ -221,7 +224,7 @@ def test_mixed_gate_paths_match_oracle(device):
     # of |terms| from above: mean(|I|) >= mean(I) only lowers the threshold.
     cond = O.voxelize_fwd(cfg.vol, P["rids"], P["rbins"], pr, cn, np.abs(inten))
     report_close("mixed gates: volume", np32(vol), ref, RTOL, ATOL, bound=amb + 1e-5 * cond)
-    g = np.random.default_rng(3).standard_normal(cfg.vol + (2,)).astype(np.float32)
+    g = np.random.default_rng(3).standard_normal(cfg.vol + (channels,)).astype(np.float32)
     rg, absum, ramb = O.voxelize_bwd(cfg.vol, P["rids"], P["rbins"], pr, cn, inten, g,
                                      diagnostics=True)
     for mode in MODES:
