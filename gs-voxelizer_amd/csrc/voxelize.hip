@@ -24,11 +24,12 @@
 //    |s| <= h path.
 //  * This file is compiled in binary32 flush-to-zero mode
 //    (-fgpu-flush-denormals-to-zero): v_mul_f32 then also returns 0 below
-//    2^-126, so the forward can form most of a row's exp2 values as products
+//    2^-126, so both kernels form most of a row's exp2 values as products
 //    with the same gate: two or three v_exp_f32 per 8-voxel row instead of
-//    eight.  A v_exp_f32 occupies the SIMD four times as long as an FMA (16
-//    against 4 cycles per wave64, measured), so the eight-exp row spent more
-//    time in them than in its 28 other instructions.  Elsewhere the kernels
+//    eight.  A v_exp_f32 issues at about half an FMA's rate (0.106 against
+//    0.222 wave64 instructions per SIMD-cycle on a throughput probe) and does
+//    not overlap the other VALU work, so the eight-exp row spent about as much
+//    time in them as in its 28 other instructions.  Elsewhere the kernels
 //    keep every binary32 value they rely on in
 //    the normal range (the backward's power-of-two staging of vol_grad), so
 //    the mode changes no result beyond denormal magnitudes.
