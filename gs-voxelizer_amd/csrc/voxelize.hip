@@ -853,6 +853,10 @@ struct BwdArgs {
     const int *order;
     const int64_t *d_work;
     int n_work;  // work items, set by each kernel from the counts
+    // One byte per wave of work items, written by k_vox_bwd for every wave:
+    // 1 when the wave's pairs span more tiles than it stages (k_vox_bwd_rest
+    // processes the others).
+    uint8_t *rest_flag;
 };
 
 // The live pair count: *d_count clamped to [0, cap], or cap without one.
@@ -1421,7 +1425,9 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
         BwdLane<C> L;
         uint64_t starts;
         int nslots;
-        if (bwd_slots(a, p0, L, starts, nslots)) {
+        const bool slots = bwd_slots(a, p0, L, starts, nslots);
+        if (threadIdx.x == 0) a.rest_flag[wv] = slots && nslots > K;
+        if (slots) {
             bwd_gaussian(a, L);
             // one wave-uniform choice: gate-free unless a live lane needs the exact gate
             const bool wave_fast = __all(!L.live || L.fast);
@@ -1439,12 +1445,9 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
 
 // The pairs that k_vox_bwd left: those of the waves spanning more than K tiles,
 // in groups of K tiles after the first.  A fixed grid of kRestBlocks
-// workgroups; workgroup b checks the waves b, b + G, b + 2G, ... (G = the grid
-// size) 64 at a time, so the waves to process (many in a sparse scene, none in
-// most dense ones) spread over the whole grid.  The tiles of a wave's first and
-// last pair come from the sorted pair -> tile map, and a wave whose tiles lie
-// within K consecutive ids spans at most K of them; the others are counted
-// exactly and processed.
+// workgroups; workgroup b reads the flags of the waves b, b + G, b + 2G, ...
+// (G = the grid size) 64 at a time, so the waves to process (many in a sparse
+// scene, none in most dense ones) spread over the whole grid.
 constexpr int kRestBlocks = 512;
 
 template <int C, int K>
@@ -1455,14 +1458,8 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd_rest(BwdArgs a) {
     const int64_t G = gridDim.x;
     for (int64_t base = blockIdx.x; base < waves; base += G * kWave) {
         const int64_t w = base + (int64_t)threadIdx.x * G;
-        bool maybe = false;
-        if (w < waves) {
-            const int64_t p0 = w * kWave;
-            const int64_t p1 = min<int64_t>(p0 + kWave, a.n_work) - 1;
-            const int t0 = a.pair_tiles[bwd_pair(a, p0)], t1 = a.pair_tiles[bwd_pair(a, p1)];
-            maybe = !(t0 >= 0 && t1 < a.T && t1 >= t0 && t1 - t0 < K);
-        }
-        for (uint64_t m = __ballot(maybe); m; m &= m - 1) {
+        const bool more = w < waves && a.rest_flag[w] != 0;
+        for (uint64_t m = __ballot(more); m; m &= m - 1) {
             const int64_t p0 = (base + (int64_t)__builtin_ctzll(m) * G) * kWave;
             BwdLane<C> L;
             uint64_t starts;
@@ -1538,14 +1535,15 @@ __global__ __launch_bounds__(kReduceThreads) void k_pair_reduce(
 }
 
 struct BwdLayout {
-    size_t tiles, partial, order, part, kept, end;
+    size_t tiles, partial, order, part, kept, rest, end;
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 // pair -> tile map (n_isect ints; unused when the caller passes the binning's
-// sorted keys), the per-pair partials in pairs mode, then the work list of the
-// culled mode (order, the per-block counts and the kept count).
+// sorted keys), the per-pair partials in pairs mode, the work list of the
+// culled mode (order, the per-block counts and the kept count), then the
+// backward's per-wave rest flags.
 BwdLayout bwd_layout(int64_t n_isect, int channels, bool pairs) {
     BwdLayout L{};
     size_t off = 0;
@@ -1555,6 +1553,7 @@ BwdLayout bwd_layout(int64_t n_isect, int channels, bool pairs) {
     L.order = off; off += align256((size_t)imax64(n_isect, 1) * 4);
     L.part = off; off += align256((size_t)((n_isect + kKeepTile - 1) / kKeepTile + 1) * 4);
     L.kept = off; off += 256;
+    L.rest = off; off += align256((size_t)((imax64(n_isect, 1) + kWave - 1) / kWave));
     L.end = off;
     return L;
 }
@@ -1712,6 +1711,7 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     args.order = order;
     args.d_work = d_work;
     args.n_work = 0;
+    args.rest_flag = reinterpret_cast<uint8_t *>(ws + L.rest);
 #define GSV_VB(CH)                                                                                  \
     {                                                                                               \
         KernelTimer timer(kTimedVoxBwd, s);                                                         \
