@@ -18,7 +18,10 @@ ellipsoid, and reports its decision per sorted pair (pair_live).  Checked here:
   with the backward's chained rows off (GSV_BWD_CHAIN=0): with them on, a
   group of pairs takes them only when all of its pairs qualify, and the flags
   change which pairs share a wave, so there the two agree to rounding
-  (rel 1e-4 / abs 1e-6) instead.
+  (rel 1e-4 / abs 1e-6) instead;
+- the backward depends on no stale workspace contents: a workspace of 0x00
+  bytes and one of 0xFF bytes give the same bits, with and without the work
+  list.
 """
 import dataclasses
 
@@ -162,3 +165,60 @@ def test_backward_with_cull_flags_is_bitwise_equal(device, monkeypatch, name, wo
     plain = _C.voxelize_backward_per_gaussian(*args, gd, *boxes, tiles_sorted=R["tiles"])
     for a, b in zip(plain, got):
         _agree(f"{name} capacity", a, b, exact)
+
+
+def _bwd_on_workspace(R, cfg, gd, fill, with_flags):
+    """Per-Gaussian backward through the C-ABI on a workspace of `fill` bytes."""
+    import ctypes
+    import gs_voxelizer.cuda as _C
+    w, n, I = R["w"], R["n"], R["I"]
+    D, H, W = cfg.vol
+    C = _C._channels(w.intensities)
+    nbytes = ctypes.c_size_t(0)
+    _C._call("voxelize_bwd_workspace_bytes", D, H, W, C, I, 1, ctypes.byref(nbytes))
+    ws = torch.full((nbytes.value,), fill, device=gd.device, dtype=torch.uint8)
+    f32 = dict(device=gd.device, dtype=torch.float32)
+    dpos, dconic, dint = (torch.empty((n, k), **f32) for k in (4, 6, C))
+    null = ctypes.c_void_p(0)
+    live = _C._ptr(R["live"]) if with_flags else null
+    with torch.cuda.device(gd.device):
+        _C._call("voxelize_bwd", D, H, W, C, n, I, _C._ptr(R["ids"]), _C._ptr(R["bins"]),
+                 _C._ptr(R["pr"]), _C._ptr(R["cn"]), _C._ptr(w.intensities), _C._ptr(gd),
+                 _C._ptr(R["tmin"]), _C._ptr(R["tmax"]), _C._ptr(R["cum"]),
+                 _C._ptr(R["tiles"]), null, live, _C._ptr(dpos), _C._ptr(dconic), _C._ptr(dint),
+                 1, _C._ptr(ws), nbytes.value, _C._stream(gd.device))
+    torch.cuda.synchronize()
+    return dpos, dconic, dint
+
+
+@pytest.mark.parametrize("with_flags", [False, True], ids=["all_pairs", "work_list"])
+@pytest.mark.parametrize("name,work", [c for c in CASES if c[0] in ("cfg1", "sparse_c1",
+                                                                    "sparse_c3", "needles")],
+                         ids=["cfg1", "sparse_c1", "sparse_c3", "needles"])
+def test_backward_ignores_stale_workspace(device, name, work, with_flags):
+    """The backward reads from its workspace only what the same call wrote there
+    (the pair -> tile map, the partials, the work list and the per-wave flags
+    that send waves spanning more than their staged tiles to the rest pass):
+    gradients from a workspace of 0x00 bytes and of 0xFF bytes agree bitwise,
+    on sparse scenes where many waves take the rest pass and on cfg1."""
+    R = _run(work, device)
+    cfg = work.cfg
+    target = S.phantom(work).numpy()[..., None]
+    g = l1_vol_grad(np32(R["vol"]), np.broadcast_to(target, tuple(R["vol"].shape)))
+    gd = torch.from_numpy(np.ascontiguousarray(g)).to(device)
+    zeros = _bwd_on_workspace(R, cfg, gd, 0x00, with_flags)
+    ones = _bwd_on_workspace(R, cfg, gd, 0xFF, with_flags)
+    for what, a, b in zip(("dpos3d_radii", "dconics", "dintensities"), zeros, ones):
+        assert torch.equal(a, b), (name, what)
+    ref = _C_api_backward(R, cfg, gd, with_flags)
+    for what, a, b in zip(("dpos3d_radii", "dconics", "dintensities"), zeros, ref):
+        assert torch.equal(a, b), (name, what, "against the Python entry")
+
+
+def _C_api_backward(R, cfg, gd, with_flags):
+    import gs_voxelizer.cuda as _C
+    w = R["w"]
+    return _C.voxelize_backward_per_gaussian(cfg.vol, R["ids"], R["bins"], R["pr"], R["cn"],
+                                             w.intensities, gd, R["tmin"], R["tmax"], R["cum"],
+                                             tiles_sorted=R["tiles"],
+                                             pair_live=R["live"] if with_flags else None)
