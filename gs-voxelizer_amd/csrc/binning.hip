@@ -286,23 +286,24 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_hist(const int *__restri
         hist[(int64_t)d * hstride + blockIdx.x] = s_hist[d];
 }
 
-// Exclusive scan of one int per thread across an NT-thread block; *total
-// gets the block's sum.  s_wtot holds NT / 64 ints.
-template <int NT>
-__device__ __forceinline__ int block_scan_total(int v, int *s_wtot, int *total) {
+// Exclusive scan of one value per thread across an NT-thread block; *total
+// gets the block's sum.  s_wtot holds NT / 64 values (int, or long long where
+// the sum may pass 2^31).
+template <int NT, typename V = int>
+__device__ __forceinline__ V block_scan_total(V v, V *s_wtot, V *total) {
     const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
-    int inc = v;
+    V inc = v;
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
-        const int o = __shfl_up(inc, d, kWave);
+        const V o = __shfl_up(inc, d, kWave);
         if (lane >= d) inc += o;
     }
     if (lane == kWave - 1) s_wtot[wave] = inc;
     __syncthreads();
-    int off = 0, sum = 0;
+    V off = 0, sum = 0;
 #pragma unroll
     for (int w = 0; w < NT / kWave; ++w) {
-        const int x = s_wtot[w];
+        const V x = s_wtot[w];
         off += w < wave ? x : 0;
         sum += x;
     }
@@ -580,9 +581,10 @@ __device__ __forceinline__ GaussRows gauss_rows(int g, int n, int64_t cap,
                                                 const int *__restrict__ cum) {
     GaussRows r{};
     if (g >= n) return r;
+    // ns in [0, cap] even where an int32 cum has wrapped past 2^31 (s0 < 0)
     const int64_t s0 = g > 0 ? cum[g - 1] : 0;
     const int64_t s1 = min<int64_t>(cum[g], cap);
-    const int64_t ns = s1 > s0 ? s1 - s0 : 0;
+    const int64_t ns = s1 > s0 ? min(s1 - s0, cap) : 0;
     r.mnx = tile_min[3 * g]; r.mny = tile_min[3 * g + 1]; r.mnz = tile_min[3 * g + 2];
     r.ex = tile_max[3 * g] - r.mnx;
     r.ey = tile_max[3 * g + 1] - r.mny;
@@ -946,18 +948,26 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
     const int *__restrict__ totals, BucketGeom G, int64_t cap, int2 *__restrict__ tile_bins) {
     __shared__ int s_cnt[kBucketWaves << LB];
     __shared__ int s_wtot[kBucketWaves];
+    __shared__ long long s_wtot64[kBucketWaves];
     __shared__ unsigned s_stage[kStageWords<LB>];
     const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
     const int b = blockIdx.x, lb = G.lb, nb = 1 << lb;
     const unsigned lmask = (unsigned)nb - 1u;
-    int start;
+    // The bucket's first word: the sum of the lower buckets' totals, in 64 bits
+    // and each total clamped to [0, cap].  The totals are int32 sums of the
+    // pair counts; past 2^31 pairs (a call far over its capacity) they wrap,
+    // and the clamps keep every access of this block inside [0, cap) whatever
+    // they hold.
+    auto clamp_total = [cap](int x) -> long long { return x < 0 ? 0 : min<long long>(x, cap); };
+    int64_t start;
     {
-        int tot;
-        block_scan_total<kBucketThreads>(t < b ? totals[t] : 0, s_wtot, &tot);
-        start = tot;
+        long long tot;
+        block_scan_total<kBucketThreads, long long>(t < b ? clamp_total(totals[t]) : 0,
+                                                    s_wtot64, &tot);
+        start = min<long long>(tot, cap);
     }
     // the words below the capacity (all of them unless the counts disagree with it)
-    const int size = start < cap ? (int)min<int64_t>(totals[b], cap - start) : 0;
+    const int size = (int)min<int64_t>(clamp_total(totals[b]), cap - start);
     for (int i = t; i < kBucketWaves * nb; i += kBucketThreads) s_cnt[i] = 0;
     // segments of whole 64-word rounds, in bucket order; batches of kBatch rounds
     const int seg = (size + kBucketWaves * kWave - 1) / (kBucketWaves * kWave) * kWave;
@@ -1010,7 +1020,8 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_sort(
         const int ks = s_cnt[t], ke = t + 1 < nb ? s_cnt[t + 1] : size;
         const int tile = padded_tile(G, key0 | (unsigned)t);
         if (tile != kInvalidKey)
-            tile_bins[tile] = ke > ks ? make_int2(start + ks, start + ke) : make_int2(0, 0);
+            tile_bins[tile] = ke > ks ? make_int2((int)(start + ks), (int)(start + ke))
+                                      : make_int2(0, 0);
     }
     const bool staged = size <= kStageWords<LB>;
     __syncthreads();

@@ -53,6 +53,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "gsv_device.h"
 #include "gsv_scan.h"
 
@@ -75,6 +77,7 @@ constexpr float kExpFlush = 126.0f;     // v_exp_f32 results below 2^-126 are 0
 constexpr float kAccUnit = 1e-6f * 0x1p126f;
 constexpr float kInvAccUnit = (float)(1.0 / (double)kAccUnit);  // rounded once: ~1e-7 overall
 constexpr float kDeadOffset = -1000.0f;  // exponent offset that zeroes a lane
+constexpr float kFwdFastConicMax = 4096.0f;  // largest conic diagonal of the forward's gate-free rows
 
 struct Gate {
     float shift;   // exact path: s = sigma2 - shift
@@ -153,6 +156,9 @@ __device__ __forceinline__ bool may_touch(float mx, float my, float mz, float a,
     const float cfx = d * f - e * e, cfy = a * f - c * c, cfz = a * d - b * b;
     const float det = a * cfx - b * (b * f - c * e) + c * (b * e - c * d);
     if (!(a > 0.f && cfz > 0.f && det > 0.f)) return true;
+    // In flush-to-zero mode the reciprocal of det >= 2^126 is 0, which would
+    // shrink the half-widths below to 0.01: keep such (very thin) Gaussians.
+    if (!(det < 0x1p125f)) return true;
     const float k2 = -2.0f * kLn2 * t2;
     const float inv = __builtin_amdgcn_rcpf(det);
     const float hx = __builtin_amdgcn_sqrtf(k2 * cfx * inv) * 1.001f + 0.01f;
@@ -298,8 +304,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(C == 1 ? 
                     live = may_touch(p.x, p.y, p.z, c01.x, c01.y, c23.x, c23.y, c45.x, c45.y, gt.t2,
                                      tg.xlo, tg.xhi, tg.ylo, tg.yhi, tg.zlo, tg.zhi);
                 if (live) {
+                    // the gate-free rows expand the form about the tile centre, whose
+                    // terms grow with the conic (~12 |q| at the tile's edge) and cancel
+                    // near the Gaussian's centre: conics above kFwdFastConicMax (axes
+                    // below 1/64 voxel) take the exact path's direct form instead
                     fast = gate_free_ok(gt, max_abs, p.x, p.y, p.z, c01.x, c01.y, c23.x, c23.y,
-                                        c45.x, c45.y);
+                                        c45.x, c45.y) &&
+                           fmaxf(c01.x, fmaxf(c23.y, c45.y)) <= kFwdFastConicMax;
                     // centred offsets: delta = c - p', p' = local index - 3.5
                     const float cx = p.x - (float)tg.x0 - 4.0f;
                     const float cy = p.y - (float)tg.y0 - 4.0f, cz = p.z - (float)tg.z0 - 4.0f;
@@ -369,10 +380,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(C == 1 ? 
 #pragma unroll
                         for (int c = 0; c < C; ++c) rec[13 + c] = C == 1 ? rho : I[c] * gt.fscale;
                     } else {
-                        // (cx, cy, cz, A2 | B, C, D, E | F, shift, half, A2 cx | I*2^shift)
+                        // (cx, cy, cz, A2 | B, C, D, E | F, shift, half, - | I*2^shift)
                         rec[0] = cx; rec[1] = cy; rec[2] = cz; rec[3] = A2;
                         rec[4] = q1.x; rec[5] = q1.y; rec[6] = q1.z; rec[7] = q1.w;
-                        rec[8] = F; rec[9] = gt.shift; rec[10] = gt.half; rec[11] = A2 * cx;
+                        rec[8] = F; rec[9] = gt.shift; rec[10] = gt.half; rec[11] = 0.f;
 #pragma unroll
                         for (int c = 0; c < C; ++c)
                             rec[12 + c] = C == 1 ? (I[0] * gt.scale) * kInvAccUnit : I[c] * gt.scale;
@@ -495,14 +506,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(C == 1 ? 
             const float dy = r0.y - py, dz = r0.z - pz;
             const float R1 = fmaf(r1.x, dy, r1.y * dz);
             const float R0 = fmaf(fmaf(r1.z, dy, r1.w * dz), dy, fmaf(r2.x * dz, dz, -r2.y));
-            // along the row: s(u') = R0 + R1*dx + A2*dx^2, dx = cx - u', rewritten
-            // around the row centre as T0 + u' * (A2 * u' - T1)
-            const float T1 = R1 + 2.0f * r2.w;
-            const float T0 = fmaf(r0.x, R1 + r2.w, R0);
+            // along the row: s(u') = R0 + dx * (R1 + A2 * dx), dx = cx - u', in
+            // the offsets themselves as the reference forms sigma (no expansion
+            // about the row centre, whose terms would cancel for a large conic)
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
-                const float uc = (float)u - 3.5f;
-                const float s = fmaf(uc, fmaf(uc, r0.w, -T1), T0);
+                const float dx = r0.x - ((float)u - 3.5f);
+                const float s = fmaf(dx, fmaf(r0.w, dx, R1), R0);
                 const float a = (fabsf(s) <= r2.z) ? __builtin_amdgcn_exp2f(s) : 0.f;
 #pragma unroll
                 for (int c = 0; c < C; ++c) acc[u][c] = fmaf(a, iw[c], acc[u][c]);
@@ -826,10 +836,26 @@ constexpr int kStageTilesVerySparse = C == 1 ? 8 : 6;  // < kVerySparsePairs
 constexpr int64_t kSparsePairs = 64;
 constexpr int64_t kVerySparsePairs = 24;
 
+// Whether the backward may take chained rows: on, unless GSV_BWD_CHAIN=0 is
+// set when the process first asks, or gsv_set_backward_chains(0) was called.
+// Read once per process, then kept here.
+std::atomic<int> g_bwd_chains{-1};
+
+bool bwd_chains_enabled() {
+    int v = g_bwd_chains.load(std::memory_order_relaxed);
+    if (v < 0) {
+        const char *env = getenv("GSV_BWD_CHAIN");
+        int unset = -1;
+        g_bwd_chains.compare_exchange_strong(unset, (env && strcmp(env, "0") == 0) ? 0 : 1);
+        v = g_bwd_chains.load(std::memory_order_relaxed);
+    }
+    return v != 0;
+}
+
 struct BwdArgs {
     int D, H, W, Tx, Ty, n, n_isect;
     FastDiv fx, fy;  // division by Tx and by Ty
-    // Chained rows allowed (GSV_BWD_CHAIN=0 turns them off).  A group takes them
+    // Chained rows allowed (bwd_chains_enabled()).  A group takes them
     // when every one of its pairs qualifies, so a pair's rounding can depend on
     // the pairs it shares a wave with (as for exact-gate pairs, which take the
     // whole group to the exact path); without them it never does.
@@ -1694,10 +1720,7 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     args.D = D; args.H = H; args.W = W; args.Tx = Tx; args.Ty = Ty; args.n = n; args.n_isect = ni;
     args.fx = make_fastdiv((uint32_t)Tx);
     args.fy = make_fastdiv((uint32_t)Ty);
-    {
-        const char *chain = getenv("GSV_BWD_CHAIN");
-        args.chain = !(chain && strcmp(chain, "0") == 0);
-    }
+    args.chain = bwd_chains_enabled() ? 1 : 0;
     args.T = T;
     args.ids = gaussian_ids_sorted; args.pair_tiles = pair_tiles;
     args.pos_radii = reinterpret_cast<const float4 *>(pos3d_radii);
@@ -1820,6 +1843,14 @@ extern "C" int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channel
                              tile_min, tile_max, cum_tiles_hit, tiles_sorted, num_intersects_dev,
                              pair_live, dpos3d_radii, dconics,
                              dintensities, variant, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int gsv_set_backward_chains(int32_t enabled, int32_t *previous) {
+    if (enabled != 0 && enabled != 1) return GSV_ERR_INVALID_ARGUMENT;
+    const int before = bwd_chains_enabled() ? 1 : 0;
+    g_bwd_chains.store(enabled, std::memory_order_relaxed);
+    if (previous) *previous = before;
+    return GSV_OK;
 }
 
 extern "C" int gsv_voxelize_bwd_l1(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,

@@ -40,6 +40,7 @@ SIGNATURES = {
                                  _P],
     "gsv_voxelize_fwd": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P, _P,
                          _P, _P],
+    "gsv_set_backward_chains": [_c_int, ctypes.POINTER(_c_int)],
     "gsv_voxelize_fwd_l1_workspace_bytes": [_c_int, _c_int, _c_int, ctypes.POINTER(_c_size_t)],
     "gsv_voxelize_fwd_l1": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P,
                             _P, _P, _P, _P, _P, _P, _c_size_t, _P],

@@ -485,3 +485,15 @@ def voxelize_backward_per_gaussian(vol_size, gaussian_ids_sorted, tile_bins, pos
                               intensities, vol_grad_in, tile_min, tile_max, cum_tiles_hit,
                               tiles_sorted=tiles_sorted, count_dev=count_dev,
                               pair_live=pair_live)
+
+
+def set_backward_chains(enabled: bool) -> bool:
+    """Turn the backward's chained rows on or off for the rest of the process;
+    returns the previous setting.  With them off the backward's results do not
+    depend on which pairs share a 64-pair group (the cull flags, the capacity
+    mode and the tile map then change no bit); with them on (the default,
+    unless GSV_BWD_CHAIN=0 was set when the process first ran a backward) they
+    agree to rounding.  Not in the reference."""
+    prev = ctypes.c_int32(0)
+    _call("set_backward_chains", 1 if enabled else 0, ctypes.byref(prev))
+    return bool(prev.value)

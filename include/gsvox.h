@@ -153,8 +153,12 @@ int gsv_bin_and_sort_device_count(int32_t n, int64_t capacity, const int64_t *nu
  * single-pass scan of its block sums (n up to 4,194,304), the bucket counts
  * are formed beside the scan's block sums and their prefix beside the scan's
  * apply pass: four kernel launches instead of six, the same results.  When
- * *total_out > capacity the binning's output is incomplete, as for
- * gsv_bin_and_sort_device_count.
+ * *total_out > capacity, only *total_out (and *total_host, cum_tiles_hit) is
+ * valid: gaussian_ids_sorted, tile_bins and tiles_sorted may hold any values
+ * (on the bucket method they are not a sorted prefix, unlike
+ * gsv_bin_and_sort_device_count's); the caller bins again with a capacity of
+ * at least the count.  Every access stays inside the arrays, also when the
+ * count passes 2^31.
  */
 int gsv_cumsum_bin_workspace_bytes(int32_t n, int64_t capacity, int32_t D, int32_t H, int32_t W,
                                    size_t *bytes);
@@ -218,8 +222,8 @@ int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
  *   - all three given (the projection's tile boxes and the prefix sum the
  *     binning used): each (tile, Gaussian) pair writes its partial gradient to
  *     its duplication slot and one pass sums each Gaussian's slots in order.
- *     No atomics, bitwise reproducible; the workspace grows by
- *     num_intersects * (9 + channels) * 4 bytes.
+ *     No atomics, and the same bits from run to run on the same inputs; the
+ *     workspace grows by num_intersects * (9 + channels) * 4 bytes.
  * tiles_sorted (optional) is the binning's sorted keys (gsv_bin_and_sort's
  * tiles_sorted, at least num_intersects entries); without it the tile of each
  * pair is rebuilt from tile_bins by one more kernel.
@@ -230,8 +234,13 @@ int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
  * backward needs no host-side count, so a caller can capture it in a graph.
  * pair_live (optional): the flags the forward wrote (gsv_voxelize_fwd's
  * pair_live, same pairs); the backward then evaluates only the pairs the
- * forward kept and gives the culled ones a zero partial.  The gradients are
- * the same bits as without it.
+ * forward kept and gives the culled ones a zero partial.  With chained rows
+ * off (gsv_set_backward_chains(0) or GSV_BWD_CHAIN=0) the gradients are the
+ * same bits as without it.  With them on (the default) a group of 64 pairs
+ * takes the chained rows only when all of its pairs qualify, so a pair's
+ * rounding depends on the pairs that share its wave, and the flags, the
+ * capacity mode and the tile map change that grouping: the results then agree
+ * to rounding (rel 1e-4 / abs 1e-6), not bit for bit.
  * Workspace size from gsv_voxelize_bwd_workspace_bytes (deterministic = 1 for
  * the second mode).
  */
@@ -247,6 +256,20 @@ int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
                      const uint8_t *pair_live, float *dpos3d_radii, float *dconics,
                      float *dintensities, int32_t variant, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/*
+ * Chained rows of the backward (no counterpart in the reference).  The
+ * backward forms most exp2 values of a tile row as products of two or three
+ * v_exp_f32 results when every pair of a 64-pair group allows it; that is
+ * faster and equal to the per-voxel evaluation to rounding, but makes a pair's
+ * last bits depend on its group (see pair_live above).  enabled = 0 turns the
+ * chains off for every later backward of the process (bitwise reproducible
+ * across culling and capacity modes), 1 turns them on; *previous (optional)
+ * receives the setting before the call.  The first backward of a process
+ * takes the setting from GSV_BWD_CHAIN (off when "0") unless this was called
+ * before; the variable is read only then.
+ */
+int gsv_set_backward_chains(int32_t enabled, int32_t *previous);
 
 /*
  * Voxelization fused with an L1 loss.  These have no reference binding.  They

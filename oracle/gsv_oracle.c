@@ -9,7 +9,8 @@
  * Build: oracle/build_oracle.sh (gcc -O2 -std=c11 -ffp-contract=off -fopenmp).
  * Every arithmetic expression keeps the reference's evaluation order in
  * binary32 with no contraction, so that the integer bin outputs are defined
- * by IEEE-754 and can be compared bit for bit with the device.
+ * by IEEE-754 and can be compared bit for bit with the device.  The same
+ * source built with -DORC_BINARY64 is the binary64 twin described below.
  *
  * Reference = PaPieta/gs-voxelizer v0.1.0; citations are path:line under
  * gs_voxelizer/.  GLM mat3 semantics are restated explicitly: matrices are
@@ -18,17 +19,35 @@
  *
  * Parity status of each entry point is documented next to it ("pinned by").
  */
-#include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#include <tgmath.h>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
 
 #include "../gs-voxelizer_amd/csrc/gsv_numerics.h"
 
-typedef float mat3[3][3]; /* [col][row], GLM layout */
+/*
+ * Arithmetic type.  The default build (liboracle.so) computes in binary32, the
+ * reference's type, in its evaluation order.  -DORC_BINARY64 builds the same
+ * source in binary64 (liboracle64.so): the same formulas, operation for
+ * operation, with the reference's binary32 constants (1e-7f, 1e-6f) kept as
+ * they are, and the natural log from libm.  Fed binary32 inputs, it estimates
+ * the exact value of each output to ~1e-16 relative, which is what the tests
+ * measure the binary32 evaluations (this oracle's and the device's) against.
+ * Math calls go through <tgmath.h>, so each resolves to the type's function.
+ */
+#ifdef ORC_BINARY64
+typedef double real;
+#define orc_log(x) log(x)
+#else
+typedef float real;
+#define orc_log(x) gsv_logf(x)
+#endif
+
+typedef real mat3[3][3]; /* [col][row], GLM layout */
 
 static void m3_mul(mat3 out, mat3 a, mat3 b) {
     mat3 r;
@@ -46,8 +65,8 @@ static void m3_transpose(mat3 out, mat3 a) {
 }
 
 /* glm::mat3(a0..a8): column-major constructor. */
-static void m3_set(mat3 m, float a0, float a1, float a2, float a3, float a4, float a5,
-                   float a6, float a7, float a8) {
+static void m3_set(mat3 m, real a0, real a1, real a2, real a3, real a4, real a5,
+                   real a6, real a7, real a8) {
     m[0][0] = a0; m[0][1] = a1; m[0][2] = a2;
     m[1][0] = a3; m[1][1] = a4; m[1][2] = a5;
     m[2][0] = a6; m[2][1] = a7; m[2][2] = a8;
@@ -57,10 +76,10 @@ static void m3_set(mat3 m, float a0, float a1, float a2, float a3, float a4, flo
  * The reference normalises with rsqrtf; the restatement uses 1/sqrtf. The
  * squared norm is summed in the order the reference reads the float4
  * (.w,.x,.y,.z = q3,q0,q1,q2). */
-static void quat_to_rotmat(const float *q, mat3 R, float *wxyz) {
-    const float n2 = q[3] * q[3] + q[0] * q[0] + q[1] * q[1] + q[2] * q[2];
-    const float s = 1.0f / sqrtf(n2);
-    const float w = q[0] * s, x = q[1] * s, y = q[2] * s, z = q[3] * s;
+static void quat_to_rotmat(const real *q, mat3 R, real *wxyz) {
+    const real n2 = q[3] * q[3] + q[0] * q[0] + q[1] * q[1] + q[2] * q[2];
+    const real s = 1.0f / sqrt(n2);
+    const real w = q[0] * s, x = q[1] * s, y = q[2] * s, z = q[3] * s;
     m3_set(R,
            1.f - 2.f * (y * y + z * z), 2.f * (x * y - w * z), 2.f * (x * z + w * y),
            2.f * (x * y + w * z), 1.f - 2.f * (x * x + z * z), 2.f * (y * z - w * x),
@@ -70,7 +89,7 @@ static void quat_to_rotmat(const float *q, mat3 R, float *wxyz) {
 
 /* Voxel-space covariance, optim_to_render.cu:85-103 (forward) and 280-300 (backward).
  * vs3 = (vs.x, vs.y, vs.z) in the kernel's dim3 order (D,H,W), i.e. (z,y,x) sizes. */
-static void voxel_covariance(const float *scale, const float *quat, const float vs3[3],
+static void voxel_covariance(const real *scale, const real *quat, const real vs3[3],
                              mat3 R, mat3 S, mat3 M2, mat3 cov) {
     m3_set(S, 1.f, 0.f, 0.f, 0.f, 1.f, 0.f, 0.f, 0.f, 1.f);
     S[0][0] = scale[0];
@@ -94,108 +113,108 @@ static void voxel_covariance(const float *scale, const float *quat, const float 
  * Pinned by: tests/test_oracle_projection.py (closed forms, fp64 linear algebra,
  * hand-computed boxes, special values).
  */
-int orc_project_fwd(int n, int C, const float *pos3d, const float *scale3d, const float *quat,
-                     const float *intens, int D, int H, int W, float wz, float wy, float wx,
-                     float cz, float cy, float cx, float *pos_radii, float *conics, int *tile_min,
+int orc_project_fwd(int n, int C, const real *pos3d, const real *scale3d, const real *quat,
+                     const real *intens, int D, int H, int W, real wz, real wy, real wx,
+                     real cz, real cy, real cx, real *pos_radii, real *conics, int *tile_min,
                      int *tile_max, int *num_tiles_hit) {
     if (n < 0 || C < 1 || C > GSV_MAX_CHANNELS) return 1;
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
-    const float vs3[3] = {wz / (float)D, wy / (float)H, wx / (float)W};
-    memset(pos_radii, 0, sizeof(float) * 4 * (size_t)n);
-    memset(conics, 0, sizeof(float) * 6 * (size_t)n);
+    const real vs3[3] = {wz / (real)D, wy / (real)H, wx / (real)W};
+    memset(pos_radii, 0, sizeof(real) * 4 * (size_t)n);
+    memset(conics, 0, sizeof(real) * 6 * (size_t)n);
     memset(tile_min, 0, sizeof(int) * 3 * (size_t)n);
     memset(tile_max, 0, sizeof(int) * 3 * (size_t)n);
     memset(num_tiles_hit, 0, sizeof(int) * (size_t)n);
 #pragma omp parallel for schedule(static)
     for (int g = 0; g < n; ++g) {
-        const float *p = pos3d + 3 * (size_t)g, *s = scale3d + 3 * (size_t)g;
-        const float pix[3] = {(p[0] - cx + (wx * 0.5f)) / vs3[2],
+        const real *p = pos3d + 3 * (size_t)g, *s = scale3d + 3 * (size_t)g;
+        const real pix[3] = {(p[0] - cx + (wx * 0.5f)) / vs3[2],
                               (p[1] - cy + (wy * 0.5f)) / vs3[1],
                               (p[2] - cz + (wz * 0.5f)) / vs3[0]};
         mat3 R, S, M2, cov;
         voxel_covariance(s, quat + 4 * (size_t)g, vs3, R, S, M2, cov);
-        const float a = cov[0][0], b = cov[0][1], c = cov[0][2];
-        const float d = cov[1][1], e = cov[1][2], f = cov[2][2];
-        const float det = a * d * f + 2 * b * c * e - a * e * e - f * b * b - d * c * c;
+        const real a = cov[0][0], b = cov[0][1], c = cov[0][2];
+        const real d = cov[1][1], e = cov[1][2], f = cov[2][2];
+        const real det = a * d * f + 2 * b * c * e - a * e * e - f * b * b - d * c * c;
         if (det == 0.0f) continue;
-        const float inv_det = 1.0f / det;
-        const float ia = inv_det * (d * f - e * e);
-        const float ib = inv_det * (c * e - b * f);
-        const float ic = inv_det * (b * e - c * d);
-        const float id = inv_det * (a * f - c * c);
-        const float ie = inv_det * (b * c - a * e);
-        const float iff = inv_det * (a * d - b * b);
-        const float radius = ceilf((3.f * fmaxf(s[0], fmaxf(s[1], s[2]))) /
-                                   fminf(vs3[2], fminf(vs3[1], vs3[0])));
-        float mean = 0.f;
+        const real inv_det = 1.0f / det;
+        const real ia = inv_det * (d * f - e * e);
+        const real ib = inv_det * (c * e - b * f);
+        const real ic = inv_det * (b * e - c * d);
+        const real id = inv_det * (a * f - c * c);
+        const real ie = inv_det * (b * c - a * e);
+        const real iff = inv_det * (a * d - b * b);
+        const real radius = ceil((3.f * fmax(s[0], fmax(s[1], s[2]))) /
+                                   fmin(vs3[2], fmin(vs3[1], vs3[0])));
+        real mean = 0.f;
         for (int ch = 0; ch < C; ++ch) mean += intens[(size_t)g * C + ch];
-        mean /= (float)C;
-        const float opt = gsv_logf(mean * GSV_ALPHA_THRESHOLD);
-        const float extent = fminf(3.f, sqrtf(2.0f * opt));
-        const float r3[3] = {fmaxf(0.0f, (sqrtf(cov[0][0]) * extent) - 0.5f),
-                             fmaxf(0.0f, (sqrtf(cov[1][1]) * extent) - 0.5f),
-                             fmaxf(0.0f, (sqrtf(cov[2][2]) * extent) - 0.5f)};
-        if (radius <= 0.f || pix[0] + radius < 0.f || pix[0] - radius > (float)W ||
-            pix[1] + radius < 0.f || pix[1] - radius > (float)H || pix[2] + radius < 0.f ||
-            pix[2] - radius > (float)D)
+        mean /= (real)C;
+        const real opt = orc_log(mean * GSV_ALPHA_THRESHOLD);
+        const real extent = fmin(3.f, sqrt(2.0f * opt));
+        const real r3[3] = {fmax(0.0f, (sqrt(cov[0][0]) * extent) - 0.5f),
+                             fmax(0.0f, (sqrt(cov[1][1]) * extent) - 0.5f),
+                             fmax(0.0f, (sqrt(cov[2][2]) * extent) - 0.5f)};
+        if (radius <= 0.f || pix[0] + radius < 0.f || pix[0] - radius > (real)W ||
+            pix[1] + radius < 0.f || pix[1] - radius > (real)H || pix[2] + radius < 0.f ||
+            pix[2] - radius > (real)D)
             continue;
         const int tb[3] = {Tx, Ty, Tz};
         int tmn[3], tmx[3];
         for (int k = 0; k < 3; ++k) {
-            tmn[k] = gsv_imin(tb[k], gsv_imax(0, gsv_f2i_sat((pix[k] - r3[k]) / (float)GSV_TILE)));
-            tmx[k] = gsv_imin(tb[k], gsv_imax(0, gsv_f2i_sat((pix[k] + r3[k] + (float)(GSV_TILE - 1)) /
-                                                              (float)GSV_TILE)));
+            tmn[k] = gsv_imin(tb[k], gsv_imax(0, gsv_f2i_sat((pix[k] - r3[k]) / (real)GSV_TILE)));
+            tmx[k] = gsv_imin(tb[k], gsv_imax(0, gsv_f2i_sat((pix[k] + r3[k] + (real)(GSV_TILE - 1)) /
+                                                              (real)GSV_TILE)));
         }
         const int tile_vol = (tmx[0] - tmn[0]) * (tmx[1] - tmn[1]) * (tmx[2] - tmn[2]);
         if (tile_vol <= 0) continue;
-        float *pr = pos_radii + 4 * (size_t)g;
+        real *pr = pos_radii + 4 * (size_t)g;
         pr[0] = pix[0]; pr[1] = pix[1]; pr[2] = pix[2]; pr[3] = radius;
         for (int k = 0; k < 3; ++k) {
             tile_min[3 * (size_t)g + k] = tmn[k];
             tile_max[3 * (size_t)g + k] = tmx[k];
         }
         num_tiles_hit[g] = tile_vol;
-        float *cn = conics + 6 * (size_t)g;
+        real *cn = conics + 6 * (size_t)g;
         cn[0] = ia; cn[1] = ib; cn[2] = ic; cn[3] = id; cn[4] = ie; cn[5] = iff;
     }
     return 0;
 }
 
 /* dL/d(voxel covariance) from dL/d(conic), get_cov_grad optim_to_render.cu:186-239. */
-static void cov_grad_from_conic_grad(mat3 cov, mat3 M2, const float *g, mat3 out) {
-    const float a = cov[0][0], b = cov[0][1], c = cov[0][2];
-    const float d = cov[1][1], e = cov[1][2], f = cov[2][2];
-    const float den = a * d * f + 2 * b * c * e - a * e * e - f * b * b - d * c * c;
-    const float den2inv = 1.0f / ((den * den) + 0.0000001f);
+static void cov_grad_from_conic_grad(mat3 cov, mat3 M2, const real *g, mat3 out) {
+    const real a = cov[0][0], b = cov[0][1], c = cov[0][2];
+    const real d = cov[1][1], e = cov[1][2], f = cov[2][2];
+    const real den = a * d * f + 2 * b * c * e - a * e * e - f * b * b - d * c * c;
+    const real den2inv = 1.0f / ((den * den) + 0.0000001f);
     m3_set(out, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f);
     if (den2inv == 0) return;
     /* cofactors and det partials */
-    const float k_a = d * f - e * e;
-    const float k_b = 2 * c * e - 2 * f * b;
-    const float k_c = 2 * b * e - 2 * d * c;
-    const float k_d = a * f - c * c;
-    const float k_e = 2 * b * c - 2 * a * e;
-    const float k_f = a * d - b * b;
-    const float n_b = c * e - b * f;
-    const float n_c = b * e - c * d;
-    const float n_e = b * c - a * e;
-    const float gA = g[0], gB = g[1], gC = g[2], gD = g[3], gE = g[4], gF = g[5];
-    const float da = den2inv * (-k_a * k_a * gA - n_b * k_a * gB - n_c * k_a * gC +
+    const real k_a = d * f - e * e;
+    const real k_b = 2 * c * e - 2 * f * b;
+    const real k_c = 2 * b * e - 2 * d * c;
+    const real k_d = a * f - c * c;
+    const real k_e = 2 * b * c - 2 * a * e;
+    const real k_f = a * d - b * b;
+    const real n_b = c * e - b * f;
+    const real n_c = b * e - c * d;
+    const real n_e = b * c - a * e;
+    const real gA = g[0], gB = g[1], gC = g[2], gD = g[3], gE = g[4], gF = g[5];
+    const real da = den2inv * (-k_a * k_a * gA - n_b * k_a * gB - n_c * k_a * gC +
                                 (f * den - k_d * k_a) * gD + (-e * den - n_e * k_a) * gE +
                                 (d * den - k_f * k_a) * gF);
-    const float db = den2inv * (-k_a * k_b * gA + (-f * den - n_b * k_b) * gB +
+    const real db = den2inv * (-k_a * k_b * gA + (-f * den - n_b * k_b) * gB +
                                 (e * den - n_c * k_b) * gC - k_d * k_b * gD +
                                 (c * den - n_e * k_b) * gE + (-2 * b * den - k_f * k_b) * gF);
-    const float dc = den2inv * (-k_a * k_c * gA + (e * den - n_b * k_c) * gB +
+    const real dc = den2inv * (-k_a * k_c * gA + (e * den - n_b * k_c) * gB +
                                 (-d * den - n_c * k_c) * gC + (-2 * c * den - k_d * k_c) * gD +
                                 (b * den - n_e * k_c) * gE - k_f * k_c * gF);
-    const float dd = den2inv * ((f * den - k_a * k_d) * gA - n_b * k_d * gB +
+    const real dd = den2inv * ((f * den - k_a * k_d) * gA - n_b * k_d * gB +
                                 (-c * den - n_c * k_d) * gC - k_d * k_d * gD - n_e * k_d * gE +
                                 (a * den - k_f * k_d) * gF);
-    const float de = den2inv * ((-2 * e * den - k_a * k_e) * gA + (c * den - n_b * k_e) * gB +
+    const real de = den2inv * ((-2 * e * den - k_a * k_e) * gA + (c * den - n_b * k_e) * gB +
                                 (b * den - n_c * k_e) * gC - k_d * k_e * gD +
                                 (-a * den - n_e * k_e) * gE + -k_f * k_e * gF);
-    const float df = den2inv * ((d * den - k_a * k_f) * gA + (-b * den - n_b * k_f) * gB -
+    const real df = den2inv * ((d * den - k_a * k_f) * gA + (-b * den - n_b * k_f) * gB -
                                 n_c * k_f * gC + (a * den - k_d * k_f) * gD - n_e * k_f * gE -
                                 k_f * k_f * gF);
     mat3 dhat, M2t, t;
@@ -213,21 +232,21 @@ static void cov_grad_from_conic_grad(mat3 cov, mat3 M2, const float *g, mat3 out
  * Pinned by: tests/test_oracle_projection.py (fp64 finite differences on dscale,
  * tangential dquat, dpos up to the reference's voxel-size factor).
  */
-int orc_project_bwd(int n, const float *pos3d, const float *scale3d, const float *quat, int D,
-                    int H, int W, float wz, float wy, float wx, float cz, float cy, float cx,
-                    const float *dpos_radii, const float *dconics, const float *pos_radii,
-                    float *dpos, float *dscale, float *dquat) {
+int orc_project_bwd(int n, const real *pos3d, const real *scale3d, const real *quat, int D,
+                    int H, int W, real wz, real wy, real wx, real cz, real cy, real cx,
+                    const real *dpos_radii, const real *dconics, const real *pos_radii,
+                    real *dpos, real *dscale, real *dquat) {
     (void)pos3d; (void)cz; (void)cy; (void)cx;
     if (n < 0) return 1;
-    const float vs3[3] = {wz / (float)D, wy / (float)H, wx / (float)W};
-    memset(dpos, 0, sizeof(float) * 3 * (size_t)n);
-    memset(dscale, 0, sizeof(float) * 3 * (size_t)n);
-    memset(dquat, 0, sizeof(float) * 4 * (size_t)n);
+    const real vs3[3] = {wz / (real)D, wy / (real)H, wx / (real)W};
+    memset(dpos, 0, sizeof(real) * 3 * (size_t)n);
+    memset(dscale, 0, sizeof(real) * 3 * (size_t)n);
+    memset(dquat, 0, sizeof(real) * 4 * (size_t)n);
 #pragma omp parallel for schedule(static)
     for (int g = 0; g < n; ++g) {
         if (pos_radii[4 * (size_t)g + 3] <= 0) continue;
-        const float *s = scale3d + 3 * (size_t)g;
-        const float *q = quat + 4 * (size_t)g;
+        const real *s = scale3d + 3 * (size_t)g;
+        const real *q = quat + 4 * (size_t)g;
         mat3 R, S, M2, cov, cg, dsig, Rg, Rgt, Rt, S2;
         voxel_covariance(s, q, vs3, R, S, M2, cov);
         cov_grad_from_conic_grad(cov, M2, dconics + 6 * (size_t)g, cg);
@@ -243,17 +262,17 @@ int orc_project_bwd(int n, const float *pos3d, const float *scale3d, const float
             dscale[3 * (size_t)g + i] = Rt[i][0] * Rgt[i][0] + Rt[i][1] * Rgt[i][1] + Rt[i][2] * Rgt[i][2];
         for (int i = 0; i < 3; ++i)
             for (int row = 0; row < 3; ++row) Rgt[i][row] *= s[i];
-        const float *dp = dpos_radii + 4 * (size_t)g;
+        const real *dp = dpos_radii + 4 * (size_t)g;
         dpos[3 * (size_t)g + 0] = dp[0] * vs3[2];
         dpos[3 * (size_t)g + 1] = dp[1] * vs3[1];
         dpos[3 * (size_t)g + 2] = dp[2] * vs3[0];
         /* rotmat_grad_to_quat_grad, optim_to_render_helpers.cuh:51-75 */
-        float qn[4];
+        real qn[4];
         mat3 Rdummy;
         quat_to_rotmat(q, Rdummy, qn);
-        const float w = qn[0], x = qn[1], y = qn[2], z = qn[3];
-        float (*v)[3] = Rgt;
-        float *o = dquat + 4 * (size_t)g;
+        const real w = qn[0], x = qn[1], y = qn[2], z = qn[3];
+        real (*v)[3] = Rgt;
+        real *o = dquat + 4 * (size_t)g;
         o[0] = 2 * z * (v[0][1] - v[1][0]) + 2 * y * (v[2][0] - v[0][2]) + 2 * x * (v[1][2] - v[2][1]);
         o[1] = 2 * y * (v[1][0] + v[0][1]) + 2 * z * (v[2][0] + v[0][2]) + 2 * w * (v[1][2] - v[2][1]) -
                4 * x * (v[2][2] + v[1][1]);
@@ -331,10 +350,13 @@ int orc_bin_and_sort(int n, int64_t n_isect, const int *tile_min, const int *til
  * evaluation orders (this oracle, the device, the reference's fast-math build)
  * can disagree on such terms; the tests allow their magnitude explicitly.
  */
-static int gate_ambiguous(float sigma, float mean) {
+static int gate_ambiguous(real sigma, real mean, real alpha) {
     if (isnan(sigma) || isinf(sigma) || !(mean > 0.f)) return 0;
-    if (fabsf(sigma) < 1e-5f) return 1;
+    if (fabs(sigma) < 1e-5f) return 1;
     if (sigma > 0.f) return 0;
+    /* alpha = exp(sigma) in the working type (a few ulp): far from the band
+     * when alpha*mean is off 1e-6 by more than twice its width */
+    if (fabs((double)alpha * (double)mean - 1e-6) > 2e-10) return 0;
     const double am = exp((double)sigma) * (double)mean;
     return fabs(am - 1e-6) <= 1e-4 * 1e-6;
 }
@@ -349,8 +371,8 @@ static int gate_ambiguous(float sigma, float mean) {
  * Pinned by: tests/test_oracle_voxelize.py (dense fp64 brute force, closed forms).
  */
 int orc_voxelize_fwd(int D, int H, int W, int C, const int *ids_sorted, const int *tile_bins,
-                     const float *pos_radii, const float *conics, const float *intens, float *out,
-                     float *amb, int64_t tile_begin, int64_t tile_end) {
+                     const real *pos_radii, const real *conics, const real *intens, real *out,
+                     real *amb, int64_t tile_begin, int64_t tile_end) {
     if (C < 1 || C > GSV_MAX_CHANNELS) return 1;
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H);
     const int64_t T = (int64_t)Tx * Ty * gsv_tiles_along(D);
@@ -364,28 +386,29 @@ int orc_voxelize_fwd(int D, int H, int W, int C, const int *ids_sorted, const in
                 for (int lx = 0; lx < GSV_TILE; ++lx) {
                     const int i = tz * GSV_TILE + lz, j = ty * GSV_TILE + ly, k = tx * GSV_TILE + lx;
                     if (i >= D || j >= H || k >= W) continue;
-                    const float px = (float)k + 0.5f, py = (float)j + 0.5f, pz = (float)i + 0.5f;
-                    float acc[GSV_MAX_CHANNELS] = {0.f, 0.f, 0.f, 0.f};
-                    float am[GSV_MAX_CHANNELS] = {0.f, 0.f, 0.f, 0.f};
+                    const real px = (real)k + 0.5f, py = (real)j + 0.5f, pz = (real)i + 0.5f;
+                    real acc[GSV_MAX_CHANNELS] = {0.f, 0.f, 0.f, 0.f};
+                    real am[GSV_MAX_CHANNELS] = {0.f, 0.f, 0.f, 0.f};
                     for (int idx = r0; idx < r1; ++idx) {
                         const int g = ids_sorted[idx];
-                        const float *xyz = pos_radii + 4 * (size_t)g;
-                        const float *cn = conics + 6 * (size_t)g;
-                        const float dx = xyz[0] - px, dy = xyz[1] - py, dz = xyz[2] - pz;
-                        const float sigma = -0.5f * (cn[0] * dx * dx + cn[3] * dy * dy + cn[5] * dz * dz) -
+                        const real *xyz = pos_radii + 4 * (size_t)g;
+                        const real *cn = conics + 6 * (size_t)g;
+                        const real dx = xyz[0] - px, dy = xyz[1] - py, dz = xyz[2] - pz;
+                        const real sigma = -0.5f * (cn[0] * dx * dx + cn[3] * dy * dy + cn[5] * dz * dz) -
                                             (cn[1] * dx * dy + cn[2] * dx * dz + cn[4] * dy * dz);
-                        float mean = 0.f;
+                        real mean = 0.f;
                         for (int ch = 0; ch < C; ++ch) mean += intens[(size_t)g * C + ch];
-                        mean /= (float)C;
-                        if (amb && gate_ambiguous(sigma, mean))
+                        mean /= (real)C;
+                        /* exp(sigma) wherever sigma <= 0 (the only case used below) */
+                        const real alpha = exp(fmin(sigma, 0.f));
+                        if (amb && gate_ambiguous(sigma, mean, alpha))
                             for (int ch = 0; ch < C; ++ch)
-                                am[ch] += fabsf(intens[(size_t)g * C + ch] * expf(fminf(sigma, 0.f)));
+                                am[ch] += fabs(intens[(size_t)g * C + ch] * alpha);
                         if (sigma > 0.f || isnan(sigma) || isinf(sigma)) continue;
-                        const float alpha = expf(sigma);
                         if (alpha * mean < GSV_MIN_CONTRIB) continue;
                         for (int ch = 0; ch < C; ++ch) acc[ch] += intens[(size_t)g * C + ch] * alpha;
                     }
-                    float *o = out + ((((size_t)i * H + j) * W) + k) * C;
+                    real *o = out + ((((size_t)i * H + j) * W) + k) * C;
                     for (int ch = 0; ch < C; ++ch) o[ch] = acc[ch];
                     if (amb)
                         for (int ch = 0; ch < C; ++ch) amb[((((size_t)i * H + j) * W) + k) * C + ch] = am[ch];
@@ -396,8 +419,8 @@ int orc_voxelize_fwd(int D, int H, int W, int C, const int *ids_sorted, const in
 
 /*
  * Backward voxelization: voxelize_backward_per_gaussian (voxelize.cu:368-574).
- * For each (tile, Gaussian) pair the per-voxel terms are summed in binary32 in
- * the kernel's voxel order (z, then y, then x within the tile), as one lane of
+ * For each (tile, Gaussian) pair the per-voxel terms are summed in the
+ * arithmetic type (binary32 by default) in the kernel's voxel order (z, then y, then x within the tile), as one lane of
  * the reference does; the per-pair partials are then added into each
  * Gaussian's gradient in binary64, in sorted pair order (the reference uses
  * float atomics in an unspecified order).  Outputs are zeroed first
@@ -412,8 +435,8 @@ int orc_voxelize_fwd(int D, int H, int W, int C, const int *ids_sorted, const in
  * Pinned by: tests/test_oracle_voxelize.py (torch autograd of a dense fp64
  * evaluation of the forward, and central finite differences).
  */
-static void bwd_terms(float sg, float dd, const float *vg, int C, float dx, float dy, float dz,
-                      const float *cn, float *term) {
+static void bwd_terms(real sg, real dd, const real *vg, int C, real dx, real dy, real dz,
+                      const real *cn, real *term) {
     for (int ch = 0; ch < C; ++ch) term[9 + ch] = dd * vg[ch];
     term[0] = -0.5f * sg * dx * dx;
     term[1] = -sg * dx * dy;
@@ -427,26 +450,26 @@ static void bwd_terms(float sg, float dd, const float *vg, int C, float dx, floa
 }
 
 int orc_voxelize_bwd(int D, int H, int W, int C, int n, const int *ids_sorted, const int *tile_bins,
-                     const float *pos_radii, const float *conics, const float *intens,
-                     const float *vol_grad, float *dpos_radii, float *dconics, float *dintens,
-                     float *abs_pos, float *abs_conics, float *abs_intens, float *amb_pos,
-                     float *amb_conics, float *amb_intens, int64_t tile_begin, int64_t tile_end) {
+                     const real *pos_radii, const real *conics, const real *intens,
+                     const real *vol_grad, real *dpos_radii, real *dconics, real *dintens,
+                     real *abs_pos, real *abs_conics, real *abs_intens, real *amb_pos,
+                     real *amb_conics, real *amb_intens, int64_t tile_begin, int64_t tile_end) {
     if (C < 1 || C > GSV_MAX_CHANNELS) return 1;
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H);
     const int64_t T = (int64_t)Tx * Ty * gsv_tiles_along(D);
     if (tile_end > T) tile_end = T;
     const int NV = 9 + C;
     const int want_abs = abs_pos != NULL, want_amb = amb_pos != NULL;
-    memset(dpos_radii, 0, sizeof(float) * 4 * (size_t)n);
-    memset(dconics, 0, sizeof(float) * 6 * (size_t)n);
-    memset(dintens, 0, sizeof(float) * (size_t)C * n);
-    float *outs[3][3] = {{dconics, dpos_radii, dintens}, {abs_conics, abs_pos, abs_intens},
+    memset(dpos_radii, 0, sizeof(real) * 4 * (size_t)n);
+    memset(dconics, 0, sizeof(real) * 6 * (size_t)n);
+    memset(dintens, 0, sizeof(real) * (size_t)C * n);
+    real *outs[3][3] = {{dconics, dpos_radii, dintens}, {abs_conics, abs_pos, abs_intens},
                          {amb_conics, amb_pos, amb_intens}};
     for (int k = 1; k < 3; ++k)
         if (outs[k][0]) {
-            memset(outs[k][0], 0, sizeof(float) * 6 * (size_t)n);
-            memset(outs[k][1], 0, sizeof(float) * 4 * (size_t)n);
-            memset(outs[k][2], 0, sizeof(float) * (size_t)C * n);
+            memset(outs[k][0], 0, sizeof(real) * 6 * (size_t)n);
+            memset(outs[k][1], 0, sizeof(real) * 4 * (size_t)n);
+            memset(outs[k][2], 0, sizeof(real) * (size_t)C * n);
         }
     if (tile_begin >= tile_end) return 0;
     /* pairs are sorted by tile, so the pairs of a tile range are contiguous */
@@ -458,7 +481,9 @@ int orc_voxelize_bwd(int D, int H, int W, int C, int n, const int *ids_sorted, c
     }
     if (p1 <= p0) return 0;
     const int64_t npairs = p1 - p0;
-    float *part = (float *)calloc((size_t)npairs * NV * 3, sizeof(float));
+    /* per pair: the partial sums, then (with diagnostics) |term| and ambiguous sums */
+    const int K = (want_abs || want_amb) ? 3 : 1;
+    real *part = (real *)calloc((size_t)npairs * NV * K, sizeof(real));
     if (!part) return 3;
 #pragma omp parallel for schedule(dynamic, 4)
     for (int64_t t = tile_begin; t < tile_end; ++t) {
@@ -466,46 +491,48 @@ int orc_voxelize_bwd(int D, int H, int W, int C, int n, const int *ids_sorted, c
         const int r0 = tile_bins[2 * t], r1 = tile_bins[2 * t + 1];
         for (int idx = r0; idx < r1; ++idx) {
             const int g = ids_sorted[idx];
-            const float *xyz = pos_radii + 4 * (size_t)g;
-            const float *cn = conics + 6 * (size_t)g;
-            const float *I = intens + (size_t)g * C;
-            float mean = 0.f;
-            for (int ch = 0; ch < C; ++ch) mean += I[ch];
-            mean /= (float)C;
-            float acc[13] = {0}, aac[13] = {0}, amb[13] = {0}, term[13];
+            const real *xyz = pos_radii + 4 * (size_t)g;
+            const real *cn = conics + 6 * (size_t)g;
+            const real *Ig = intens + (size_t)g * C;
+            real mean = 0.f;
+            for (int ch = 0; ch < C; ++ch) mean += Ig[ch];
+            mean /= (real)C;
+            real acc[13] = {0}, aac[13] = {0}, amb[13] = {0}, term[13];
             for (int v = 0; v < GSV_TILE_VOXELS; ++v) {
                 const int lz = v / 64, ly = (v / 8) % 8, lx = v % 8;
                 const int gx = tx * GSV_TILE + lx, gy = ty * GSV_TILE + ly, gz = tz * GSV_TILE + lz;
                 if (gx >= W || gy >= H || gz >= D) continue;
-                const float px = (float)gx + 0.5f, py = (float)gy + 0.5f, pz = (float)gz + 0.5f;
-                const float *vg = vol_grad + ((((size_t)gz * H + gy) * W) + gx) * C;
-                const float dx = xyz[0] - px, dy = xyz[1] - py, dz = xyz[2] - pz;
-                const float sigma = -0.5f * (cn[0] * dx * dx + cn[3] * dy * dy + cn[5] * dz * dz) -
+                const real px = (real)gx + 0.5f, py = (real)gy + 0.5f, pz = (real)gz + 0.5f;
+                const real *vg = vol_grad + ((((size_t)gz * H + gy) * W) + gx) * C;
+                const real dx = xyz[0] - px, dy = xyz[1] - py, dz = xyz[2] - pz;
+                const real sigma = -0.5f * (cn[0] * dx * dx + cn[3] * dy * dy + cn[5] * dz * dz) -
                                     (cn[1] * dx * dy + cn[2] * dx * dz + cn[4] * dy * dz);
-                if (want_amb && gate_ambiguous(sigma, mean)) {
-                    const float da = expf(fminf(sigma, 0.f));
-                    float sa = 0.f;
-                    for (int ch = 0; ch < C; ++ch) sa += I[ch] * vg[ch];
-                    bwd_terms(sa * da, da, vg, C, dx, dy, dz, cn, term);
-                    for (int q = 0; q < NV; ++q) amb[q] += fabsf(term[q]);
+                /* exp(sigma) wherever sigma <= 0 (the only case used below) */
+                const real dd = exp(fmin(sigma, 0.f));
+                if (want_amb && gate_ambiguous(sigma, mean, dd)) {
+                    real sa = 0.f;
+                    for (int ch = 0; ch < C; ++ch) sa += Ig[ch] * vg[ch];
+                    bwd_terms(sa * dd, dd, vg, C, dx, dy, dz, cn, term);
+                    for (int q = 0; q < NV; ++q) amb[q] += fabs(term[q]);
                 }
                 if (sigma > 0.f || isnan(sigma) || isinf(sigma)) continue;
-                const float dd = expf(sigma);
                 if (dd * mean < GSV_MIN_CONTRIB) continue;
-                float sg = 0.f;
-                for (int ch = 0; ch < C; ++ch) sg += I[ch] * vg[ch];
+                real sg = 0.f;
+                for (int ch = 0; ch < C; ++ch) sg += Ig[ch] * vg[ch];
                 sg *= dd;
                 bwd_terms(sg, dd, vg, C, dx, dy, dz, cn, term);
                 for (int q = 0; q < NV; ++q) {
                     acc[q] += term[q];
-                    aac[q] += fabsf(term[q]);
+                    aac[q] += fabs(term[q]);
                 }
             }
-            float *dst = part + (size_t)(idx - p0) * NV * 3;
+            real *dst = part + (size_t)(idx - p0) * NV * K;
             for (int q = 0; q < NV; ++q) {
                 dst[q] = acc[q];
-                dst[NV + q] = aac[q];
-                dst[2 * NV + q] = amb[q];
+                if (K == 3) {
+                    dst[NV + q] = aac[q];
+                    dst[2 * NV + q] = amb[q];
+                }
             }
         }
     }
@@ -515,9 +542,9 @@ int orc_voxelize_bwd(int D, int H, int W, int C, int n, const int *ids_sorted, c
         const int r0 = tile_bins[2 * t], r1 = tile_bins[2 * t + 1];
         for (int idx = r0; idx < r1; ++idx) {
             const int g = ids_sorted[idx];
-            const float *src = part + (size_t)(idx - p0) * NV * 3;
+            const real *src = part + (size_t)(idx - p0) * NV * K;
             double *dst = gacc + (size_t)g * NV * 3;
-            for (int q = 0; q < 3 * NV; ++q) dst[q] += (double)src[q];
+            for (int q = 0; q < K * NV; ++q) dst[q] += (double)src[q];
         }
     }
     for (int g = 0; g < n; ++g) {
@@ -525,9 +552,9 @@ int orc_voxelize_bwd(int D, int H, int W, int C, int n, const int *ids_sorted, c
             if (k == 1 && !want_abs) continue;
             if (k == 2 && !want_amb) continue;
             const double *a = gacc + (size_t)g * NV * 3 + (size_t)k * NV;
-            for (int q = 0; q < 6; ++q) outs[k][0][6 * (size_t)g + q] = (float)a[q];
-            for (int q = 0; q < 3; ++q) outs[k][1][4 * (size_t)g + q] = (float)a[6 + q];
-            for (int ch = 0; ch < C; ++ch) outs[k][2][(size_t)g * C + ch] = (float)a[9 + ch];
+            for (int q = 0; q < 6; ++q) outs[k][0][6 * (size_t)g + q] = (real)a[q];
+            for (int q = 0; q < 3; ++q) outs[k][1][4 * (size_t)g + q] = (real)a[6 + q];
+            for (int ch = 0; ch < C; ++ch) outs[k][2][(size_t)g * C + ch] = (real)a[9 + ch];
         }
     }
     free(gacc);

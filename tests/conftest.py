@@ -36,3 +36,21 @@ def binning_path(request, monkeypatch):
     else:
         monkeypatch.setenv("GSV_BINNING", request.param)
     return request.param
+
+
+@pytest.fixture
+def set_chains():
+    """A setter of the backward's chained rows for one test
+    (gs_voxelizer.cuda.set_backward_chains); the setting before the test is
+    restored afterwards."""
+    import gs_voxelizer.cuda as _C
+    saved = []
+
+    def _set(enabled: bool) -> None:
+        prev = _C.set_backward_chains(enabled)
+        if not saved:
+            saved.append(prev)
+
+    yield _set
+    if saved:
+        _C.set_backward_chains(saved[0])

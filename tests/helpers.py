@@ -80,6 +80,56 @@ def report_close(name, got, ref, rtol, atol, bound=None, log_only=False):
                              f"rtol={rtol} atol={atol}; worst {worst}")
 
 
+def accuracy(got, truth, allow_extra=None, rtol=1e-4, atol=1e-6):
+    """(count, worst) of `got` against a binary64 `truth`: how many elements lie
+    outside atol + rtol*|truth| (+ allow_extra, the gate-ambiguous mass), and the
+    largest |got - truth| / that bound (NaN against a non-NaN counts as outside
+    and as an infinite error)."""
+    got = np.asarray(got, dtype=np.float64)
+    truth = np.asarray(truth, dtype=np.float64)
+    assert got.shape == truth.shape, (got.shape, truth.shape)
+    allow = atol + rtol * np.abs(truth)
+    if allow_extra is not None:
+        allow = allow + np.asarray(allow_extra, dtype=np.float64)
+    both_nan = np.isnan(got) & np.isnan(truth)
+    with np.errstate(invalid="ignore"):
+        err = np.where(both_nan, 0.0, np.abs(got - truth))
+    err = np.where(np.isnan(err), np.inf, err)
+    ratio = err / allow
+    return int((ratio > 1.0).sum()), float(ratio.max()) if ratio.size else 0.0
+
+
+# How much less accurate than the binary32 oracle the device may be, per
+# comparison against the binary64 truth: at most COUNT_SLACK_REL * the oracle's
+# count + COUNT_SLACK_ABS elements outside the bound, and a worst normalised
+# error of at most WORST_FACTOR * the oracle's (or 1, inside the bound).
+COUNT_SLACK_REL, COUNT_SLACK_ABS, WORST_FACTOR = 0.25, 2, 2.0
+
+
+def assert_no_less_accurate(name, got, oracle32, truth, allow_extra=None, rtol=1e-4, atol=1e-6):
+    """The device result `got` is no less accurate than the binary32 oracle's
+    `oracle32` against the binary64 `truth` (each within atol + rtol*|truth| +
+    allow_extra per element): its count of elements outside that bound is at
+    most the oracle's plus the slack above, and its worst normalised error at
+    most WORST_FACTOR times the oracle's, or 1.  Both statistics are logged
+    (GSV_MARGIN_LOG: name, elements, device count, oracle count, device worst,
+    oracle worst)."""
+    n_dev, w_dev = accuracy(got, truth, allow_extra, rtol, atol)
+    n_orc, w_orc = accuracy(oracle32, truth, allow_extra, rtol, atol)
+    log = os.environ.get("GSV_MARGIN_LOG")
+    if log:
+        with open(log, "a") as f:
+            f.write(f"{name}\t{np.size(truth)}\tdev {n_dev}\torc {n_orc}\t"
+                    f"{w_dev:.4g}\t{w_orc:.4g}\n")
+    n_max = int(n_orc + COUNT_SLACK_REL * n_orc + COUNT_SLACK_ABS)
+    w_max = max(1.0, WORST_FACTOR * w_orc)
+    assert n_dev <= n_max and w_dev <= w_max, (
+        f"{name}: device {n_dev} elements outside rel {rtol} / abs {atol} of the binary64 "
+        f"truth (worst {w_dev:.4g} of the bound), binary32 oracle {n_orc} (worst {w_orc:.4g}); "
+        f"allowed {n_max} (worst {w_max:.4g})")
+    return n_dev, n_orc, w_dev, w_orc
+
+
 def l1_vol_grad(vol, target):
     """Gradient of mean |vol - target| w.r.t. vol (torch.nn.functional.l1_loss)."""
     return (np.sign(vol.astype(np.float64) - target.astype(np.float64)) / vol.size).astype(np.float32)

@@ -98,7 +98,7 @@ def test_forward_first_tile_layer(full):
     assert float(vol[8:].abs().sum()) > 0
 
 
-def test_backward_intensity_identity(full, monkeypatch):
+def test_backward_intensity_identity(full, set_chains):
     import gs_voxelizer.cuda as _C
     P = full
     cfg = P["work"].cfg
@@ -135,7 +135,7 @@ def test_backward_intensity_identity(full, monkeypatch):
     for a, b in zip((dp, dc, di), bwd(pair_live=live)):
         gap = float(torch.linalg.vector_norm((a - b).double()))
         assert gap <= 1e-4 * float(torch.linalg.vector_norm(a.double())), (cfg.name, gap)
-    monkeypatch.setenv("GSV_BWD_CHAIN", "0")
+    set_chains(False)
     for a, b in zip(bwd(), bwd(pair_live=live)):
         assert torch.equal(a, b)
 

@@ -15,7 +15,7 @@ ellipsoid, and reports its decision per sorted pair (pair_live).  Checked here:
   for the culled ones) returns the same bits as without them, for vol_grad and
   fused-L1 sources, in host-count and capacity (device-count) modes, including
   sparse scenes whose waves span more tiles than one wave stages.  That holds
-  with the backward's chained rows off (GSV_BWD_CHAIN=0): with them on, a
+  with the backward's chained rows off (set_backward_chains(False)): with them on, a
   group of pairs takes them only when all of its pairs qualify, and the flags
   change which pairs share a wave, so there the two agree to rounding
   (rel 1e-4 / abs 1e-6) instead;
@@ -126,9 +126,9 @@ def _agree(what, a, b, exact):
 
 @pytest.mark.parametrize("chain", ["0", "1"], ids=["chain_off", "chain_on"])
 @pytest.mark.parametrize("name,work", CASES, ids=IDS)
-def test_backward_with_cull_flags_is_bitwise_equal(device, monkeypatch, name, work, chain):
+def test_backward_with_cull_flags_is_bitwise_equal(device, set_chains, name, work, chain):
     import gs_voxelizer.cuda as _C
-    monkeypatch.setenv("GSV_BWD_CHAIN", chain)
+    set_chains(chain == "1")
     exact = chain == "0"
     R = _run(work, device)
     cfg, w = work.cfg, R["w"]
@@ -222,3 +222,49 @@ def _C_api_backward(R, cfg, gd, with_flags):
                                              w.intensities, gd, R["tmin"], R["tmax"], R["cum"],
                                              tiles_sorted=R["tiles"],
                                              pair_live=R["live"] if with_flags else None)
+
+
+def test_very_thin_gaussians_are_not_culled_from_tiles_they_reach(device):
+    """Conics with one diagonal entry of 1e38 (det >= 2^126, whose binary32
+    reciprocal flushes to zero) and a mean intensity of 5e-6 (so the gate's
+    K^2 stays below 3.4 and K^2 * 1e38 finite): each Gaussian's centre sits
+    on a voxel-centre plane across its thin axis and 0.3 voxel below a tile
+    face in a wide one, 0.8 voxel from the first voxel centre of the next
+    tile, which passes its gates.  No pair whose tile holds a passing voxel
+    may be culled, and the volume matches the oracle's (channel 0, intensity
+    1, carries ~0.7 there; channel 1 is -0.99999, so the mean is 5e-6)."""
+    import gs_voxelizer.cuda as _C
+    import oracle as O
+    vol = (24, 24, 24)
+    big = 1e38
+    # thin along z, along x, along y; centre 0.3 voxel below a tile face in
+    # a wide axis, on a voxel-centre plane in the thin one
+    pr = np.array([[7.7, 11.5, 3.5, 1.0], [3.5, 7.7, 11.5, 1.0], [11.5, 3.5, 7.7, 1.0]],
+                  np.float32)
+    cn = np.array([[1, 0, 0, 1, 0, big], [big, 0, 0, 1, 0, 1], [1, 0, 0, big, 0, 1]],
+                  np.float32)
+    inten = np.tile(np.array([[1.0, -0.99999]], np.float32), (3, 1))
+    # boxes (x, y, z) of two tiles across the face plus the tile holding the centre
+    tmin = np.array([[0, 1, 0], [0, 0, 1], [1, 0, 0]], np.int32)
+    tmax = np.array([[2, 2, 1], [1, 2, 2], [2, 1, 2]], np.int32)
+    nt = np.prod(tmax - tmin, 1).astype(np.int32)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    cum, total = _C.cumsum_tiles_hit(dev(nt))
+    I = int(total.item())
+    ids, bins, tiles = _C.bin_and_sort_gaussians(3, I, dev(tmin), dev(tmax), cum, vol,
+                                                 return_tiles=True)
+    live = torch.full((I,), 7, device=device, dtype=torch.uint8)
+    out = _C.voxelize_forward(vol, ids, bins, dev(pr), dev(cn), dev(inten), pair_live=live)
+    torch.cuda.synchronize()
+    flags, ids_np, tiles_np = np32(live), np32(ids), np32(tiles)
+    cfg = type("Cfg", (), {"vol": vol})
+    passing = [_passing(cfg, pr.astype(np.float64), cn.astype(np.float64),
+                        inten.astype(np.float64), int(g), int(t))
+               for g, t in zip(ids_np, tiles_np)]
+    assert sum(passing) == 6, passing  # both tiles of every box hold a passing voxel
+    for p, (ok, f) in enumerate(zip(passing, flags)):
+        assert not (ok and f == 0), ("culled a reachable tile", p, int(ids_np[p]),
+                                     int(tiles_np[p]))
+    ref, amb = O.voxelize_fwd(vol, ids_np, np32(bins), pr, cn, inten, with_amb=True)
+    report_close("very thin Gaussians: volume", np32(out), ref, 1e-4, 1e-6, bound=amb)
+    assert ref[..., 0].max() > 0.3

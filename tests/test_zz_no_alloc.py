@@ -58,12 +58,13 @@ def _bin_both(work, device):
     return I, out, (tmin, tmax, cum)
 
 
-def test_noalloc_binning_matches_workspace_binning_twice(device):
+def test_noalloc_binning_matches_workspace_binning_twice(device, binning_path):
+    """Through each sort path (GSV_BINNING) and the library's own choice."""
     works = [("cfg3_full", S.make_gaussians(S.CONFIGS[3], seed=0)),
              ("cfg1_smaller", S.make_gaussians(S.CONFIGS[1], seed=1))]
     sizes = []
     for name, work in works:
-        print(f"noalloc binning: {name}", flush=True)
+        print(f"noalloc binning: {name}, path {binning_path}", flush=True)
         I, ((ids_a, bins_a, tiles_a), (ids_b, bins_b, tiles_b)), (tmin, tmax, cum) = \
             _bin_both(work, device)
         assert 0 < I <= MAX_PAIRS
@@ -98,3 +99,47 @@ def test_noalloc_binning_empty_and_limit(device):
                                     16, 24, 32, _ptr(bins), _ptr(bins), ctypes.c_void_p(0),
                                     stream)
     assert st == 6
+
+
+def test_noalloc_falls_back_to_lsd_when_bucket_counts_do_not_fit(device):
+    """3.5M one-tile Gaussians on a 512^3 grid (18-bit keys, 1024 buckets): the
+    bucket path's counts, 1024 per 256 Gaussians (56 MB), exceed the scratch
+    array, so the allocation-free entry takes the LSD passes while the
+    workspace entry takes the bucket path; both give the oracle's bits."""
+    L = _lib.load()
+    D = H = W = 512
+    n = 3_500_000
+    g = torch.Generator().manual_seed(5)
+    tmin = torch.randint(0, 64, (n, 3), generator=g, dtype=torch.int32)
+    tmax = tmin + 1
+    cum = torch.arange(1, n + 1, dtype=torch.int32)
+    I = n
+    assert I <= MAX_PAIRS
+    T = 64 ** 3
+    dev = [t.to(device) for t in (tmin, tmax, cum)]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ws_bytes = ctypes.c_size_t(0)
+    assert L.gsv_bin_workspace_bytes(n, I, D, H, W, ctypes.byref(ws_bytes)) == 0
+    assert ws_bytes.value > 52431104  # the bucket layout alone outgrows the scratch
+    ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=device)
+    out = []
+    for noalloc in (False, True):
+        print(f"noalloc LSD fallback: noalloc={noalloc}", flush=True)
+        ids = torch.full((I,), -7, dtype=torch.int32, device=device)
+        tiles = torch.full((I,), -7, dtype=torch.int32, device=device)
+        bins = torch.full((T, 2), -7, dtype=torch.int32, device=device)
+        if noalloc:
+            st = L.gsv_bin_and_sort_noalloc(n, I, _ptr(dev[0]), _ptr(dev[1]), _ptr(dev[2]), D, H,
+                                            W, _ptr(ids), _ptr(bins), _ptr(tiles), stream)
+        else:
+            st = L.gsv_bin_and_sort(n, I, _ptr(dev[0]), _ptr(dev[1]), _ptr(dev[2]), D, H, W,
+                                    _ptr(ws), ws_bytes, _ptr(ids), _ptr(bins), _ptr(tiles),
+                                    stream)
+        assert st == 0, L.gsv_status_string(st)
+        torch.cuda.synchronize()
+        out.append((ids.cpu().numpy(), bins.cpu().numpy(), tiles.cpu().numpy()))
+    for a, b, what in zip(out[0], out[1], ("gaussian_ids_sorted", "tile_bins", "tiles_sorted")):
+        np.testing.assert_array_equal(b, a, err_msg=what)
+    ref_ids, ref_bins = O.bin_and_sort(n, I, tmin.numpy(), tmax.numpy(), cum.numpy(), (D, H, W))
+    np.testing.assert_array_equal(out[1][0], ref_ids)
+    np.testing.assert_array_equal(out[1][1], ref_bins)
