@@ -656,27 +656,33 @@ struct Moments {
 // dy, planes in dz.
 // Taking moments about the Gaussian (not the tile) keeps every sum
 // well-conditioned: h is large only where |delta| is small.
-//   kGateFree: a = exp2(sigma2 + bound), zero below the threshold by the
-//              hardware flush (bound = the gate-free offset, shift unused).
-//              Along a row sigma2 + bound = S0 + P_k - p' S1 with
-//              p' = u - 3.5 = +-(k + 1/2): S0 and S1 are the form and its
-//              x-slope at the row centre, P_k = A2 p'^2 + bound is per lane, so
-//              the voxels u and 7 - u share S0 + P_k (at C = 2 the four P_k
-//              cost a wave per SIMD, 5 -> 4, and still gain ~6 %; at C >= 3
-//              the staged tiles' LDS limits occupancy first);
-//   kChain (gate-free too): a row's a from two v_exp_f32 instead of eight,
+// Every path evaluates the form in the offsets from the Gaussian, as the
+// reference forms sigma: per row R1 = Bn dy + Cn dz and R0 = Dn dy^2 + En dy dz
+// + Fn dz^2 (+ a per-path constant), and sigma2 = R0 + dx (R1 + A2 dx) at the
+// voxel dx_u.  (An expansion about the tile centre saves an operation per
+// voxel but its terms reach ~12 |A2| times the squared tile half-width and
+// cancel near a small Gaussian: ~5x the rounding of each a.)
+//   kGateFree: a = exp2(sigma2) * 2^bound, zero below the threshold by the
+//              flush of the product (bound = the gate-free offset, shift
+//              unused; 2^bound is one v_exp_f32 per lane).  The offset stays
+//              out of the exponent: an argument near -100 rounds to ~8e-6 in
+//              binary32, ~3e-6 relative in a;
+//   kChain (gate-free too): a row's a from three v_exp_f32 instead of eight,
 //              as products, which the binary32 flush-to-zero mode gates like
-//              v_exp_f32: E = S0 + bound + K - p' S1 from 2^E at p' = -3.5 and
-//              p' = +0.5, each stepped three times by 2^-S1, times the lane's
-//              2^(A2 p'^2 - K); the step itself is the previous row's times
-//              2^Bn.  K (chain_shift) keeps every product of a chain up to a
-//              passing voxel above 2^-126 and every factor finite;
+//              v_exp_f32: a_u = 2^E_u * G_u with the lane's column factors
+//              G_u = 2^(A2 (dx_u - d)^2 - K) and E_u the rest of the exponent,
+//              linear in u (dx falls by 1 per column): 2^E at u = 0 and u = 4,
+//              each stepped three times.  chain_shift picks d = 0 (factors
+//              about the Gaussian's centre: E's terms stay near sigma2's own
+//              size) or, where that does not qualify, d = mx (about the tile
+//              centre), and K, which keeps every factor finite and every
+//              product of a chain up to a passing voxel above 2^-126;
 //   otherwise: a = exp2(s) if |s| <= bound, s = sigma2 - shift.
 template <int C, bool kGateFree, bool kChain = false>
 __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int nz,
                                              float mxl, float myl, float mzl, float A2, float Bn,
                                              float Cn, float Dn, float En, float Fn, float shift,
-                                             float bound, float K, const float (&I)[C],
+                                             float bound, float K, float dch, const float (&I)[C],
                                              Moments<C> &M) {
     static_assert(kGateFree || !kChain, "the chained rows are gate-free");
     // Sxx is only needed whole: the loop sums h per voxel column (col[u], a
@@ -689,33 +695,37 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
         col[u] = 0.f;
     }
     constexpr bool kSym = kGateFree && !kChain;
-    float P[4];  // kSym: A2 p'^2 + bound;  kChain: 2^(A2 p'^2 - K), both at |p'| = k + 1/2
-    const float A2m = A2 * mxl, Bm = Bn * mxl, Cm = Cn * mxl;
-    if (kSym) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) P[k] = fmaf(A2, (0.5f + k) * (0.5f + k), bound);
-    }
+    // kSym: 2^bound, a normal number on live lanes (bound in [-126, -66]) and 0
+    // at the dead offset, where sigma2 is 0 (a zero form) and a = 1 * 0
+    const float Fb = kSym ? __builtin_amdgcn_exp2f(bound) : 0.f;
+    // kChain: G_u = 2^(A2 (dx_u - d)^2 - K) about dx = d (chain_shift's choice:
+    // 0, the Gaussian's centre, or mx, the tile's).  A2 (dx_u - d)^2 is formed
+    // with its rounding residual (two FMAs), applied as the factor
+    // 1 + lo ln 2, so each G_u is within ~1e-7 of its value; 2^-K is applied
+    // exactly.  Then E_u = sigma2 + off - A2 (dx_u - d)^2 + K
+    //   = dx_u (R1 + 2 A2 d) + R0 - A2 d^2 + off + K:
+    // the slope and constant take 2 A2 d and -A2 d^2 (both 0 for d = 0).
+    float G[GSV_TILE];
     if (kChain) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k)  // 2^-K applied exactly: the exp2 argument stays small
-            P[k] = ldexpf(__builtin_amdgcn_exp2f(A2 * ((0.5f + k) * (0.5f + k))), -(int)K);
+        for (int u = 0; u < GSV_TILE; ++u) {
+            const float x = dch == 0.f ? dxu[u] : (float)u - 3.5f;  // dx_u - d, up to sign
+            const float p = A2 * x;
+            const float plo = fmaf(A2, x, -p);
+            const float hi = p * x;
+            const float lo = fmaf(plo, x, fmaf(p, x, -hi));
+            G[u] = ldexpf(__builtin_amdgcn_exp2f(hi) * fmaf(lo, kLn2, 1.0f), -(int)K);
+        }
     }
-    const float K0base = kChain ? fmaf(A2m, mxl, bound + K) : A2m * mxl;
-    // kChain: a row's step 2^-S1 is the previous row's times 2^Bn (S1 falls by
-    // Bn per row), one v_mul_f32 instead of a v_exp_f32; the first row of each
-    // plane takes its own exp2
-    const float rB = kChain ? __builtin_amdgcn_exp2f(Bn) : 0.f;
+    // the constant of R0: the chain's offset, shift and -A2 d^2, the exact
+    // path's shift; the chain's slope adds 2 A2 d
+    const float c0 =
+        kChain ? fmaf(-A2 * dch, dch, bound + K) : (kGateFree ? 0.f : -shift);
+    const float s0 = kChain ? 2.0f * A2 * dch : 0.f;
     for (int lz = 0; lz < nz; ++lz) {
         const float dz = mzl - ((float)lz - 3.5f);
-        const float Cdz = Cn * dz, Edz = En * dz;
-        // gate-free: S1 = Bn dy + K1, S0 = dy (Dn dy + L1) + K0
-        const float K1 = fmaf(2.0f, A2m, Cdz), L1 = Bm + Edz;
-        const float K0 = fmaf(dz, fmaf(Fn, dz, Cm), K0base);
-        // kChain: the exponent at p' = -3.5, S0 + 3.5 S1 = dy (Dn dy + L1a) + K0a
-        const float L1a = kChain ? fmaf(3.5f, Bn, L1) : 0.f;
-        const float K0a = kChain ? fmaf(3.5f, K1, K0) : 0.f;
-        const float R0z = kGateFree ? (Fn * dz) * dz : fmaf(Fn * dz, dz, -shift);
-        float stp = kChain ? __builtin_amdgcn_exp2f(-fmaf(Bn, myl + 3.5f, K1)) : 0.f;  // ly = 0
+        const float Cdz = fmaf(Cn, dz, s0), Edz = En * dz;
+        const float R0z = fmaf(Fn * dz, dz, c0);
         float Q0 = 0.f, Qx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
 #pragma unroll
         for (int ly = 0; ly < GSV_TILE; ++ly) {
@@ -728,37 +738,22 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                 gv[4 * q] = t4.x; gv[4 * q + 1] = t4.y; gv[4 * q + 2] = t4.z; gv[4 * q + 3] = t4.w;
             }
             const float dy = myl - ((float)ly - 3.5f);
-            float sv[GSV_TILE];  // kSym: the row's exponents; kChain: its a
-            float R1 = 0.f, R0 = 0.f;
+            const float R1 = fmaf(Bn, dy, Cdz);
+            const float R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
+            float sv[GSV_TILE];  // kChain: the row's a
             if (kChain) {
-                const float S1 = fmaf(Bn, dy, K1);
-                const float Ea = fmaf(dy, fmaf(Dn, dy, L1a), K0a);  // E at p' = -3.5 (+ bound + K)
-                const float step = stp;  // 2^-S1
-                stp *= rB;
-                float e1 = __builtin_amdgcn_exp2f(Ea);                    // p' = -3.5
-                float e2 = __builtin_amdgcn_exp2f(fmaf(-4.0f, S1, Ea));  // p' = +0.5
+                const float step = __builtin_amdgcn_exp2f(-R1);                // 2^-R1
+                float e1 = __builtin_amdgcn_exp2f(fmaf(dxu[0], R1, R0));  // u = 0
+                float e2 = __builtin_amdgcn_exp2f(fmaf(dxu[4], R1, R0));  // u = 4
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    sv[k] = e1 * P[3 - k];
-                    sv[4 + k] = e2 * P[k];
+                    sv[k] = e1 * G[k];
+                    sv[4 + k] = e2 * G[4 + k];
                     if (k < 3) {
                         e1 *= step;
                         e2 *= step;
                     }
                 }
-            } else if (kSym) {
-                const float S1 = fmaf(Bn, dy, K1);
-                const float S0 = fmaf(dy, fmaf(Dn, dy, L1), K0);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const float V = S0 + P[k];
-                    sv[4 + k] = fmaf(-(0.5f + k), S1, V);
-                    sv[3 - k] = fmaf(0.5f + k, S1, V);
-                }
-            } else {
-                R1 = fmaf(Bn, dy, Cdz);
-                R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
-                if (kGateFree) R0 += bound;  // the offset enters after the small terms
             }
             float W1 = 0.f, h[GSV_TILE];
 #pragma unroll
@@ -767,22 +762,22 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                 if (kChain) {
                     a = sv[u];
                 } else {
-                    const float s = kSym ? sv[u] : fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
+                    const float s = fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
                     if (kGateFree)
-                        a = __builtin_amdgcn_exp2f(s);
+                        a = __builtin_amdgcn_exp2f(s) * Fb;  // flushed below 2^-126: the gate
                     else
                         a = (fabsf(s) <= bound) ? __builtin_amdgcn_exp2f(s) : 0.f;
                 }
                 if (C == 1) {
                     h[u] = a * gv[u];
                 } else {
-                    float G = 0.f;
+                    float Gs = 0.f;
 #pragma unroll
                     for (int c = 0; c < C; ++c) {
-                        G = fmaf(I[c], gv[u * C + c], G);
+                        Gs = fmaf(I[c], gv[u * C + c], Gs);
                         M.dI[c] = fmaf(a, gv[u * C + c], M.dI[c]);
                     }
-                    h[u] = a * G;
+                    h[u] = a * Gs;
                 }
                 W1 = fmaf(h[u], dxu[u], W1);
                 col[u] = add_nc(col[u], h[u]);
@@ -1119,36 +1114,44 @@ __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
     }
 }
 
-// Shift K of the chained row evaluation of one pair (pair_moments, kChain), or
-// -1 when the pair's rows are too steep for it: the largest integer K with
-// K + 12.25 |A2| <= 120 (so 2^(A2 p'^2 - K) >= 2^-120, and
-// 2^E <= 2^(-66 + 12.25 |A2| + K) < 2^54 since sigma2 + off <= off <= -66),
-// provided K >= 3M + 2 for an M >= |S1| on every row that can hold a passing
-// voxel.  The largest K brings the exp2 arguments of passing voxels nearest to
-// 0, where their rounding costs least.  S1 = 2 A2 mx + Bn dy + Cn dz is linear in the
-// row's offsets (dy, dz) from the centre: over the tile's rows it stays within
-// 3.5 (|Bn| + |Cn|) of its value at the tile's centre row; rows outside the
-// projection onto (y, z) of the gate ellipsoid d^T Q d <= k2 hold no passing
-// voxel, and over that ellipse Bn dy + Cn dz stays within sqrt(k2 g^T S g),
-// g = (Bn, Cn), S the (y, z) block of Q^-1.  Also, on a row whose gate interval
-// (half-width <= sqrt(k2 / Q_xx)) meets the voxel centres |p'| <= 3.5, the
-// form's peak lies within 3.5 + sqrt(k2 / Q_xx) of the row centre, where the
-// slope is 2 |A2| times that distance.  Along a chain (three steps of p'), E
-// then falls by at most 3M before a passing voxel, where E >= -126 + K: no
-// product flushes early.
+// Shift K of the chained row evaluation of one pair (pair_moments, kChain) and
+// the centre d of its column factors (*dch), or -1 when the pair does not
+// qualify.  With a_u = 2^E_u * G_u, G_u = 2^(A2 (dx_u - d)^2 - K) and
+// E_u = sigma2 + off - A2 (dx_u - d)^2 + K, linear in u with slope
+// -(R1 + 2 A2 d) per column (R1 = Bn dy + Cn dz), the chain is exact in binary32
+// flush-to-zero arithmetic (every product below 2^-126 is 0 exactly where the
+// reference's gate fails, up to rounding at the threshold) when
+//  (a) every G_u of a voxel that can pass is >= 2^-125 and every G_u <= 1;
+//  (b) along each chain (an anchor and three steps) no product before a
+//      passing voxel, where E >= -126 + K, falls below 2^-124: K >= 3M + 2
+//      with M >= |slope| on every row that can hold a passing voxel;
+//  (c) no step or E overflows on any row of the tile, live or dead.
+// d = 0 (about the Gaussian's centre) is preferred: E's terms then stay near
+// sigma2's own size, where their rounding costs least.  A voxel passes only
+// inside the gate ellipsoid d^T Q d <= k2, so there dx^2 <= k2 (Q^-1)_xx, and
+// in this tile |dx| <= |mx| + 3.5: K <= 125 + A2 max(...) gives (a); the
+// slope is R1, within sqrt(k2 w^T S w) over the ellipsoid's projection onto
+// (y, z) (w = (Bn, Cn), S the (y, z) block of Q^-1) and within m_tile over
+// the tile's rows; E_u = dx_u R1 + R0 + off + K is at most K - 66 +
+// min(|A2| dx_max, m_tile) dx_max (sigma2 <= 0, R0 <= 0, off <= -66), kept
+// below 127.  Strongly coupled conics (R1 large over the gate) fail (b)
+// there and take d = mx (about the tile centre): G_u = 2^(A2 p'^2 - K),
+// |p'| <= 3.5, with K + 12.25 |A2| <= 120 for (a); the slope 2 A2 mx + R1 is
+// within 2 |A2| (3.5 + sqrt(k2 / Q_xx)) on a row whose gate interval meets the
+// voxel centres (its peak lies that close to the row centre), within
+// |2 A2 mx| + sqrt(k2 w^T S w) over the ellipse and within that m_tile over the
+// tile; E <= -66 + 12.25 |A2| + K < 54 for (c).  With d = 0, E is off + K at
+// the Gaussian's centre, so K is the admissible integer nearest 126 + t2;
+// with d = mx it is the largest admissible one.  Both bring the exp2
+// arguments of the voxels that weigh most near 0, where they round least.
+// Binary32 margins: 1e-3 relative and 0.01 on M, 1e-3 on the ellipsoid's
+// extent (whose binary32 error the conditioning checks keep below 5e-4).
 template <int C>
-__device__ __forceinline__ float chain_shift(const BwdLane<C> &L, float A2, float Bn, float Cn) {
-    const float m_tile = fabsf(fmaf(2.0f * A2, L.mxl, fmaf(Bn, L.myl, Cn * L.mzl))) +
-                         3.5f * (fabsf(Bn) + fabsf(Cn));
-    const float K = floorf(120.0f - 12.25f * fabsf(A2));
-    // Rows outside the gate ellipse are bounded by m_tile alone: below 120 every
-    // row's step 2^-S1 (and 2^Bn, the ratio of neighbouring rows' steps) is a
-    // finite normal number, so no product of a dead row is inf * 0.
-    if (!(m_tile < 120.0f)) return -1.0f;
+__device__ __forceinline__ float chain_shift(const BwdLane<C> &L, float A2, float Bn, float Cn,
+                                             float &dch) {
+    dch = 0.f;
     const float k2 = -2.0f * kLn2 * L.gt.t2;
-    const float m_reach = fabsf(2.0f * A2) *
-                          (3.5f + __builtin_amdgcn_sqrtf(fmaxf(k2 * __builtin_amdgcn_rcpf(L.ca), 0.f)));
-    // sqrt(k2 g^T S g) = sqrt(k2 w^T Q^-1 w), w = (0, Bn, Cn), from the Cholesky
+    // sqrt(k2 w^T S w) = sqrt(k2 w^T Q^-1 w), w = (0, Bn, Cn), from the Cholesky
     // factor Q = L L^T in binary32: w^T Q^-1 w = y2^2 + y3^2 with y = L^-1 w.
     // With both pivots above 1e-3 of their diagonal (condition number below
     // ~1e3) the relative error stays near 1e-4, inside the margins below; a
@@ -1164,12 +1167,39 @@ __device__ __forceinline__ float chain_shift(const BwdLane<C> &L, float A2, floa
         if (t33 > 1e-3f * L.cf) {
             const float y2 = Bn * i22;
             const float y3 = fmaf(-l32, y2, Cn) * __builtin_amdgcn_rsqf(t33);
-            m_ell = fabsf(2.0f * A2 * L.mxl) +
-                    __builtin_amdgcn_sqrtf(fmaxf(k2 * fmaf(y2, y2, y3 * y3), 0.f));
+            m_ell = __builtin_amdgcn_sqrtf(fmaxf(k2 * fmaf(y2, y2, y3 * y3), 0.f));
         }
     }
-    const float M = fminf(m_tile, fminf(m_ell, m_reach)) * 1.001f + 0.01f;
-    return ceilf(3.0f * M) + 2.0f <= K ? K : -1.0f;
+    const float r1_tile = fabsf(fmaf(Bn, L.myl, Cn * L.mzl)) + 3.5f * (fabsf(Bn) + fabsf(Cn));
+    // d = 0.  (Q^-1)_xx = (d f - e^2) / det: with the (y, z) minor above
+    // 1e-3 d f and the x pivot det / (d f - e^2) above 1e-3 a, both are within
+    // ~5e-4 of their values; det stays within the reciprocal's normal range
+    const float cfx = fmaf(L.cd, L.cf, -L.ce * L.ce);
+    const float det = L.ca * cfx - L.cb * fmaf(L.cb, L.cf, -L.cc * L.ce) +
+                      L.cc * fmaf(L.cb, L.ce, -L.cc * L.cd);
+    const float dx_max = fabsf(L.mxl) + 3.5f;
+    if (cfx > 1e-3f * (L.cd * L.cf) && det > 1e-3f * (L.ca * cfx) && det > 0x1p-100f &&
+        det < 0x1p100f && r1_tile < 120.0f) {
+        const float g_ell = A2 * (k2 * cfx * __builtin_amdgcn_rcpf(det));  // A2 k2 (Q^-1)_xx
+        const float g_min = fmaxf(g_ell, A2 * (dx_max * dx_max));             // <= 0
+        const float k_max = floorf(fminf(120.0f, 125.0f + 1.001f * g_min));
+        const float M = fminf(r1_tile, m_ell) * 1.001f + 0.01f;
+        const float k_min = ceilf(3.0f * M) + 2.0f;
+        // E at the Gaussian's centre is off + K: nearest 0 at K = 126 + t2
+        const float K = fminf(k_max, fmaxf(k_min, floorf(126.5f + L.gt.t2)));
+        if (k_min <= K && fminf(-A2 * dx_max, r1_tile) * dx_max + K < 190.0f) return K;
+    }
+    // d = mx
+    const float m_tile = fabsf(fmaf(2.0f * A2, L.mxl, fmaf(Bn, L.myl, Cn * L.mzl))) +
+                         3.5f * (fabsf(Bn) + fabsf(Cn));
+    if (!(m_tile < 120.0f)) return -1.0f;
+    const float K = floorf(120.0f - 12.25f * fabsf(A2));
+    const float m_reach = fabsf(2.0f * A2) *
+                          (3.5f + __builtin_amdgcn_sqrtf(fmaxf(k2 * __builtin_amdgcn_rcpf(L.ca), 0.f)));
+    const float M = fminf(m_tile, fminf(fabsf(2.0f * A2 * L.mxl) + m_ell, m_reach)) * 1.001f + 0.01f;
+    if (!(ceilf(3.0f * M) + 2.0f <= K)) return -1.0f;
+    dch = L.mxl;
+    return K;
 }
 
 // Exponent e such that m * 2^e lies in [2^(kGradScaleExp-1), 2^kGradScaleExp);
@@ -1331,16 +1361,18 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
         const float gx = in_grp ? L.mxl : 0.f, gy = in_grp ? L.myl : 0.f, gz = in_grp ? L.mzl : 0.f;
         if (wave_fast) {
             const float off = in_grp ? L.gt.off : kDeadOffset;
-            const float kshift = in_grp ? chain_shift(L, A2, Bn, Cn) : 2.0f;
+            float dch = 0.f;
+            const float kshift = in_grp ? chain_shift(L, A2, Bn, Cn, dch) : 2.0f;
             if (a.chain && __all(kshift >= 0.f))
                 pair_moments<C, true, true>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn,
-                                            Cn, Dn, En, Fn, 0.f, off, kshift, L.I, M);
+                                            Cn, Dn, En, Fn, 0.f, off, kshift, dch, L.I, M);
             else
                 pair_moments<C, true>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn, Cn,
-                                      Dn, En, Fn, 0.f, off, 0.f, L.I, M);
+                                      Dn, En, Fn, 0.f, off, 0.f, 0.f, L.I, M);
         } else {
             pair_moments<C, false>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn, Cn,
-                                   Dn, En, Fn, L.gt.shift, in_grp ? L.gt.half : -1.f, 0.f, L.I, M);
+                                   Dn, En, Fn, L.gt.shift, in_grp ? L.gt.half : -1.f, 0.f, 0.f,
+                                   L.I, M);
         }
         __syncthreads();  // a later group restages the slots
     }

@@ -233,3 +233,29 @@ def reference_value_scenario(seed: int = 0, n: Optional[int] = None):
     work = Workload(cfg, pos.contiguous(), scale, quat.contiguous(), inten,
                     {"kind": "spheres"}, seed)
     return work, vol
+
+
+def volume_scaling_scenario(edge: int, seed: int = 0, base_edge: int = 96,
+                            base_gaussians: int = 6000) -> Workload:
+    """The reference's volume-scaling case (test/test_volume_scaling.py:53-64,
+    130-139), seeded: a cubic volume of `edge` voxels in a unit world centred
+    at 0.5, round(base_gaussians * edge / base_edge) Gaussians from
+    random_gauss_init(anisotropicScale=True) (test/utils.py:91-154): positions
+    U[0,1)^3, scales (0.03, 0.01, 0.02) world units, identity rotations, and
+    intensities read from generate_noise_volume (test/utils.py:32-71:
+    0.1 + 0.9 * avg_pool3d_5(U[0,1)), clamped to [0, 1]) at the voxel
+    floor(pos * (edge - 1)).  The smoothed noise is not formed over the whole
+    volume (6.9 GB at 1200^3): each Gaussian's value is 0.1 + 0.9 times the
+    mean of 125 uniform draws of its own, the same distribution at an interior
+    voxel (nearby Gaussians do not share draws, which nothing here depends on)."""
+    n = max(1, int(round(base_gaussians * edge / base_edge)))
+    cfg = Config(f"volume_scaling_{edge}cube_{n // 1000}k", (edge, edge, edge), n, 1,
+                 ("fixed", 0.03, 0.01, 0.02), "identity", (0.1, 1.0), "uniform", "noise")
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    pos = torch.rand((n, 3), generator=g, dtype=torch.float32)
+    scale = torch.tensor([0.03, 0.01, 0.02], dtype=torch.float32).expand(n, 3).contiguous()
+    quat = torch.zeros((n, 4), dtype=torch.float32)
+    quat[:, 0] = 1.0
+    u = torch.rand((n, 125), generator=g, dtype=torch.float32).mean(1, keepdim=True)
+    inten = (0.1 + 0.9 * u).clamp(0.0, 1.0).contiguous()
+    return Workload(cfg, pos.contiguous(), scale, quat, inten, {"kind": "noise"}, seed)

@@ -368,11 +368,14 @@ static int gate_ambiguous(real sigma, real mean, real alpha) {
  * voxels of other tiles are left untouched (the caller zero-fills).
  * amb (optional, same layout as out) receives per voxel the sum of |I_c*alpha|
  * over gate-ambiguous evaluations (see gate_ambiguous).
+ * out and amb hold the z planes [z_base, z_base + z_count) of the volume
+ * (z_base = 0, z_count = D for the whole volume); voxels of other planes are
+ * skipped.
  * Pinned by: tests/test_oracle_voxelize.py (dense fp64 brute force, closed forms).
  */
 int orc_voxelize_fwd(int D, int H, int W, int C, const int *ids_sorted, const int *tile_bins,
                      const real *pos_radii, const real *conics, const real *intens, real *out,
-                     real *amb, int64_t tile_begin, int64_t tile_end) {
+                     real *amb, int64_t tile_begin, int64_t tile_end, int z_base, int z_count) {
     if (C < 1 || C > GSV_MAX_CHANNELS) return 1;
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H);
     const int64_t T = (int64_t)Tx * Ty * gsv_tiles_along(D);
@@ -386,6 +389,7 @@ int orc_voxelize_fwd(int D, int H, int W, int C, const int *ids_sorted, const in
                 for (int lx = 0; lx < GSV_TILE; ++lx) {
                     const int i = tz * GSV_TILE + lz, j = ty * GSV_TILE + ly, k = tx * GSV_TILE + lx;
                     if (i >= D || j >= H || k >= W) continue;
+                    if (i < z_base || i >= z_base + z_count) continue;
                     const real px = (real)k + 0.5f, py = (real)j + 0.5f, pz = (real)i + 0.5f;
                     real acc[GSV_MAX_CHANNELS] = {0.f, 0.f, 0.f, 0.f};
                     real am[GSV_MAX_CHANNELS] = {0.f, 0.f, 0.f, 0.f};
@@ -408,10 +412,10 @@ int orc_voxelize_fwd(int D, int H, int W, int C, const int *ids_sorted, const in
                         if (alpha * mean < GSV_MIN_CONTRIB) continue;
                         for (int ch = 0; ch < C; ++ch) acc[ch] += intens[(size_t)g * C + ch] * alpha;
                     }
-                    real *o = out + ((((size_t)i * H + j) * W) + k) * C;
-                    for (int ch = 0; ch < C; ++ch) o[ch] = acc[ch];
+                    const size_t at = ((((size_t)(i - z_base) * H + j) * W) + k) * C;
+                    for (int ch = 0; ch < C; ++ch) out[at + ch] = acc[ch];
                     if (amb)
-                        for (int ch = 0; ch < C; ++ch) amb[((((size_t)i * H + j) * W) + k) * C + ch] = am[ch];
+                        for (int ch = 0; ch < C; ++ch) amb[at + ch] = am[ch];
                 }
     }
     return 0;

@@ -84,7 +84,8 @@ class Oracle:
             L.orc_bin_and_sort.argtypes = [_c_int, _c_i64, _i32p, _i32p, _i32p, _c_int, _c_int,
                                            _c_int, _i32p, _i32p, ctypes.c_void_p]
             L.orc_voxelize_fwd.argtypes = [_c_int, _c_int, _c_int, _c_int, _i32p, _i32p, rp, rp,
-                                           rp, rp, ctypes.c_void_p, _c_i64, _c_i64]
+                                           rp, rp, ctypes.c_void_p, _c_i64, _c_i64, _c_int,
+                                           _c_int]
             L.orc_voxelize_bwd.argtypes = [_c_int, _c_int, _c_int, _c_int, _c_int, _i32p, _i32p,
                                            rp, rp, rp, rp, rp, rp, rp] + \
                 [ctypes.c_void_p] * 6 + [_c_i64, _c_i64]
@@ -163,21 +164,25 @@ class Oracle:
         return (ids, bins, keys) if return_keys else (ids, bins)
 
     def voxelize_fwd(self, vol_size, ids_sorted, tile_bins, pos_radii, conics, intensities,
-                     tile_range=None, with_amb=False):
+                     tile_range=None, with_amb=False, z_slab=None):
         """(D,H,W,C) volume; with ``with_amb`` also the per-voxel sum of |I*alpha|
-        over gate-ambiguous evaluations (see gate_ambiguous in gsv_oracle.c)."""
+        over gate-ambiguous evaluations (see gate_ambiguous in gsv_oracle.c).
+        With ``z_slab = (z0, z1)`` only the voxel planes [z0, z1) are held and
+        returned, (z1 - z0, H, W, C) (pair it with a tile_range inside them)."""
         D, H, W = (int(v) for v in vol_size)
+        z0, z1 = (0, D) if z_slab is None else (int(z_slab[0]), int(z_slab[1]))
         pr = self._r(pos_radii, 4)
         n = pr.shape[0]
         I = self._r(intensities).reshape(n, -1)
         C = I.shape[1]
-        out = np.zeros((D, H, W, C), self.real)
-        amb = np.zeros((D, H, W, C), self.real) if with_amb else None
+        out = np.zeros((z1 - z0, H, W, C), self.real)
+        amb = np.zeros((z1 - z0, H, W, C), self.real) if with_amb else None
         bins = _i32(tile_bins, 2)
         t0, t1 = tile_range if tile_range is not None else (0, bins.shape[0])
         _check(self.lib().orc_voxelize_fwd(D, H, W, C, _i32(ids_sorted).reshape(-1), bins, pr,
                                            self._r(conics, 6), I, out,
-                                           _ptr(amb) if with_amb else None, int(t0), int(t1)),
+                                           _ptr(amb) if with_amb else None, int(t0), int(t1),
+                                           z0, z1 - z0),
                "voxelize_fwd")
         return (out, amb) if with_amb else out
 

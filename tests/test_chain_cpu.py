@@ -1,9 +1,10 @@
 """The chained row evaluation of the voxelize kernels, checked on the CPU.
 
 Both voxelize kernels form most exp2 values of an 8-voxel row as products
-(an anchor 2^E and a step 2^-T1, times a per-Gaussian 2^(A2 uc^2 - K)) and
-rely on binary32 flush-to-zero for the reference's 1e-6 gate: a product below
-2^-126 is 0.  That is only the gate if no factor of a chain flushes before a
+(an anchor 2^E and a step along the row, times per-Gaussian column factors:
+2^(A2 uc^2 - K) about the tile centre in the forward, 2^(A2 dx_u^2 - K) about
+the Gaussian's centre in the backward) and rely on binary32 flush-to-zero for
+the reference's 1e-6 gate: a product below 2^-126 is 0.  That is only the gate if no factor of a chain flushes before a
 passing voxel and nothing overflows, which the choice of K guarantees for the
 pairs that qualify (csrc/voxelize.hip: the forward's record set-up and
 chain_shift).  This test restates those rules in numpy (binary32 with
@@ -161,73 +162,104 @@ def _forward_chains(P):
     return out, chain
 
 
+def _f(x):
+    return np.asarray(x, np.float64).astype(np.float32)
+
+
+def _fma(a, b, c):
+    """fmaf in binary32 with flush-to-zero (the product and sum in binary64,
+    rounded once: exact for the magnitudes here)."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        return _ftz(np.float64(a) * np.float64(b) + np.float64(c))
+
+
 def _backward_chains(P):
     """The backward's rows (lane = pair, rows walked in order), as pair_moments
-    with kChain forms them, and chain_shift's qualification."""
+    with kChain forms them: a_u = 2^E_u * G_u with the column factors
+    G_u = 2^(A2 (dx_u - d)^2 - K) (with the rounding residual of the
+    exponent) and E_u linear in u, 2^E at u = 0 and u = 4 stepped along the
+    row; and chain_shift's choice of d (0, the Gaussian's centre, or mx, the
+    tile's) and K.  Returns (a, qualifies, excluded, centred): excluded are the
+    pairs that pass the Gaussian-centred conditions but the dead-row bounds
+    and have no tile-centred fallback, centred those that take d = 0."""
     uc, py, pz = _grid()
-    mx, my, mz = (P[:, i].astype(np.float32) for i in range(3))
-    ca, cb, cc_, cd, ce, cf = (P[:, 3 + i].astype(np.float32) for i in range(6))
-    t2 = P[:, 9].astype(np.float32)
-    off = (-(t2 + F32(126.0))).astype(np.float32)
-    A2 = F32(-0.5 * L2E) * ca
-    Bn, Cn = F32(-L2E) * cb, F32(-L2E) * cc_
-    Dn, En, Fn = F32(-0.5 * L2E) * cd, F32(-L2E) * ce, F32(-0.5 * L2E) * cf
-    # chain_shift (binary32): the tile bound, the gate interval's reach, and the
-    # slope bound over the gate ellipse from a Cholesky factor of the conic,
-    # left out when a pivot falls below 1e-3 of its diagonal
-    m_tile = np.abs(2 * A2 * mx + Bn * my + Cn * mz) + F32(3.5) * (np.abs(Bn) + np.abs(Cn))
-    k2 = (F32(-2.0 * 0.693147180559945309) * t2).astype(np.float32)
-    with np.errstate(divide="ignore", invalid="ignore"):
-        m_reach = (np.abs(F32(2) * A2) * (F32(3.5) + np.sqrt(np.maximum(k2 / ca, F32(0))))
-                   ).astype(np.float32)
-        i11 = (F32(1) / np.sqrt(ca)).astype(np.float32)
+    F = np.float32
+    mx, my, mz = (P[:, i].astype(F) for i in range(3))
+    ca, cb, cc_, cd, ce, cf = (P[:, 3 + i].astype(F) for i in range(6))
+    t2 = P[:, 9].astype(F)
+    off = (-(t2 + F(126.0))).astype(F)
+    A2 = F(-0.5 * L2E) * ca
+    Bn, Cn = F(-L2E) * cb, F(-L2E) * cc_
+    Dn, En, Fn = F(-0.5 * L2E) * cd, F(-L2E) * ce, F(-0.5 * L2E) * cf
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        k2 = (F(-2.0 * 0.693147180559945309) * t2).astype(F)
+        i11 = (F(1) / np.sqrt(ca)).astype(F)
         l21, l31 = cb * i11, cc_ * i11
-        t22 = (cd - l21 * l21).astype(np.float32)
-        i22 = (F32(1) / np.sqrt(t22)).astype(np.float32)
-        l32 = ((ce - l31 * l21) * i22).astype(np.float32)
-        t33 = (cf - l31 * l31 - l32 * l32).astype(np.float32)
+        t22 = _fma(-l21, l21, cd)
+        i22 = (F(1) / np.sqrt(t22)).astype(F)
+        l32 = _f(_fma(-l31, l21, ce) * i22)
+        t33 = _fma(-l32, l32, _fma(-l31, l31, cf))
         y2 = Bn * i22
-        y3 = ((Cn - l32 * y2) / np.sqrt(t33)).astype(np.float32)
-        ell = (np.abs(F32(2) * A2 * mx) + np.sqrt(np.maximum(k2 * (y2 * y2 + y3 * y3), F32(0)))
-               ).astype(np.float32)
-    ok = (t22 > F32(1e-3) * cd) & (t33 > F32(1e-3) * cf)
-    m_ell = np.where(ok, ell, np.float32(np.inf)).astype(np.float32)
-    M = np.minimum(m_tile, np.minimum(m_ell, m_reach)) * F32(1.001) + F32(0.01)
-    K = np.floor(F32(120.0) - F32(12.25) * np.abs(A2))
-    span_ok = np.ceil(F32(3.0) * M) + 2 <= K
-    # every row of the tile, dead ones included, keeps |S1| below 120
-    qualifies = span_ok & (m_tile < F32(120.0))
-    k = (np.arange(4) + 0.5).astype(np.float32)
-    with np.errstate(over="ignore"):  # K < 0 only for pairs that do not qualify
-        Pk = _ftz(np.ldexp(_exp2(A2[:, None] * (k * k)), -K.astype(np.int64)[:, None]))
-    # per row: dy = my - p'_y, dz = mz - p'_z (rows walked z-major, lane-independent order)
-    dy = (my[:, None] - py[None, :]).astype(np.float64)
-    dz = (mz[:, None] - pz[None, :]).astype(np.float64)
-    A2d, Bd, Cd = A2.astype(np.float64)[:, None], Bn.astype(np.float64)[:, None], Cn.astype(np.float64)[:, None]
-    Dd, Ed, Fd = Dn.astype(np.float64)[:, None], En.astype(np.float64)[:, None], Fn.astype(np.float64)[:, None]
-    mxd = mx.astype(np.float64)[:, None]
-    S1 = (2 * A2d * mxd + Bd * dy + Cd * dz).astype(np.float32)
-    S0 = (A2d * mxd * mxd + Bd * mxd * dy + Cd * mxd * dz + Dd * dy * dy + Ed * dy * dz
-          + Fd * dz * dz)
-    Ea = (S0 + 3.5 * S1.astype(np.float64) + off.astype(np.float64)[:, None]
-          + K.astype(np.float64)[:, None]).astype(np.float32)            # E at p' = -3.5
-    # the step 2^-S1 of row (ly, lz) is row (0, lz)'s times (2^Bn)^ly
-    rB = _exp2(Bn)
-    step = np.zeros_like(S1)
+        y3 = _f(_fma(-l32, y2, Cn) * (F(1) / np.sqrt(t33)).astype(F))
+        m_ell = np.sqrt(np.maximum(k2 * _fma(y2, y2, y3 * y3), F(0))).astype(F)
+        m_ell = np.where((t22 > F(1e-3) * cd) & (t33 > F(1e-3) * cf), m_ell,
+                         np.float32(np.inf)).astype(F)
+        r1_tile = _f(np.abs(_fma(Bn, my, Cn * mz)) + F(3.5) * (np.abs(Bn) + np.abs(Cn)))
+        # d = 0
+        cfx = _fma(cd, cf, -(ce * ce))
+        det = _f(ca * cfx - cb * _fma(cb, cf, -(cc_ * ce)) + cc_ * _fma(cb, ce, -(cc_ * cd)))
+        dx_max = _f(np.abs(mx) + F(3.5))
+        cond = ((cfx > F(1e-3) * (cd * cf)) & (det > F(1e-3) * (ca * cfx)) & (det > F(2.0 ** -100))
+                & (det < F(2.0 ** 100)) & (r1_tile < F(120.0)))
+        g_ell = _f(A2 * _f(k2 * cfx * _f(F(1) / det)))
+        g_min = np.maximum(g_ell, _f(A2 * (dx_max * dx_max)))
+        Kmax = np.floor(np.minimum(F(120.0), F(125.0) + F(1.001) * g_min)).astype(F)
+        M0 = (np.minimum(r1_tile, m_ell) * F(1.001) + F(0.01)).astype(F)
+        Kmin = np.ceil(F(3.0) * M0) + 2
+        K0 = np.minimum(Kmax, np.maximum(Kmin, np.floor(F(126.5) + t2))).astype(F)
+        live0 = cond & (Kmin <= K0)
+        dead0 = np.minimum(-A2 * dx_max, r1_tile) * dx_max + K0 < F(190.0)
+        centred = live0 & dead0
+        # d = mx
+        m_tile = _f(np.abs(_fma(F(2.0) * A2, mx, _fma(Bn, my, Cn * mz))) +
+                    F(3.5) * (np.abs(Bn) + np.abs(Cn)))
+        K1 = np.floor(F(120.0) - F(12.25) * np.abs(A2)).astype(F)
+        m_reach = (np.abs(F(2) * A2) * (F(3.5) + np.sqrt(np.maximum(k2 / ca, F(0))))).astype(F)
+        M1 = (np.minimum(m_tile, np.minimum(np.abs(F(2) * A2 * mx) + m_ell, m_reach)) * F(1.001)
+              + F(0.01)).astype(F)
+        tile_ok = (m_tile < F(120.0)) & (np.ceil(F(3.0) * M1) + 2 <= K1)
+    qualifies = centred | tile_ok
+    K = np.where(centred, K0, np.where(tile_ok, K1, np.where(live0, K0, F(2.0)))).astype(F)
+    d = np.where(centred | ~tile_ok, F(0), mx).astype(F)
+    dxu = _f(mx[:, None] - uc[None, :].astype(F))                      # (N, 8)
+    x = np.where((d == 0)[:, None], dxu, uc[None, :].astype(F)).astype(F)
+    p = _f(A2[:, None] * x)
+    plo = _fma(A2[:, None], x, -p)
+    hi = _f(p * x)
+    lo = _fma(plo, x, _fma(p, x, -hi))
+    with np.errstate(over="ignore"):
+        G = _ftz(np.ldexp(np.float64(_f(np.float64(_exp2(hi)) * _fma(lo, F(0.693147180559945309), F(1)))),
+                          -K.astype(np.int64)[:, None]))
+    c0 = _fma(-A2 * d, d, _f(off + K))
+    s0 = _f(F(2.0) * A2 * d)
+    out = np.zeros((P.shape[0], 64, 8), np.float32)
     for lz in range(8):
-        rows = slice(8 * lz, 8 * lz + 8)
-        st = _exp2(-S1[:, 8 * lz])
+        dz = _f(mz - F(lz - 3.5))
+        Cdz, Edz = _fma(Cn, dz, s0), _f(En * dz)
+        R0z = _fma(_f(Fn * dz), dz, c0)
         for ly in range(8):
-            step[:, 8 * lz + ly] = st
-            st = _mul(st, rB)
-    e1 = _exp2(Ea)
-    e2 = _exp2((Ea.astype(np.float64) - 4.0 * S1).astype(np.float32))  # p' = +0.5
-    out = np.zeros(Ea.shape + (8,), np.float32)
-    for kk in range(4):
-        out[..., kk] = _mul(e1, Pk[:, 3 - kk][:, None])
-        out[..., 4 + kk] = _mul(e2, Pk[:, kk][:, None])
-        e1, e2 = _mul(e1, step), _mul(e2, step)
-    return out, qualifies, span_ok & ~qualifies
+            row = lz * 8 + ly
+            dy = _f(my - F(ly - 3.5))
+            R1 = _fma(Bn, dy, Cdz)
+            R0 = _fma(_fma(Dn, dy, Edz), dy, R0z)
+            step = _exp2(-R1)
+            e1 = _exp2(_fma(dxu[:, 0], R1, R0))
+            e2 = _exp2(_fma(dxu[:, 4], R1, R0))
+            for k in range(4):
+                out[:, row, k] = _mul(e1, G[:, k])
+                out[:, row, 4 + k] = _mul(e2, G[:, 4 + k])
+                e1, e2 = _mul(e1, step), _mul(e2, step)
+    return out, qualifies, live0 & ~dead0 & ~tile_ok, centred
 
 
 def _random_pairs(n, seed):
@@ -296,23 +328,26 @@ def test_chained_rows_gate_like_exp2(name, make, npairs, share):
     fwd, fwd_ok = _forward_chains(P)
     n_f, live_f = _check(f"{name} forward", s_exact, fwd, fwd_ok)
     # the backward walks the same rows with the Gaussian-centred form
-    bwd, bwd_ok, _ = _backward_chains(P)
+    bwd, bwd_ok, _, _ = _backward_chains(P)
     n_b, live_b = _check(f"{name} backward", s_exact, bwd, bwd_ok)
     assert n_f > share * len(P) and n_b > share * len(P), (name, n_f, n_b, len(P))
     assert live_f > 0 and live_b > 0
 
 
 def test_backward_chain_bounds_dead_rows():
-    """chain_shift's m_tile < 120 condition: needles whose live rows qualify
-    but whose dead rows reach |S1| >= 128 must take the exact path, and every
-    qualifying pair stays finite with the right gate."""
-    P = _needle_pairs(6000, seed=9)
+    """chain_shift's dead-row conditions (every tile row's slope |R1| below
+    120, and the bound on E over the tile): pairs whose passing rows qualify
+    but whose tile reaches beyond those bounds must take another path, and
+    every qualifying pair stays finite with the right gate.  On rotated
+    anisotropic conics and tilted needles; evaluated anyway, some of the
+    excluded pairs overflow."""
+    P = np.concatenate([_random_pairs(12000, seed=5), _needle_pairs(6000, seed=9)])
     s_exact = _exact_exponent(P)
-    bwd, ok, excluded = _backward_chains(P)
-    n_b, live_b = _check("needles backward", s_exact, bwd, ok)
-    assert n_b > 0.05 * len(P) and live_b > 0, (n_b, len(P))
-    # the scene exercises the condition: without it these pairs would take the
-    # chains and some of their products would overflow
+    bwd, ok, excluded, centred = _backward_chains(P)
+    n_b, live_b = _check("conics and needles backward", s_exact, bwd, ok)
+    assert n_b > 0.3 * len(P) and live_b > 0, (n_b, len(P))
+    # the scene exercises the conditions: without them these pairs would take
+    # the chains and some of their products would overflow
     assert excluded.sum() > 0.01 * len(P), int(excluded.sum())
     assert not np.isfinite(bwd[excluded]).all()
 

@@ -34,7 +34,7 @@ import torch.nn.functional as F
 
 import oracle as O
 from gs_voxelizer import optim_to_render, synthetic as S, voxelize
-from helpers import assert_no_less_accurate, np32, report_close
+from helpers import AccuracyChecks, assert_no_less_accurate, np32, report_close
 
 pytestmark = pytest.mark.gpu
 
@@ -138,10 +138,12 @@ def test_every_voxelize_gradient_element(scene, grad):
     rg = O.voxelize_bwd(cfg.vol, ref["gaussian_ids_sorted"], ref["tile_bins"],
                         ref["pos3d_radii"], ref["conics"], work.intensities.numpy(), g)
     tg, tamb = _truth_bwd(P, g)
+    acc = AccuracyChecks()
     for mode in ("pairs", "atomic"):
         got = _voxelize_grads(P, g, mode)
         for nm, a, b, t, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, rg, tg, tamb):
-            assert_no_less_accurate(f"{cfg.name} {grad} {mode}: {nm}", a, b, t, m)
+            acc.check(f"{cfg.name} {grad} {mode}: {nm}", a, b, t, m)
+    acc.done()
 
 
 def test_leaf_gradients_end_to_end(scene, device):
@@ -183,12 +185,13 @@ def test_leaf_gradients_end_to_end(scene, device):
                         ref["pos3d_radii"], ref["conics"], inten, g)
     tv, tamb = _truth_bwd(P, g)
     got_v = (np32(seen["dpr"]), np32(seen["dcn"]), np32(leaves[3].grad))
+    acc = AccuracyChecks()
     for nm, a, b, t, m in zip(("dpos3d_radii", "dconics", "dintensities"), got_v, rv, tv, tamb):
-        assert_no_less_accurate(f"{cfg.name} end-to-end stage 1: {nm}", a, b, t, m)
+        acc.check(f"{cfg.name} end-to-end stage 1: {nm}", a, b, t, m)
     if cfg.name.startswith("ref_value_test"):
         # the intensity leaf under the reference's own bound (test_gs_voxelizer.py:142)
-        assert_no_less_accurate(f"{cfg.name} leaf vs binary64, reference's bound: dintensities",
-                                got_v[2], rv[2], tv[2], tamb[2], rtol=1e-4, atol=1e-3)
+        acc.check(f"{cfg.name} leaf vs binary64, reference's bound: dintensities",
+                  got_v[2], rv[2], tv[2], tamb[2], rtol=1e-4, atol=1e-3)
     leaves_np = (work.pos3d.numpy(), work.scale3d.numpy(), work.quat.numpy())
     geo = (cfg.vol, cfg.world, cfg.center)
     same_in = O.project_bwd(*leaves_np, *geo, got_v[0], got_v[1], np32(pr))
@@ -203,8 +206,9 @@ def test_leaf_gradients_end_to_end(scene, device):
         assert np.isfinite(got).all(), nm
         scale = max(1e-30, float(np.abs(a).max()))
         report_close(f"{cfg.name} end-to-end stage 2: {nm}", got, a, 1e-5, 1e-6 * scale)
-        assert_no_less_accurate(f"{cfg.name} leaf vs binary64: {nm}", got, b, t)
+        acc.check(f"{cfg.name} leaf vs binary64: {nm}", got, b, t)
         if cfg.name.startswith("ref_value_test"):
             # the reference's own gradient bound (test_gs_voxelizer.py:142)
-            assert_no_less_accurate(f"{cfg.name} leaf vs binary64, reference's bound: {nm}",
-                                    got, b, t, rtol=1e-4, atol=1e-3)
+            acc.check(f"{cfg.name} leaf vs binary64, reference's bound: {nm}", got, b, t,
+                      rtol=1e-4, atol=1e-3)
+    acc.done()

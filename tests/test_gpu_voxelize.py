@@ -267,15 +267,15 @@ _NEEDLE = np.array([3.490655, 1.9826925, -3.301888, 2.745941, 9.987584, -5.31287
 
 def test_backward_chain_guard_on_needle_in_a_chained_wave(device):
     """One tile, one backward wave: 63 round Gaussians that take the chained
-    rows and the needle above.  Without chain_shift's m_tile < 120 condition
-    the wave would take the chains and the needle's dead rows would turn into
-    inf / NaN; with it the wave takes the exact path, and every gradient
-    matches the oracle."""
+    rows and the needle above.  Chained anyway, the needle's dead rows would
+    turn into inf / NaN (the CPU restatement of the chain shows it); chain_shift
+    refuses it, so the wave takes another path, and every gradient matches the
+    oracle."""
     import gs_voxelizer.cuda as _C
     from test_chain_cpu import _backward_chains
     P = _NEEDLE.astype(np.float64)[None, :]
-    _, qualifies, excluded = _backward_chains(P)
-    assert excluded[0] and not qualifies[0]  # the span rule alone would take it
+    chained, qualifies, _, _ = _backward_chains(P)
+    assert not qualifies[0] and not np.isfinite(chained).all()
     rng = np.random.default_rng(1)
     n, vol, centre = 64, (24, 24, 24), np.float32(12.0)  # tile (1, 1, 1): voxels 8..15
     pr = np.zeros((n, 4), np.float32)
