@@ -649,6 +649,68 @@ struct Moments {
     float dI[C];
 };
 
+// The quadratic form of a gate-free pair in the LDL^T coordinates of its conic,
+// about the tile centre.  With delta = mu - p = m - p' (m the Gaussian's
+// centre relative to the tile centre, p' = local voxel index - 3.5 per axis),
+// Q = L D L^T (L unit lower triangular) and k = log2(e) / 2,
+//   sigma2 = -k delta^T Q delta = -(tau^2 + eta^2 + zeta^2),
+//   tau  = sqrt(k D1) (delta_x + l21 delta_y + l31 delta_z) = tc - al p'x - be p'y - ga p'z,
+//   eta  = sqrt(k D2) (delta_y + l32 delta_z)               = ec - be2 p'y - ga2 p'z,
+//   zeta = sqrt(k D3) delta_z                               = zc - ga3 p'z.
+// sigma2 is then a sum of squares of quantities that are small wherever a
+// voxel weighs (|tau|, |eta|, |zeta| <= sqrt(-t2) inside the gate), so its
+// binary32 rounding stays near that of sigma2 itself.  The expanded form
+// A2 dx^2 + dx (Bn dy + Cn dz) + ... sums terms of up to |Q| |delta|^2 that
+// cancel for an elongated, rotated Gaussian (terms of ~1e3 for a sum of ~10
+// on a 0.5 x 6 voxel Gaussian 15 voxels from its centre), and their rounding
+// is shared by whole rows (R0, R1) or by the whole Gaussian (the scaled
+// coefficients), so it does not average out of the gradient sums: ~30x the
+// reference's error on its worst dconics elements.  The tile-centre terms tc,
+// ec, zc are formed in binary64 from the binary64 factor; the per-row and
+// per-voxel coefficients multiply |p'| <= 3.5 only, so their binary32
+// rounding costs little.
+struct RowForm {
+    float al, be, ga, be2, ga2, ga3;  // coefficients of p'
+    float tc, ec, zc;                 // tau, eta, zeta at the tile centre
+    float r_ell;                      // w^T Q^-1 w, w = 2k (0, b, c): the slope's spread over the gate
+};
+
+// The LDL^T factor of a conic (binary64) and the row form of the pair whose
+// Gaussian lies at (mx, my, mz) from the tile centre.  False (the pair then
+// takes the exact path) unless the binary64 pivots are positive and each
+// k * pivot lies in [2^-100, 2^100], where its binary32 square root is a
+// normal number.  Zero coefficients otherwise.
+__device__ __forceinline__ bool row_form(float ca, float cb, float cc, float cd, float ce,
+                                         float cf, float mx, float my, float mz, RowForm &f) {
+    f.al = f.be = f.ga = f.be2 = f.ga2 = f.ga3 = f.tc = f.ec = f.zc = f.r_ell = 0.f;
+    constexpr double k = 0.72134752044448170368;  // log2(e) / 2
+    const double a = ca, b = cb, c = cc, d = cd, e = ce, ff = cf;
+    const double ia = 1.0 / a;
+    const double l21 = b * ia, l31 = c * ia;
+    const double d2 = fma(-b, l21, d), e2 = fma(-c, l21, e), f2 = fma(-c, l31, ff);
+    const double l32 = e2 / d2;
+    const double d3 = fma(-e2, l32, f2);
+    const double p1 = k * a, p2 = k * d2, p3 = k * d3;
+    constexpr double lo = 0x1p-100, hi = 0x1p100;
+    if (!(p1 >= lo && p1 <= hi && p2 >= lo && p2 <= hi && p3 >= lo && p3 <= hi)) return false;
+    const float al = __builtin_amdgcn_sqrtf((float)p1);
+    const float b2 = __builtin_amdgcn_sqrtf((float)p2);
+    const float g3 = __builtin_amdgcn_sqrtf((float)p3);
+    f.al = al;
+    f.be = (float)(al * l21);
+    f.ga = (float)(al * l31);
+    f.be2 = b2;
+    f.ga2 = (float)(b2 * l32);
+    f.ga3 = g3;
+    f.tc = (float)(al * fma(l31, (double)mz, fma(l21, (double)my, (double)mx)));
+    f.ec = (float)(b2 * fma(l32, (double)mz, (double)my));
+    f.zc = g3 * mz;
+    // y = L^-1 w, w = 2k (0, b, c): w^T Q^-1 w = y2^2 / D2 + y3^2 / D3
+    const double y2 = 2.0 * k * b, y3 = fma(-l32, y2, 2.0 * k * c);
+    f.r_ell = (float)(y2 * y2 / d2 + y3 * y3 / d3);
+    return true;
+}
+
 // Adds to M the moments of h = a * G about the Gaussian's centre for one lane's pair:
 // S[..] = sum h * delta^k, delta = mu - p, G = sum_c I_c g_c (g_c alone for
 // C == 1; I folds into the final scale).  Per voxel: h, h*dx by an FMA against
@@ -656,80 +718,79 @@ struct Moments {
 // dy, planes in dz.
 // Taking moments about the Gaussian (not the tile) keeps every sum
 // well-conditioned: h is large only where |delta| is small.
-// Every path evaluates the form in the offsets from the Gaussian, as the
-// reference forms sigma: per row R1 = Bn dy + Cn dz and R0 = Dn dy^2 + En dy dz
-// + Fn dz^2 (+ a per-path constant), and sigma2 = R0 + dx (R1 + A2 dx) at the
-// voxel dx_u.  (An expansion about the tile centre saves an operation per
-// voxel but its terms reach ~12 |A2| times the squared tile half-width and
-// cancel near a small Gaussian: ~5x the rounding of each a.)
-//   kGateFree: a = exp2(sigma2) * 2^bound, zero below the threshold by the
-//              flush of the product (bound = the gate-free offset, shift
-//              unused; 2^bound is one v_exp_f32 per lane).  The offset stays
-//              out of the exponent: an argument near -100 rounds to ~8e-6 in
-//              binary32, ~3e-6 relative in a;
-//   kChain (gate-free too): a row's a from three v_exp_f32 instead of eight,
-//              as products, which the binary32 flush-to-zero mode gates like
-//              v_exp_f32: a_u = 2^E_u * G_u with the lane's column factors
-//              G_u = 2^(A2 (dx_u - d)^2 - K) and E_u the rest of the exponent,
-//              linear in u (dx falls by 1 per column): 2^E at u = 0 and u = 4,
-//              each stepped three times.  chain_shift picks d = 0 (factors
-//              about the Gaussian's centre: E's terms stay near sigma2's own
-//              size) or, where that does not qualify, d = mx (about the tile
-//              centre), and K, which keeps every factor finite and every
+// The exponent a = 2^(sigma2 + ...) per mode:
+//   kRowsForm (gate-free): sigma2 = -(t^2 + c_r) from the row form (RowForm),
+//              t = tau = u_r - x_u with u_r = tau + al p'x per row and
+//              x_u = al p'_u per lane, c_r = eta^2 + zeta^2 per row;
+//              a = exp2(sigma2) * 2^off, zero below the threshold by the flush
+//              of the product (off = the gate-free offset, one v_exp_f32 per
+//              lane for 2^off).  The offset stays out of the exponent: an
+//              argument near -100 rounds to ~8e-6 in binary32, ~3e-6 relative
+//              in a;
+//   kRowsChain (gate-free too): a row's a from three v_exp_f32 instead of
+//              eight, as products, which the binary32 flush-to-zero mode gates
+//              like v_exp_f32: a_u = 2^E_u * G_u with the lane's column factors
+//              G_u = 2^(-x_u^2 - K) and E_u = sigma2_u + off + x_u^2 + K
+//              = (off + K - c_r - u_r^2) + 2 u_r x_u, linear in x_u: 2^E at
+//              u = 0 and u = 4, each stepped three times by 2^(2 al u_r).
+//              chain_shift picks K, which keeps every factor finite and every
 //              product of a chain up to a passing voxel above 2^-126;
-//   otherwise: a = exp2(s) if |s| <= bound, s = sigma2 - shift.
-template <int C, bool kGateFree, bool kChain = false>
-__device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int nz,
-                                             float mxl, float myl, float mzl, float A2, float Bn,
-                                             float Cn, float Dn, float En, float Fn, float shift,
-                                             float bound, float K, float dch, const float (&I)[C],
-                                             Moments<C> &M) {
-    static_assert(kGateFree || !kChain, "the chained rows are gate-free");
+//   kRowsExact: a = exp2(s) if |s| <= bound, s = sigma2 - shift, with sigma2 =
+//              R0 + dx (R1 + A2 dx) from the scaled conic (R1 = Bn dy + Cn dz,
+//              R0 = Dn dy^2 + En dy dz + Fn dz^2 per row): any conic, including
+//              indefinite and non-finite ones, as the reference evaluates it.
+constexpr int kRowsExact = 0, kRowsForm = 1, kRowsChain = 2;
+
+template <int C, int kMode>
+__device__ __forceinline__ void pair_moments(const float4 *s_rows, float mxl, float myl, float mzl,
+                                             const RowForm &f, float A2, float Bn, float Cn,
+                                             float Dn, float En, float Fn, float shift, float bound,
+                                             float K, const float (&I)[C], Moments<C> &M) {
+    constexpr bool kForm = kMode != kRowsExact, kChain = kMode == kRowsChain;
     // Sxx is only needed whole: the loop sums h per voxel column (col[u], a
     // two-operand add per voxel) and Sxx = sum_u dx_u^2 col[u] is formed once at
     // the end, instead of an FMA chain against dx_u^2 in every row
-    float dxu[GSV_TILE], col[GSV_TILE];
+    float dxu[GSV_TILE], col[GSV_TILE], xu[GSV_TILE];
 #pragma unroll
     for (int u = 0; u < GSV_TILE; ++u) {
         dxu[u] = mxl - ((float)u - 3.5f);
         col[u] = 0.f;
+        xu[u] = f.al * ((float)u - 3.5f);  // kForm: x_u = al p'_u
     }
-    constexpr bool kSym = kGateFree && !kChain;
-    // kSym: 2^bound, a normal number on live lanes (bound in [-126, -66]) and 0
-    // at the dead offset, where sigma2 is 0 (a zero form) and a = 1 * 0
-    const float Fb = kSym ? __builtin_amdgcn_exp2f(bound) : 0.f;
-    // kChain: G_u = 2^(A2 (dx_u - d)^2 - K) about dx = d (chain_shift's choice:
-    // 0, the Gaussian's centre, or mx, the tile's).  A2 (dx_u - d)^2 is formed
-    // with its rounding residual (two FMAs), applied as the factor
-    // 1 + lo ln 2, so each G_u is within ~1e-7 of its value; 2^-K is applied
-    // exactly.  Then E_u = sigma2 + off - A2 (dx_u - d)^2 + K
-    //   = dx_u (R1 + 2 A2 d) + R0 - A2 d^2 + off + K:
-    // the slope and constant take 2 A2 d and -A2 d^2 (both 0 for d = 0).
+    // kRowsForm: 2^off, a normal number on live lanes (off in [-126, -66]) and 0
+    // at the dead offset, where the form is 0 (zero coefficients) and a = 1 * 0
+    const float Fb = kMode == kRowsForm ? __builtin_amdgcn_exp2f(bound) : 0.f;
+    // kRowsChain: G_u = 2^(-x_u^2 - K), x_u^2 with its rounding residual (one
+    // FMA), applied as the factor 1 - lo ln 2, so each G_u is within ~1e-7 of
+    // its value; 2^-K is applied exactly.  The step 2^(2 al u_r) of a row
+    // takes al itself, and the chain's x_u = x_0 + u al holds up to the
+    // rounding of x_u (~6e-8 |x_u|, against the slope: ~1e-6 in E).
     float G[GSV_TILE];
     if (kChain) {
 #pragma unroll
         for (int u = 0; u < GSV_TILE; ++u) {
-            const float x = dch == 0.f ? dxu[u] : (float)u - 3.5f;  // dx_u - d, up to sign
-            const float p = A2 * x;
-            const float plo = fmaf(A2, x, -p);
-            const float hi = p * x;
-            const float lo = fmaf(plo, x, fmaf(p, x, -hi));
-            G[u] = ldexpf(__builtin_amdgcn_exp2f(hi) * fmaf(lo, kLn2, 1.0f), -(int)K);
+            const float hi = xu[u] * xu[u];
+            const float lo = fmaf(xu[u], xu[u], -hi);
+            G[u] = ldexpf(__builtin_amdgcn_exp2f(-hi) * fmaf(-lo, kLn2, 1.0f), -(int)K);
         }
     }
-    // the constant of R0: the chain's offset, shift and -A2 d^2, the exact
-    // path's shift; the chain's slope adds 2 A2 d
-    const float c0 =
-        kChain ? fmaf(-A2 * dch, dch, bound + K) : (kGateFree ? 0.f : -shift);
-    const float s0 = kChain ? 2.0f * A2 * dch : 0.f;
-    for (int lz = 0; lz < nz; ++lz) {
-        const float dz = mzl - ((float)lz - 3.5f);
-        const float Cdz = fmaf(Cn, dz, s0), Edz = En * dz;
-        const float R0z = fmaf(Fn * dz, dz, c0);
+    // the per-plane constant: the chain's offset and K (its E), the exact
+    // path's shift
+    const float c0 = kChain ? bound + K : (kForm ? 0.f : -shift);
+    for (int lz = 0; lz < GSV_TILE; ++lz) {
+        const float pz = (float)lz - 3.5f;
+        const float dz = mzl - pz;
+        // kForm: zeta, then -zeta^2 + c0, and the plane's parts of tau and eta
+        const float zt = kForm ? fmaf(-f.ga3, pz, f.zc) : 0.f;
+        const float zz = kForm ? fmaf(-zt, zt, c0) : 0.f;
+        const float tz = kForm ? fmaf(-f.ga, pz, f.tc) : 0.f;
+        const float ez = kForm ? fmaf(-f.ga2, pz, f.ec) : 0.f;
+        // kRowsExact: the plane's parts of R1 and R0
+        const float Cdz = kForm ? 0.f : Cn * dz, Edz = kForm ? 0.f : En * dz;
+        const float R0z = kForm ? 0.f : fmaf(Fn * dz, dz, c0);
         float Q0 = 0.f, Qx = 0.f, Qy = 0.f, Qxy = 0.f, Qyy = 0.f;
 #pragma unroll
         for (int ly = 0; ly < GSV_TILE; ++ly) {
-            if (ly >= ny) break;
             const int row = lz * GSV_TILE + ly;
             float gv[GSV_TILE * C];
 #pragma unroll
@@ -737,14 +798,24 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                 const float4 t4 = s_rows[row * 2 * C + q];
                 gv[4 * q] = t4.x; gv[4 * q + 1] = t4.y; gv[4 * q + 2] = t4.z; gv[4 * q + 3] = t4.w;
             }
-            const float dy = myl - ((float)ly - 3.5f);
-            const float R1 = fmaf(Bn, dy, Cdz);
-            const float R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
-            float sv[GSV_TILE];  // kChain: the row's a
+            const float py = (float)ly - 3.5f;
+            const float dy = myl - py;
+            float ur = 0.f, cr = 0.f, R1 = 0.f, R0 = 0.f;
+            if (kForm) {
+                ur = fmaf(-f.be, py, tz);              // u_r = tau + al p'x
+                const float et = fmaf(-f.be2, py, ez);  // eta
+                cr = fmaf(-et, et, zz);                 // -(eta^2 + zeta^2) (+ off + K)
+            } else {
+                R1 = fmaf(Bn, dy, Cdz);
+                R0 = fmaf(fmaf(Dn, dy, Edz), dy, R0z);
+            }
+            float sv[GSV_TILE];  // kRowsChain: the row's a
             if (kChain) {
-                const float step = __builtin_amdgcn_exp2f(-R1);                // 2^-R1
-                float e1 = __builtin_amdgcn_exp2f(fmaf(dxu[0], R1, R0));  // u = 0
-                float e2 = __builtin_amdgcn_exp2f(fmaf(dxu[4], R1, R0));  // u = 4
+                // E_u = q + 2 u_r x_u (2 x_u and 2 al are exact doublings)
+                const float q = fmaf(-ur, ur, cr);
+                const float step = __builtin_amdgcn_exp2f(ur * (2.0f * f.al));      // 2^(2 al u_r)
+                float e1 = __builtin_amdgcn_exp2f(fmaf(ur, 2.0f * xu[0], q));  // u = 0
+                float e2 = __builtin_amdgcn_exp2f(fmaf(ur, 2.0f * xu[4], q));  // u = 4
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     sv[k] = e1 * G[k];
@@ -761,12 +832,12 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, int ny, int n
                 float a;
                 if (kChain) {
                     a = sv[u];
+                } else if (kForm) {
+                    const float t = ur - xu[u];
+                    a = __builtin_amdgcn_exp2f(fmaf(-t, t, cr)) * Fb;  // flushed below 2^-126: the gate
                 } else {
                     const float s = fmaf(dxu[u], fmaf(dxu[u], A2, R1), R0);
-                    if (kGateFree)
-                        a = __builtin_amdgcn_exp2f(s) * Fb;  // flushed below 2^-126: the gate
-                    else
-                        a = (fabsf(s) <= bound) ? __builtin_amdgcn_exp2f(s) : 0.f;
+                    a = (fabsf(s) <= bound) ? __builtin_amdgcn_exp2f(s) : 0.f;
                 }
                 if (C == 1) {
                     h[u] = a * gv[u];
@@ -909,6 +980,8 @@ struct BwdLane {
     float I[C];
     Gate gt;
     TileGeom tg;
+    RowForm rf;  // gate-free pairs: the row form about the tile centre
+    float kch;   // gate-free pairs: chain_shift's K, or -1
 };
 
 // Emission slot of the pair (tile, g): e = cum[g-1] + ((tz-min.z)*ny +
@@ -1070,6 +1143,51 @@ __device__ __forceinline__ bool bwd_slots(const BwdArgs &a, int64_t p0, BwdLane<
     return nslots > 0;
 }
 
+// Shift K of the chained row evaluation of one gate-free pair (pair_moments,
+// kRowsChain), or -1 when the pair does not qualify.  With x_u = al p'_u
+// (|p'_u| <= 3.5, so x_u^2 <= 12.25 al^2), a_u = 2^E_u * G_u,
+// G_u = 2^(-x_u^2 - K) and E_u = sigma2_u + off + x_u^2 + K, linear in u with
+// the slope 2 al u_r per column (2 al u_r = 2k (a dx + b dy + c dz) at the row
+// centre, the form's x-slope), the chain is exact in binary32 flush-to-zero
+// arithmetic (every product below 2^-126 is 0 exactly where the reference's
+// gate fails, up to rounding at the threshold) when
+//  (a) every G_u >= 2^-125 and <= 1: 2 <= K <= 120 - 12.25 al^2;
+//  (b) along each chain (an anchor and three steps) no product before a
+//      passing voxel, where E >= -126 + K, falls below 2^-124: K >= 3M + 2
+//      with M >= |slope| on every row that can hold a passing voxel;
+//  (c) no step or E overflows on any row of the tile, live or dead: the slope
+//      stays below 120 over the tile's rows (m_tile), and E <= off + 12.25
+//      al^2 + K <= 54 everywhere since sigma2 <= 0.
+// M is the least of three bounds on the slope: m_tile; on a row whose gate
+// interval (half-width <= sqrt(k2 / Q_xx), k2 = -2 ln2 t2) meets the voxel
+// centres, whose peak then lies within 3.5 + sqrt(k2 / Q_xx) of the row
+// centre, 2 al^2 times that distance; and over the projection onto (y, z) of
+// the gate ellipsoid d^T Q d <= k2, where 2k (b dy + c dz) stays within
+// sqrt(k2 w^T Q^-1 w) of 0 (RowForm::r_ell), plus 2 al^2 |mx|.  K is the
+// admissible integer nearest -off: E at the Gaussian's peak is then near
+// x_u^2, where the exp2 arguments round least.  (Column factors about the
+// Gaussian's centre instead, x_u - al mx, step only by the form's coupling
+// but carry |x_u - al mx|^2 into E; measured at cfg3 they left ~1.9x as many
+// dconics elements outside rel 1e-4 / abs 1e-6 for an N(0,1) vol_grad.)
+// Binary32 margins: 1e-3 relative and 0.01 on M.
+template <int C>
+__device__ __forceinline__ float chain_shift(const BwdLane<C> &L) {
+    const RowForm &f = L.rf;
+    const float a2 = f.al * f.al;
+    const float m_tile = 2.0f * f.al * (fabsf(f.tc) + 3.5f * (fabsf(f.be) + fabsf(f.ga)));
+    if (!(m_tile < 120.0f)) return -1.0f;
+    const float k_max = floorf(120.0f - 12.25f * a2);
+    const float k2 = -2.0f * kLn2 * L.gt.t2;
+    const float m_reach =
+        2.0f * a2 * (3.5f + __builtin_amdgcn_sqrtf(fmaxf(k2 * __builtin_amdgcn_rcpf(L.ca), 0.f)));
+    const float m_ell =
+        2.0f * a2 * fabsf(L.mxl) + __builtin_amdgcn_sqrtf(fmaxf(k2 * f.r_ell, 0.f));
+    const float M = fminf(m_tile, fminf(m_ell, m_reach)) * 1.001f + 0.01f;
+    const float k_min = ceilf(3.0f * M) + 2.0f;
+    if (!(k_min <= k_max)) return -1.0f;
+    return fminf(k_max, fmaxf(k_min, rintf(-L.gt.off)));
+}
+
 // The lane's Gaussian, its gate and its offsets from the tile centre.
 template <int C>
 __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
@@ -1080,6 +1198,8 @@ __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
 #pragma unroll
     for (int c = 0; c < C; ++c) L.I[c] = 0.f;
     L.gt = make_gate(0.f);
+    L.rf = RowForm{};
+    L.kch = -1.0f;
     L.tg = tile_geom(L.valid ? L.tile : 0, a.fx, a.Tx, a.fy, a.Ty, a.D, a.H, a.W);
     if (!L.valid) return;
     const int g = a.ids[L.p];
@@ -1111,95 +1231,11 @@ __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
         L.mxl = pr.x - (float)tg.x0 - 4.0f;
         L.myl = pr.y - (float)tg.y0 - 4.0f;
         L.mzl = pr.z - (float)tg.z0 - 4.0f;
-    }
-}
-
-// Shift K of the chained row evaluation of one pair (pair_moments, kChain) and
-// the centre d of its column factors (*dch), or -1 when the pair does not
-// qualify.  With a_u = 2^E_u * G_u, G_u = 2^(A2 (dx_u - d)^2 - K) and
-// E_u = sigma2 + off - A2 (dx_u - d)^2 + K, linear in u with slope
-// -(R1 + 2 A2 d) per column (R1 = Bn dy + Cn dz), the chain is exact in binary32
-// flush-to-zero arithmetic (every product below 2^-126 is 0 exactly where the
-// reference's gate fails, up to rounding at the threshold) when
-//  (a) every G_u of a voxel that can pass is >= 2^-125 and every G_u <= 1;
-//  (b) along each chain (an anchor and three steps) no product before a
-//      passing voxel, where E >= -126 + K, falls below 2^-124: K >= 3M + 2
-//      with M >= |slope| on every row that can hold a passing voxel;
-//  (c) no step or E overflows on any row of the tile, live or dead.
-// d = 0 (about the Gaussian's centre) is preferred: E's terms then stay near
-// sigma2's own size, where their rounding costs least.  A voxel passes only
-// inside the gate ellipsoid d^T Q d <= k2, so there dx^2 <= k2 (Q^-1)_xx, and
-// in this tile |dx| <= |mx| + 3.5: K <= 125 + A2 max(...) gives (a); the
-// slope is R1, within sqrt(k2 w^T S w) over the ellipsoid's projection onto
-// (y, z) (w = (Bn, Cn), S the (y, z) block of Q^-1) and within m_tile over
-// the tile's rows; E_u = dx_u R1 + R0 + off + K is at most K - 66 +
-// min(|A2| dx_max, m_tile) dx_max (sigma2 <= 0, R0 <= 0, off <= -66), kept
-// below 127.  Strongly coupled conics (R1 large over the gate) fail (b)
-// there and take d = mx (about the tile centre): G_u = 2^(A2 p'^2 - K),
-// |p'| <= 3.5, with K + 12.25 |A2| <= 120 for (a); the slope 2 A2 mx + R1 is
-// within 2 |A2| (3.5 + sqrt(k2 / Q_xx)) on a row whose gate interval meets the
-// voxel centres (its peak lies that close to the row centre), within
-// |2 A2 mx| + sqrt(k2 w^T S w) over the ellipse and within that m_tile over the
-// tile; E <= -66 + 12.25 |A2| + K < 54 for (c).  With d = 0, E is off + K at
-// the Gaussian's centre, so K is the admissible integer nearest 126 + t2;
-// with d = mx it is the largest admissible one.  Both bring the exp2
-// arguments of the voxels that weigh most near 0, where they round least.
-// Binary32 margins: 1e-3 relative and 0.01 on M, 1e-3 on the ellipsoid's
-// extent (whose binary32 error the conditioning checks keep below 5e-4).
-template <int C>
-__device__ __forceinline__ float chain_shift(const BwdLane<C> &L, float A2, float Bn, float Cn,
-                                             float &dch) {
-    dch = 0.f;
-    const float k2 = -2.0f * kLn2 * L.gt.t2;
-    // sqrt(k2 w^T S w) = sqrt(k2 w^T Q^-1 w), w = (0, Bn, Cn), from the Cholesky
-    // factor Q = L L^T in binary32: w^T Q^-1 w = y2^2 + y3^2 with y = L^-1 w.
-    // With both pivots above 1e-3 of their diagonal (condition number below
-    // ~1e3) the relative error stays near 1e-4, inside the margins below; a
-    // worse-conditioned conic leaves this bound out (M only grows).
-    float m_ell = __builtin_inff();
-    const float i11 = __builtin_amdgcn_rsqf(L.ca);
-    const float l21 = L.cb * i11, l31 = L.cc * i11;
-    const float t22 = fmaf(-l21, l21, L.cd);
-    if (t22 > 1e-3f * L.cd) {
-        const float i22 = __builtin_amdgcn_rsqf(t22);
-        const float l32 = fmaf(-l31, l21, L.ce) * i22;
-        const float t33 = fmaf(-l32, l32, fmaf(-l31, l31, L.cf));
-        if (t33 > 1e-3f * L.cf) {
-            const float y2 = Bn * i22;
-            const float y3 = fmaf(-l32, y2, Cn) * __builtin_amdgcn_rsqf(t33);
-            m_ell = __builtin_amdgcn_sqrtf(fmaxf(k2 * fmaf(y2, y2, y3 * y3), 0.f));
+        if (L.fast) {
+            L.fast = row_form(L.ca, L.cb, L.cc, L.cd, L.ce, L.cf, L.mxl, L.myl, L.mzl, L.rf);
+            if (L.fast) L.kch = chain_shift(L);
         }
     }
-    const float r1_tile = fabsf(fmaf(Bn, L.myl, Cn * L.mzl)) + 3.5f * (fabsf(Bn) + fabsf(Cn));
-    // d = 0.  (Q^-1)_xx = (d f - e^2) / det: with the (y, z) minor above
-    // 1e-3 d f and the x pivot det / (d f - e^2) above 1e-3 a, both are within
-    // ~5e-4 of their values; det stays within the reciprocal's normal range
-    const float cfx = fmaf(L.cd, L.cf, -L.ce * L.ce);
-    const float det = L.ca * cfx - L.cb * fmaf(L.cb, L.cf, -L.cc * L.ce) +
-                      L.cc * fmaf(L.cb, L.ce, -L.cc * L.cd);
-    const float dx_max = fabsf(L.mxl) + 3.5f;
-    if (cfx > 1e-3f * (L.cd * L.cf) && det > 1e-3f * (L.ca * cfx) && det > 0x1p-100f &&
-        det < 0x1p100f && r1_tile < 120.0f) {
-        const float g_ell = A2 * (k2 * cfx * __builtin_amdgcn_rcpf(det));  // A2 k2 (Q^-1)_xx
-        const float g_min = fmaxf(g_ell, A2 * (dx_max * dx_max));             // <= 0
-        const float k_max = floorf(fminf(120.0f, 125.0f + 1.001f * g_min));
-        const float M = fminf(r1_tile, m_ell) * 1.001f + 0.01f;
-        const float k_min = ceilf(3.0f * M) + 2.0f;
-        // E at the Gaussian's centre is off + K: nearest 0 at K = 126 + t2
-        const float K = fminf(k_max, fmaxf(k_min, floorf(126.5f + L.gt.t2)));
-        if (k_min <= K && fminf(-A2 * dx_max, r1_tile) * dx_max + K < 190.0f) return K;
-    }
-    // d = mx
-    const float m_tile = fabsf(fmaf(2.0f * A2, L.mxl, fmaf(Bn, L.myl, Cn * L.mzl))) +
-                         3.5f * (fabsf(Bn) + fabsf(Cn));
-    if (!(m_tile < 120.0f)) return -1.0f;
-    const float K = floorf(120.0f - 12.25f * fabsf(A2));
-    const float m_reach = fabsf(2.0f * A2) *
-                          (3.5f + __builtin_amdgcn_sqrtf(fmaxf(k2 * __builtin_amdgcn_rcpf(L.ca), 0.f)));
-    const float M = fminf(m_tile, fminf(fabsf(2.0f * A2 * L.mxl) + m_ell, m_reach)) * 1.001f + 0.01f;
-    if (!(ceilf(3.0f * M) + 2.0f <= K)) return -1.0f;
-    dch = L.mxl;
-    return K;
 }
 
 // Exponent e such that m * 2^e lies in [2^(kGradScaleExp-1), 2^kGradScaleExp);
@@ -1354,25 +1390,25 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
         }
         __syncthreads();
         const int my = in_grp ? L.slot - g0 : 0;
-        // lanes outside the group evaluate a zero form at the dead offset (a = 0)
-        const float A2 = in_grp ? -0.5f * kLog2e * L.ca : 0.f, Bn = in_grp ? -kLog2e * L.cb : 0.f;
-        const float Cn = in_grp ? -kLog2e * L.cc : 0.f, Dn = in_grp ? -0.5f * kLog2e * L.cd : 0.f;
-        const float En = in_grp ? -kLog2e * L.ce : 0.f, Fn = in_grp ? -0.5f * kLog2e * L.cf : 0.f;
         const float gx = in_grp ? L.mxl : 0.f, gy = in_grp ? L.myl : 0.f, gz = in_grp ? L.mzl : 0.f;
         if (wave_fast) {
+            // lanes outside the group: a zero form (zero coefficients) at the dead offset
+            const RowForm rf = in_grp ? L.rf : RowForm{};
             const float off = in_grp ? L.gt.off : kDeadOffset;
-            float dch = 0.f;
-            const float kshift = in_grp ? chain_shift(L, A2, Bn, Cn, dch) : 2.0f;
+            const float kshift = in_grp ? L.kch : 2.0f;
             if (a.chain && __all(kshift >= 0.f))
-                pair_moments<C, true, true>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn,
-                                            Cn, Dn, En, Fn, 0.f, off, kshift, dch, L.I, M);
+                pair_moments<C, kRowsChain>(s_g + my * kSlot, gx, gy, gz, rf, 0.f, 0.f, 0.f, 0.f, 0.f,
+                                            0.f, 0.f, off, kshift, L.I, M);
             else
-                pair_moments<C, true>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn, Cn,
-                                      Dn, En, Fn, 0.f, off, 0.f, 0.f, L.I, M);
+                pair_moments<C, kRowsForm>(s_g + my * kSlot, gx, gy, gz, rf, 0.f, 0.f, 0.f, 0.f, 0.f,
+                                           0.f, 0.f, off, 0.f, L.I, M);
         } else {
-            pair_moments<C, false>(s_g + my * kSlot, GSV_TILE, GSV_TILE, gx, gy, gz, A2, Bn, Cn,
-                                   Dn, En, Fn, L.gt.shift, in_grp ? L.gt.half : -1.f, 0.f, 0.f,
-                                   L.I, M);
+            // lanes outside the group: a zero form, never inside the gate (|s| <= -1)
+            const float A2 = in_grp ? -0.5f * kLog2e * L.ca : 0.f, Bn = in_grp ? -kLog2e * L.cb : 0.f;
+            const float Cn = in_grp ? -kLog2e * L.cc : 0.f, Dn = in_grp ? -0.5f * kLog2e * L.cd : 0.f;
+            const float En = in_grp ? -kLog2e * L.ce : 0.f, Fn = in_grp ? -0.5f * kLog2e * L.cf : 0.f;
+            pair_moments<C, kRowsExact>(s_g + my * kSlot, gx, gy, gz, RowForm{}, A2, Bn, Cn, Dn, En,
+                                        Fn, L.gt.shift, in_grp ? L.gt.half : -1.f, 0.f, L.I, M);
         }
         __syncthreads();  // a later group restages the slots
     }

@@ -1,9 +1,10 @@
 """The chained row evaluation of the voxelize kernels, checked on the CPU.
 
 Both voxelize kernels form most exp2 values of an 8-voxel row as products
-(an anchor 2^E and a step along the row, times per-Gaussian column factors:
-2^(A2 uc^2 - K) about the tile centre in the forward, 2^(A2 dx_u^2 - K) about
-the Gaussian's centre in the backward) and rely on binary32 flush-to-zero for
+(an anchor 2^E and a step along the row, times per-pair column factors:
+2^(A2 uc^2 - K) about the tile centre in the forward, 2^(-x_u^2 - K) in the
+backward's row form, the LDL^T coordinates of the conic about the tile centre)
+and rely on binary32 flush-to-zero for
 the reference's 1e-6 gate: a product below 2^-126 is 0.  That is only the gate if no factor of a chain flushes before a
 passing voxel and nothing overflows, which the choice of K guarantees for the
 pairs that qualify (csrc/voxelize.hip: the forward's record set-up and
@@ -173,93 +174,100 @@ def _fma(a, b, c):
         return _ftz(np.float64(a) * np.float64(b) + np.float64(c))
 
 
+def _row_form(P):
+    """row_form (csrc/voxelize.hip) per pair: the binary64 LDL^T factor of the
+    conic and the row-form coefficients about the tile centre, rounded to
+    binary32 as the kernel rounds them.  Returns (ok, al, be, ga, be2, ga2,
+    ga3, tc, ec, zc, r_ell)."""
+    F = np.float32
+    mx, my, mz = (P[:, i].astype(F).astype(np.float64) for i in range(3))
+    a, b, c, d, e, f = (P[:, 3 + i].astype(F).astype(np.float64) for i in range(6))
+    k = 0.5 * L2E
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        l21, l31 = b / a, c / a
+        d2, e2, f2 = d - b * l21, e - c * l21, f - c * l31
+        l32 = e2 / d2
+        d3 = f2 - e2 * l32
+        p1, p2, p3 = k * a, k * d2, k * d3
+        ok = np.ones(len(P), bool)
+        for pv in (p1, p2, p3):
+            ok &= (pv >= 2.0 ** -100) & (pv <= 2.0 ** 100)
+        al = np.sqrt(p1.astype(F)).astype(np.float64)
+        b2 = np.sqrt(p2.astype(F)).astype(np.float64)
+        g3 = np.sqrt(p3.astype(F)).astype(np.float64)
+        y2 = 2.0 * k * b
+        y3 = 2.0 * k * c - l32 * y2
+        r_ell = y2 * y2 / d2 + y3 * y3 / d3
+        out = (al, al * l21, al * l31, b2, b2 * l32, g3, al * (mx + l21 * my + l31 * mz),
+               b2 * (my + l32 * mz), g3 * mz.astype(F), r_ell)
+    z = F(0)
+    out = tuple(np.where(ok, _f(v), z).astype(F) for v in out)
+    return (ok,) + out
+
+
 def _backward_chains(P):
     """The backward's rows (lane = pair, rows walked in order), as pair_moments
-    with kChain forms them: a_u = 2^E_u * G_u with the column factors
-    G_u = 2^(A2 (dx_u - d)^2 - K) (with the rounding residual of the
-    exponent) and E_u linear in u, 2^E at u = 0 and u = 4 stepped along the
-    row; and chain_shift's choice of d (0, the Gaussian's centre, or mx, the
-    tile's) and K.  Returns (a, qualifies, excluded, centred): excluded are the
-    pairs that pass the Gaussian-centred conditions but the dead-row bounds
-    and have no tile-centred fallback, centred those that take d = 0."""
+    with kRowsChain forms them from the row form (LDL^T coordinates of the
+    conic about the tile centre): a_u = 2^E_u * G_u with the column factors
+    G_u = 2^(-x_u^2 - K) (x_u = al p'_u, with the rounding residual of the
+    square) and E_u = q_r + 2 u_r x_u linear in u, 2^E at u = 0 and u = 4
+    stepped three times by 2^(2 al u_r); and chain_shift's K.  Returns (a,
+    qualifies, excluded, K): excluded are the pairs whose rows that can hold a
+    passing voxel qualify but whose tile's other rows exceed the slope bound
+    (m_tile >= 120); their rows are evaluated with that K anyway."""
     uc, py, pz = _grid()
     F = np.float32
-    mx, my, mz = (P[:, i].astype(F) for i in range(3))
-    ca, cb, cc_, cd, ce, cf = (P[:, 3 + i].astype(F) for i in range(6))
+    mx = P[:, 0].astype(F)
+    ca = P[:, 3].astype(F)
     t2 = P[:, 9].astype(F)
     off = (-(t2 + F(126.0))).astype(F)
-    A2 = F(-0.5 * L2E) * ca
-    Bn, Cn = F(-L2E) * cb, F(-L2E) * cc_
-    Dn, En, Fn = F(-0.5 * L2E) * cd, F(-L2E) * ce, F(-0.5 * L2E) * cf
+    ok, al, be, ga, be2, ga2, ga3, tc, ec, zc, r_ell = _row_form(P)
     with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        a2 = _f(al * al)
         k2 = (F(-2.0 * 0.693147180559945309) * t2).astype(F)
-        i11 = (F(1) / np.sqrt(ca)).astype(F)
-        l21, l31 = cb * i11, cc_ * i11
-        t22 = _fma(-l21, l21, cd)
-        i22 = (F(1) / np.sqrt(t22)).astype(F)
-        l32 = _f(_fma(-l31, l21, ce) * i22)
-        t33 = _fma(-l32, l32, _fma(-l31, l31, cf))
-        y2 = Bn * i22
-        y3 = _f(_fma(-l32, y2, Cn) * (F(1) / np.sqrt(t33)).astype(F))
-        m_ell = np.sqrt(np.maximum(k2 * _fma(y2, y2, y3 * y3), F(0))).astype(F)
-        m_ell = np.where((t22 > F(1e-3) * cd) & (t33 > F(1e-3) * cf), m_ell,
-                         np.float32(np.inf)).astype(F)
-        r1_tile = _f(np.abs(_fma(Bn, my, Cn * mz)) + F(3.5) * (np.abs(Bn) + np.abs(Cn)))
-        # d = 0
-        cfx = _fma(cd, cf, -(ce * ce))
-        det = _f(ca * cfx - cb * _fma(cb, cf, -(cc_ * ce)) + cc_ * _fma(cb, ce, -(cc_ * cd)))
-        dx_max = _f(np.abs(mx) + F(3.5))
-        cond = ((cfx > F(1e-3) * (cd * cf)) & (det > F(1e-3) * (ca * cfx)) & (det > F(2.0 ** -100))
-                & (det < F(2.0 ** 100)) & (r1_tile < F(120.0)))
-        g_ell = _f(A2 * _f(k2 * cfx * _f(F(1) / det)))
-        g_min = np.maximum(g_ell, _f(A2 * (dx_max * dx_max)))
-        Kmax = np.floor(np.minimum(F(120.0), F(125.0) + F(1.001) * g_min)).astype(F)
-        M0 = (np.minimum(r1_tile, m_ell) * F(1.001) + F(0.01)).astype(F)
-        Kmin = np.ceil(F(3.0) * M0) + 2
-        K0 = np.minimum(Kmax, np.maximum(Kmin, np.floor(F(126.5) + t2))).astype(F)
-        live0 = cond & (Kmin <= K0)
-        dead0 = np.minimum(-A2 * dx_max, r1_tile) * dx_max + K0 < F(190.0)
-        centred = live0 & dead0
-        # d = mx
-        m_tile = _f(np.abs(_fma(F(2.0) * A2, mx, _fma(Bn, my, Cn * mz))) +
-                    F(3.5) * (np.abs(Bn) + np.abs(Cn)))
-        K1 = np.floor(F(120.0) - F(12.25) * np.abs(A2)).astype(F)
-        m_reach = (np.abs(F(2) * A2) * (F(3.5) + np.sqrt(np.maximum(k2 / ca, F(0))))).astype(F)
-        M1 = (np.minimum(m_tile, np.minimum(np.abs(F(2) * A2 * mx) + m_ell, m_reach)) * F(1.001)
-              + F(0.01)).astype(F)
-        tile_ok = (m_tile < F(120.0)) & (np.ceil(F(3.0) * M1) + 2 <= K1)
-    qualifies = centred | tile_ok
-    K = np.where(centred, K0, np.where(tile_ok, K1, np.where(live0, K0, F(2.0)))).astype(F)
-    d = np.where(centred | ~tile_ok, F(0), mx).astype(F)
-    dxu = _f(mx[:, None] - uc[None, :].astype(F))                      # (N, 8)
-    x = np.where((d == 0)[:, None], dxu, uc[None, :].astype(F)).astype(F)
-    p = _f(A2[:, None] * x)
-    plo = _fma(A2[:, None], x, -p)
-    hi = _f(p * x)
-    lo = _fma(plo, x, _fma(p, x, -hi))
+        m_tile = _f(F(2.0) * al * _f(np.abs(tc) + F(3.5) * (np.abs(be) + np.abs(ga))))
+        k_max = np.floor(F(120.0) - F(12.25) * a2).astype(F)
+        m_reach = _f(F(2.0) * a2 * _f(F(3.5) + np.sqrt(np.maximum(k2 / ca, F(0))).astype(F)))
+        m_ell = _f(F(2.0) * a2 * np.abs(mx) + np.sqrt(np.maximum(k2 * r_ell, F(0))).astype(F))
+        m_rows = np.minimum(m_ell, m_reach)
+        M = _f(np.minimum(m_tile, m_rows) * F(1.001) + F(0.01))
+        k_min = (np.ceil(F(3.0) * M) + 2).astype(F)
+        rows_ok = ok & (np.ceil(F(3.0) * _f(m_rows * F(1.001) + F(0.01))) + 2 <= k_max)
+        qualifies = ok & (m_tile < F(120.0)) & (k_min <= k_max)
+        K = np.minimum(k_max, np.maximum(k_min, np.rint(-off))).astype(F)
+        K = np.where(qualifies, K, np.maximum(k_max, F(2.0))).astype(F)
+    excluded = rows_ok & ~(m_tile < F(120.0))
+    xu = _f(al[:, None] * uc[None, :].astype(F))                       # (N, 8)
+    hi = _f(xu * xu)
+    lo = _fma(xu, xu, -hi)
     with np.errstate(over="ignore"):
-        G = _ftz(np.ldexp(np.float64(_f(np.float64(_exp2(hi)) * _fma(lo, F(0.693147180559945309), F(1)))),
+        G = _ftz(np.ldexp(np.float64(_f(np.float64(_exp2(-hi)) *
+                                         _fma(-lo, F(0.693147180559945309), F(1)))),
                           -K.astype(np.int64)[:, None]))
-    c0 = _fma(-A2 * d, d, _f(off + K))
-    s0 = _f(F(2.0) * A2 * d)
+    c0 = _f(off + K)
+    al2 = _f(F(2.0) * al)
     out = np.zeros((P.shape[0], 64, 8), np.float32)
     for lz in range(8):
-        dz = _f(mz - F(lz - 3.5))
-        Cdz, Edz = _fma(Cn, dz, s0), _f(En * dz)
-        R0z = _fma(_f(Fn * dz), dz, c0)
+        pzl = F(lz - 3.5)
+        zt = _fma(-ga3, pzl, zc)
+        zz = _fma(-zt, zt, c0)
+        tz = _fma(-ga, pzl, tc)
+        ez = _fma(-ga2, pzl, ec)
         for ly in range(8):
             row = lz * 8 + ly
-            dy = _f(my - F(ly - 3.5))
-            R1 = _fma(Bn, dy, Cdz)
-            R0 = _fma(_fma(Dn, dy, Edz), dy, R0z)
-            step = _exp2(-R1)
-            e1 = _exp2(_fma(dxu[:, 0], R1, R0))
-            e2 = _exp2(_fma(dxu[:, 4], R1, R0))
+            pyl = F(ly - 3.5)
+            ur = _fma(-be, pyl, tz)
+            et = _fma(-be2, pyl, ez)
+            cr = _fma(-et, et, zz)
+            q = _fma(-ur, ur, cr)
+            step = _exp2(_f(ur * al2))
+            e1 = _exp2(_fma(ur, _f(F(2.0) * xu[:, 0]), q))
+            e2 = _exp2(_fma(ur, _f(F(2.0) * xu[:, 4]), q))
             for k in range(4):
                 out[:, row, k] = _mul(e1, G[:, k])
                 out[:, row, 4 + k] = _mul(e2, G[:, 4 + k])
                 e1, e2 = _mul(e1, step), _mul(e2, step)
-    return out, qualifies, live0 & ~dead0 & ~tile_ok, centred
+    return out, qualifies, excluded, K
 
 
 def _random_pairs(n, seed):
@@ -327,7 +335,7 @@ def test_chained_rows_gate_like_exp2(name, make, npairs, share):
     s_exact = _exact_exponent(P)
     fwd, fwd_ok = _forward_chains(P)
     n_f, live_f = _check(f"{name} forward", s_exact, fwd, fwd_ok)
-    # the backward walks the same rows with the Gaussian-centred form
+    # the backward walks the same rows with its row form
     bwd, bwd_ok, _, _ = _backward_chains(P)
     n_b, live_b = _check(f"{name} backward", s_exact, bwd, bwd_ok)
     assert n_f > share * len(P) and n_b > share * len(P), (name, n_f, n_b, len(P))
@@ -343,44 +351,42 @@ def test_backward_chain_bounds_dead_rows():
     excluded pairs overflow."""
     P = np.concatenate([_random_pairs(12000, seed=5), _needle_pairs(6000, seed=9)])
     s_exact = _exact_exponent(P)
-    bwd, ok, excluded, centred = _backward_chains(P)
+    bwd, ok, excluded, _ = _backward_chains(P)
     n_b, live_b = _check("conics and needles backward", s_exact, bwd, ok)
     assert n_b > 0.3 * len(P) and live_b > 0, (n_b, len(P))
     # the scene exercises the conditions: without them these pairs would take
     # the chains and some of their products would overflow
-    assert excluded.sum() > 0.01 * len(P), int(excluded.sum())
+    assert excluded.sum() >= 100, int(excluded.sum())
     assert not np.isfinite(bwd[excluded]).all()
 
 
-def test_backward_ellipse_bound_in_binary32():
-    """chain_shift's slope bound over the gate ellipse, sqrt(k2 w^T Q^-1 w) with
-    w = (0, Bn, Cn), from a binary32 Cholesky factor of the conic: wherever both
-    pivots stay above 1e-3 of their diagonal it agrees with the binary64
-    cofactor formula to 2e-4 relative (the kernel's margin is 1e-3 + 0.01), on
-    random rotated conics, narrow ones and tilted needles."""
-    P = np.concatenate([_random_pairs(12000, seed=15), _needle_pairs(6000, seed=16)])
-    F = np.float32
-    ca, cb, cc_, cd, ce, cf = (P[:, 3 + i].astype(F) for i in range(6))
-    t2 = P[:, 9].astype(F)
-    Bn, Cn = F(-L2E) * cb, F(-L2E) * cc_
-    k2 = (F(-2.0 * 0.693147180559945309) * t2).astype(F)
-    with np.errstate(divide="ignore", invalid="ignore"):
-        i11 = (F(1) / np.sqrt(ca)).astype(F)
-        l21, l31 = cb * i11, cc_ * i11
-        t22 = (cd - l21 * l21).astype(F)
-        i22 = (F(1) / np.sqrt(t22)).astype(F)
-        l32 = ((ce - l31 * l21) * i22).astype(F)
-        t33 = (cf - l31 * l31 - l32 * l32).astype(F)
-        y2 = Bn * i22
-        y3 = ((Cn - l32 * y2) / np.sqrt(t33)).astype(F)
-        got = np.sqrt(np.maximum(k2 * (y2 * y2 + y3 * y3), F(0))).astype(np.float64)
-    ok = (t22 > F(1e-3) * cd) & (t33 > F(1e-3) * cf)
-    a, b, c, d, e, f = (v.astype(np.float64) for v in (ca, cb, cc_, cd, ce, cf))
+def test_backward_row_form_is_the_quadratic_form():
+    """row_form's LDL^T coordinates: -(tau^2 + eta^2 + zeta^2), from the
+    binary32-rounded coefficients exactly as the kernel combines them, equals
+    sigma2 = -log2(e)/2 * delta^T Q delta for every voxel of the tile to
+    within 5e-6 of the larger of |sigma2| and 1 (the binary32 rounding of
+    coefficients of up to ~10 that multiply |p'| <= 3.5), and r_ell equals w^T Q^-1 w
+    (w = log2(e) (0, b, c)) from the binary64 cofactors to 1e-6 relative; on
+    rotated anisotropic conics and tilted needles."""
+    P = np.concatenate([_random_pairs(6000, seed=15), _needle_pairs(3000, seed=16)])
+    ok, al, be, ga, be2, ga2, ga3, tc, ec, zc, r_ell = (np.asarray(v, np.float64)
+                                                         for v in _row_form(P))
+    ok = ok.astype(bool)
+    assert ok.mean() > 0.99, ok.mean()
+    uc, py, pz = _grid()
+    tau = tc[:, None, None] - al[:, None, None] * uc[None, None, :] - \
+        (be[:, None] * py[None, :] + ga[:, None] * pz[None, :])[:, :, None]
+    eta = (ec[:, None] - be2[:, None] * py[None, :] - ga2[:, None] * pz[None, :])[:, :, None]
+    zeta = (zc[:, None] - ga3[:, None] * pz[None, :])[:, :, None]
+    got = -(tau * tau + eta * eta + zeta * zeta)
+    t2 = P[:, 9]
+    want = _exact_exponent(P) + (t2 + 126.0)[:, None, None]      # sigma2 alone
+    err = np.abs(got - want) / np.maximum(np.abs(want), 1.0)
+    assert err[ok].max() <= 5e-6, err[ok].max()
+    a, b, c, d, e, f = (P[:, 3 + i].astype(np.float32).astype(np.float64) for i in range(6))
     syy, szz, syz = a * f - c * c, a * d - b * b, b * c - a * e
     det = a * (d * f - e * e) - b * (b * f - c * e) + c * (b * e - c * d)
-    gb, gc = Bn.astype(np.float64), Cn.astype(np.float64)
-    ref = np.sqrt(np.maximum(k2.astype(np.float64) *
-                             (gb * gb * syy + 2 * gb * gc * syz + gc * gc * szz) / det, 0))
-    assert ok.mean() > 0.9, ok.mean()
-    rel = np.abs(got[ok] - ref[ok]) / np.maximum(ref[ok], 1e-30)
-    assert rel.max() <= 2e-4, rel.max()
+    gb, gc = L2E * b, L2E * c
+    ref = (gb * gb * syy + 2 * gb * gc * syz + gc * gc * szz) / det
+    rel = np.abs(r_ell[ok] - ref[ok]) / ref[ok]
+    assert rel.max() <= 1e-6, rel.max()
