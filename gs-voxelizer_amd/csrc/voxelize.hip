@@ -734,7 +734,15 @@ __device__ __forceinline__ bool row_form(float ca, float cb, float cc, float cd,
 //              = (off + K - c_r - u_r^2) + 2 u_r x_u, linear in x_u: 2^E at
 //              u = 0 and u = 4, each stepped three times by 2^(2 al u_r).
 //              chain_shift picks K, which keeps every factor finite and every
-//              product of a chain up to a passing voxel above 2^-126;
+//              product of a chain up to a passing voxel above 2^-126.  Its
+//              rounding: the step's exponent (|2 al u_r| up to ~40, rounded once
+//              per row) and each anchor's (up to 3 columns from the voxels it
+//              serves) enter up to 4 values at once, where the form path
+//              rounds only per-voxel quantities near sigma2's own size; at cfg3
+//              and cfg5 the chained rows leave ~1.5-3x as many gradient
+//              elements as the form path outside rel 1e-4 / abs 1e-6 of the
+//              binary64 value for an N(0,1) vol_grad, and run the backward
+//              ~20 % faster (GSV_BWD_CHAIN=0 selects the form path);
 //   kRowsExact: a = exp2(s) if |s| <= bound, s = sigma2 - shift, with sigma2 =
 //              R0 + dx (R1 + A2 dx) from the scaled conic (R1 = Bn dy + Cn dz,
 //              R0 = Dn dy^2 + En dy dz + Fn dz^2 per row): any conic, including
@@ -760,18 +768,25 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, float mxl, fl
     // kRowsForm: 2^off, a normal number on live lanes (off in [-126, -66]) and 0
     // at the dead offset, where the form is 0 (zero coefficients) and a = 1 * 0
     const float Fb = kMode == kRowsForm ? __builtin_amdgcn_exp2f(bound) : 0.f;
-    // kRowsChain: G_u = 2^(-x_u^2 - K), x_u^2 with its rounding residual (one
-    // FMA), applied as the factor 1 - lo ln 2, so each G_u is within ~1e-7 of
-    // its value; 2^-K is applied exactly.  The step 2^(2 al u_r) of a row
-    // takes al itself, and the chain's x_u = x_0 + u al holds up to the
-    // rounding of x_u (~6e-8 |x_u|, against the slope: ~1e-6 in E).
+    // kRowsChain: G_u = 2^(-x_u^2 - K) at the positions the chain implies,
+    // x_u = x_a + (u - a) al from its anchor a (0 or 4; x_0 and x_4 as the
+    // anchors' exponents take them, x_4 = al/2 exactly) and the step's exact
+    // multiples of al: x_u^2 in binary64, its binary32 rounding residual applied
+    // as the factor 1 + lo ln 2, so each G_u is within ~1e-7 of its value;
+    // 2^-K is applied exactly.  (G_u from the separately rounded al p'_u
+    // instead differs from the chain's exponents by 2 u_r (x_u - x_a - (u - a)
+    // al), the same in every row and tile of the Gaussian, which does not
+    // average out of its sums: at cfg5 1.3x as many dpos and dintensities
+    // elements outside rel 1e-4 / abs 1e-6 for an N(0,1) vol_grad.)
     float G[GSV_TILE];
     if (kChain) {
 #pragma unroll
         for (int u = 0; u < GSV_TILE; ++u) {
-            const float hi = xu[u] * xu[u];
-            const float lo = fmaf(xu[u], xu[u], -hi);
-            G[u] = ldexpf(__builtin_amdgcn_exp2f(-hi) * fmaf(-lo, kLn2, 1.0f), -(int)K);
+            const double xe = (double)xu[u < 4 ? 0 : 4] + (double)f.al * (u < 4 ? u : u - 4);
+            const double d = -xe * xe;
+            const float hi = (float)d;
+            const float lo = (float)(d - (double)hi);
+            G[u] = ldexpf(__builtin_amdgcn_exp2f(hi) * fmaf(lo, kLn2, 1.0f), -(int)K);
         }
     }
     // the per-plane constant: the chain's offset and K (its E), the exact

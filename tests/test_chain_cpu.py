@@ -208,13 +208,14 @@ def _row_form(P):
 def _backward_chains(P):
     """The backward's rows (lane = pair, rows walked in order), as pair_moments
     with kRowsChain forms them from the row form (LDL^T coordinates of the
-    conic about the tile centre): a_u = 2^E_u * G_u with the column factors
-    G_u = 2^(-x_u^2 - K) (x_u = al p'_u, with the rounding residual of the
-    square) and E_u = q_r + 2 u_r x_u linear in u, 2^E at u = 0 and u = 4
-    stepped three times by 2^(2 al u_r); and chain_shift's K.  Returns (a,
-    qualifies, excluded, K): excluded are the pairs whose rows that can hold a
-    passing voxel qualify but whose tile's other rows exceed the slope bound
-    (m_tile >= 120); their rows are evaluated with that K anyway."""
+    conic about the tile centre): a_u = 2^E_u * G_u with E_u = q_r + 2 u_r x_u
+    (q_r = c_r - u_r^2, c_r holding off + K) at the anchors u = 0 and u = 4,
+    each stepped three times by 2^(2 al u_r), times the column factors
+    G_u = 2^(-x_u^2 - K) at the positions the chain implies (x_a + (u - a) al,
+    the square in binary64 with its binary32 residual); and chain_shift's K.
+    Returns (a, qualifies, excluded, K): excluded are the pairs whose rows that
+    can hold a passing voxel qualify but whose tile's other rows exceed the
+    slope bound (m_tile >= 120); their rows are evaluated with that K anyway."""
     uc, py, pz = _grid()
     F = np.float32
     mx = P[:, 0].astype(F)
@@ -238,11 +239,14 @@ def _backward_chains(P):
         K = np.where(qualifies, K, np.maximum(k_max, F(2.0))).astype(F)
     excluded = rows_ok & ~(m_tile < F(120.0))
     xu = _f(al[:, None] * uc[None, :].astype(F))                       # (N, 8)
-    hi = _f(xu * xu)
-    lo = _fma(xu, xu, -hi)
+    anc = xu[:, [0, 0, 0, 0, 4, 4, 4, 4]].astype(np.float64)
+    xe = anc + al[:, None].astype(np.float64) * np.array([0, 1, 2, 3, 0, 1, 2, 3])
+    d = -xe * xe
+    hi = _f(d)
+    lo = _f(d - hi.astype(np.float64))
     with np.errstate(over="ignore"):
-        G = _ftz(np.ldexp(np.float64(_f(np.float64(_exp2(-hi)) *
-                                         _fma(-lo, F(0.693147180559945309), F(1)))),
+        G = _ftz(np.ldexp(np.float64(_f(np.float64(_exp2(hi)) *
+                                         _fma(lo, F(0.693147180559945309), F(1)))),
                           -K.astype(np.int64)[:, None]))
     c0 = _f(off + K)
     al2 = _f(F(2.0) * al)
