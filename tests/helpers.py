@@ -120,20 +120,26 @@ def normalised_error_percentiles(got, truth, allow_extra, rtol, atol, qs):
 #   - 99.9th percentile of the normalised error: at most P999_FACTOR * the
 #     oracle's, or 0.1;
 #   - worst normalised error: at most WORST_FACTOR * the oracle's, or 1.
-# The device evaluates each exp2 of a chained row as products of an anchor, a
-# step and a column factor whose arguments reach |30|-|40| in binary32 (the
-# flush-to-zero gate needs them there), ~1e-6 relative per value where the
-# reference's single expf of |sigma| <= ~14 is ~2e-7; on sums that cancel below
-# 1e-4 of their terms that shows as up to ~3x more elements outside the bound
-# and ~1.6x the oracle's 99.9th percentile (cfg3, cfg2, the reference's
-# scenario); elsewhere the device is as accurate or better.
+# Two tiers.  The default backward evaluates most rows as chained products (an
+# anchor exp2 stepped along the row), whose exponent roundings (a per-row
+# slope of up to ~40, an anchor up to 3 columns from the voxels it serves)
+# are shared by several voxels and so average out of the gradient sums less
+# than the oracle's per-voxel roundings: measured (cfg3, cfg5's 100k sample,
+# N(0,1) vol_grad) it leaves ~0.3-2.5x the oracle's count of elements outside
+# the bound, the most on cfg5's dpos and dintensities, and up to ~1.7x its
+# 99.9th percentile.  With the chained rows off (GSV_BWD_CHAIN=0 or
+# gsv_set_backward_chains(0): every row from the per-voxel form) the device is
+# at or below the oracle's count in every such comparison, and STRICT holds.
 COUNT_SLACK_REL, COUNT_SLACK_ABS, P999_FACTOR, WORST_FACTOR = 3.0, 10, 2.0, 4.0
+STRICT = dict(count_rel=1.25, count_abs=10, p999=1.5, worst=2.0)
 
 
-def assert_no_less_accurate(name, got, oracle32, truth, allow_extra=None, rtol=1e-4, atol=1e-6):
+def assert_no_less_accurate(name, got, oracle32, truth, allow_extra=None, rtol=1e-4, atol=1e-6,
+                            strict=False):
     """The device result `got` is no less accurate than the binary32 oracle's
     `oracle32` against the binary64 `truth` (each within atol + rtol*|truth| +
-    allow_extra per element), up to the slack above.  The statistics are logged
+    allow_extra per element), up to the slack above (STRICT's with `strict`).
+    The statistics are logged
     (GSV_MARGIN_LOG: name, elements, device count, oracle count, device worst,
     oracle worst, then the 99th, 99.9th and 99.99th percentiles of both)."""
     n_dev, w_dev = accuracy(got, truth, allow_extra, rtol, atol)
@@ -147,9 +153,11 @@ def assert_no_less_accurate(name, got, oracle32, truth, allow_extra=None, rtol=1
             f.write(f"{name}\t{np.size(truth)}\tdev {n_dev}\torc {n_orc}\t"
                     f"{w_dev:.4g}\t{w_orc:.4g}\tpct dev {' '.join(f'{v:.3g}' for v in pd)}"
                     f"\torc {' '.join(f'{v:.3g}' for v in po)}\n")
-    n_max = int(COUNT_SLACK_REL * n_orc + COUNT_SLACK_ABS)
-    p_max = max(0.1, P999_FACTOR * float(po[1]))
-    w_max = max(1.0, WORST_FACTOR * w_orc)
+    cr, ca, pf, wf = ((STRICT["count_rel"], STRICT["count_abs"], STRICT["p999"], STRICT["worst"])
+                      if strict else (COUNT_SLACK_REL, COUNT_SLACK_ABS, P999_FACTOR, WORST_FACTOR))
+    n_max = int(cr * n_orc + ca)
+    p_max = max(0.1, pf * float(po[1]))
+    w_max = max(1.0, wf * w_orc)
     assert n_dev <= n_max and float(pd[1]) <= p_max and w_dev <= w_max, (
         f"{name}: device {n_dev} elements outside rel {rtol} / abs {atol} of the binary64 "
         f"truth (99.9th percentile {float(pd[1]):.4g}, worst {w_dev:.4g} of the bound), "

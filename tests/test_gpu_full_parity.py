@@ -16,16 +16,16 @@ scenario (test/test_gs_voxelizer.py:15-26: 100,000 Gaussians on (100,150,80),
 Bar, per comparison: the device is no less accurate than the binary32 oracle
 (a restatement of the reference's binary32 arithmetic) against the binary64
 truth (the oracle's binary64 build on the same binary32 inputs and the same
-pair lists): at most 1.25 x + 2 as many elements outside rel 1e-4 / abs 1e-6
+pair lists), up to a stated slack: elements outside rel 1e-4 / abs 1e-6
 (north_star's bound) of the truth, plus its gate-ambiguous mass for the
-voxelize outputs, and a worst normalised error at most 2 x the oracle's or
-inside the bound (helpers.assert_no_less_accurate).  Where the binary32
-oracle itself is inside the bound everywhere, this is north_star's bound on
-the device, with at most two elements beyond it.  The volume is also held to
-rel 1e-4 / abs 1e-6 (+ ambiguity) against the binary32 oracle directly, and the
-leaf gradients to rel 1e-5 against the oracle's projection backward fed the
-device's own voxelize gradients.  Both statistics of every comparison go to
-GSV_MARGIN_LOG.
+voxelize outputs, at most 3 x + 10 the oracle's count, the 99.9th percentile
+of the normalised error at most 2 x the oracle's, and the worst at most 4 x
+(helpers.assert_no_less_accurate, which states why).  The backward's per-voxel
+form path (chained rows off) is also held to the strict tier, 1.25 x + 10,
+1.5 x and 2 x.  The volume is also held to rel 1e-4 / abs 1e-6 (+ ambiguity)
+against the binary32 oracle directly, and the leaf gradients to rel 1e-5
+against the oracle's projection backward fed the device's own voxelize
+gradients.  Every comparison's statistics go to GSV_MARGIN_LOG.
 """
 import numpy as np
 import pytest
@@ -143,6 +143,15 @@ def test_every_voxelize_gradient_element(scene, grad):
         got = _voxelize_grads(P, g, mode)
         for nm, a, b, t, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, rg, tg, tamb):
             acc.check(f"{cfg.name} {grad} {mode}: {nm}", a, b, t, m)
+    # the per-voxel form path (chained rows off), under the strict tier
+    import gs_voxelizer.cuda as _C
+    before = _C.set_backward_chains(False)
+    try:
+        got = _voxelize_grads(P, g, "pairs")
+    finally:
+        _C.set_backward_chains(before)
+    for nm, a, b, t, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, rg, tg, tamb):
+        acc.check(f"{cfg.name} {grad} form rows: {nm}", a, b, t, m, strict=True)
     acc.done()
 
 

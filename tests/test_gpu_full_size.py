@@ -148,17 +148,24 @@ def test_whole_volume_every_voxel(full):
 
 def test_every_gradient_element_whole_volume(full):
     """vol_grad N(0,1) over the whole volume; every element of the three
-    gradients, per-pair reduction with the binning's tiles."""
+    gradients, per-pair reduction with the binning's tiles; the per-voxel form
+    path (chained rows off) under the strict tier."""
     import gs_voxelizer.cuda as _C
     P = full
     work = P["work"]
     cfg = work.cfg
     C = work.intensities.shape[1]
     g = np.random.default_rng(23).standard_normal(cfg.vol + (C,)).astype(np.float32)
-    got = [np32(t) for t in _C.voxelize_backward_per_gaussian(
-        cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"], P["w"].intensities,
-        torch.from_numpy(g).to(P["pr"].device), P["tmin"], P["tmax"], P["cum"],
-        tiles_sorted=P["tiles"])]
+    def device(chains):
+        before = _C.set_backward_chains(chains)
+        try:
+            return [np32(t) for t in _C.voxelize_backward_per_gaussian(
+                cfg.vol, P["ids"], P["bins"], P["pr"], P["cn"], P["w"].intensities,
+                torch.from_numpy(g).to(P["pr"].device), P["tmin"], P["tmax"], P["cum"],
+                tiles_sorted=P["tiles"])]
+        finally:
+            _C.set_backward_chains(before)
+    got, form = device(True), device(False)
     args = (cfg.vol, np32(P["ids"]), np32(P["bins"]), P["rpr"], P["rcn"], work.intensities.numpy(),
             g)
     print(f"{cfg.name}: oracle backward (binary32)", flush=True)
@@ -176,6 +183,8 @@ def test_every_gradient_element_whole_volume(full):
         for acc, part in zip(truth + tamb, list(tg) + list(am)):
             acc += part
     checks = AccuracyChecks()
-    for nm, a, b, t, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, ref, truth, tamb):
+    for nm, a, f, b, t, m in zip(("dpos3d_radii", "dconics", "dintensities"), got, form, ref,
+                                 truth, tamb):
         checks.check(f"{cfg.name} whole-volume normal: {nm}", a, b, t, m)
+        checks.check(f"{cfg.name} whole-volume normal, form rows: {nm}", f, b, t, m, strict=True)
     checks.done()
