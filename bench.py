@@ -26,6 +26,12 @@ vector peak.  `ref_formulation_tflops` is the reference's flop count for the
 same evaluations (E x (65 + 4C), SURVEY's per-evaluation figure) over the same
 duration; this kernel evaluates a cheaper but equivalent formulation and skips
 culled pairs, so that figure can exceed the peak and is not a utilisation.
+The kernel is co-limited by VALU issue and by per-wave memory latency (a timing
+build without its row loop keeps most of its time), so `bound` names both:
+`frac` is the VALU side; `hbm_frac` is its HBM traffic (`traffic`, calibrated
+FETCH_SIZE + WRITE_SIZE from profiles/traffic_<workload>.json) over the same
+duration against the 8 TB/s peak, and `wait_inst_any_frac` / `l2_hit_rate`
+(profiles/mem_<workload>.json) show the wait.
 `cpu_baseline` times the C oracle (a binary32 C restatement of the reference,
 OpenMP over the host cores) on the same inputs.
 
@@ -251,9 +257,13 @@ def main():
     ref_fwd_tflops = evals * (22 + 2 * C) / (fwd_ms * 1e-3) / 1e12
     counters = _load_profile("valu", cfg.name)
     traffic = _load_profile("traffic", cfg.name)
-    roof = {"kernel": "k_vox_bwd + k_vox_bwd_rest (voxelize backward)", "bound": "valu",
+    # co-limited: VALU issue (frac, against the FP32 peak) and per-wave memory
+    # latency (the loop-free timing build keeps most of the time; the HBM rate
+    # of its traffic is hbm_frac of the peak)
+    roof = {"kernel": "k_vox_bwd + k_vox_bwd_rest (voxelize backward)",
+            "bound": "valu + memory latency",
             "achieved": None, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": None,
-            "traffic": None, "duration_ms": round(bwd_ms, 4)}
+            "traffic": None, "hbm_frac": None, "duration_ms": round(bwd_ms, 4)}
     if counters is not None and counters.get("evals") == evals:
         bw = counters["per_launch"]["voxelize_backward"]
         achieved = bw["fp32_flops"] / (bwd_ms * 1e-3) / 1e12
@@ -269,6 +279,16 @@ def main():
             roof["forward"]["frac"] = round(roof["forward"]["achieved"] / FP32_PEAK_TFLOPS, 4)
     if traffic is not None and traffic.get("evals") == evals:
         roof["traffic"] = traffic.get("voxelize_backward_hbm_bytes_per_launch")
+        if roof["traffic"]:
+            roof["hbm_achieved_GBps"] = round(roof["traffic"] / (bwd_ms * 1e-3) / 1e9, 1)
+            roof["hbm_frac"] = round(roof["hbm_achieved_GBps"] / HBM_PEAK_GBS, 4)
+    mem = _load_profile("mem", cfg.name)
+    if mem is not None and mem.get("pairs") == n_isect:
+        k = mem["per_kernel"].get(f"k_vox_bwd<{C}, 3>") or next(
+            (v for n, v in mem["per_kernel"].items() if n.startswith("k_vox_bwd<")), None)
+        if k is not None:
+            roof["wait_inst_any_frac"] = k["wait_inst_any_frac"]
+            roof["l2_hit_rate"] = k["tcc_hit_rate"]
     roof["ref_formulation_tflops"] = round(ref_bwd_tflops, 3)
     roof["ref_formulation_flops_per_eval"] = 65 + 4 * C
 
