@@ -842,6 +842,11 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, float mxl, fl
                 }
             }
             float W1 = 0.f, h[GSV_TILE];
+            // C > 1: the row's sums of a * g_c, added to the pair's totals once
+            // per row (64 additions of row sums, not 512 running ones)
+            float rI[C];
+#pragma unroll
+            for (int c = 0; c < C; ++c) rI[c] = 0.f;
 #pragma unroll
             for (int u = 0; u < GSV_TILE; ++u) {
                 float a;
@@ -861,12 +866,16 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, float mxl, fl
 #pragma unroll
                     for (int c = 0; c < C; ++c) {
                         Gs = fmaf(I[c], gv[u * C + c], Gs);
-                        M.dI[c] = fmaf(a, gv[u * C + c], M.dI[c]);
+                        rI[c] = fmaf(a, gv[u * C + c], rI[c]);
                     }
                     h[u] = a * Gs;
                 }
                 W1 = fmaf(h[u], dxu[u], W1);
                 col[u] = add_nc(col[u], h[u]);
+            }
+            if (C > 1) {
+#pragma unroll
+                for (int c = 0; c < C; ++c) M.dI[c] = add_nc(M.dI[c], rI[c]);
             }
             // the row sum of the h already formed: 7 two-operand adds, which
             // issue faster than the 8 three-operand FMAs a contracted a*g sum takes
