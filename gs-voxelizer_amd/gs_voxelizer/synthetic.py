@@ -235,6 +235,40 @@ def reference_value_scenario(seed: int = 0, n: Optional[int] = None):
     return work, vol
 
 
+# The reference's multi-channel test (test/test_multi_channel.py:15-26): the
+# same (100, 150, 80) volume in a (1.0, 1.5, 0.8) world (z, y, x) centred at
+# (0.5, 0.7, 0.5), 5,000 Gaussians from random_gauss_init(anisotropicScale=True)
+# without rotation, and two channels, the phantom's value and half of it.
+REFERENCE_MULTICHANNEL = Config("ref_multichannel_test_100x150x80_5k_c2", (100, 150, 80), 5_000,
+                                2, ("fixed", 0.03, 0.01, 0.02), "identity", (0.1, 1.0),
+                                "uniform", "spheres", world=(1.0, 1.5, 0.8),
+                                center=(0.5, 0.7, 0.5))
+
+
+def reference_multichannel_scenario(seed: int = 0):
+    """(Workload, phantom (D, H, W)) of the reference's multi-channel test, seeded.
+
+    Positions U[0,1)^3 (world units, x y z); scales (0.02 * 1.5, 0.02 * 0.5,
+    0.02) world units; identity rotations; channel 0 = the phantom's value at
+    the voxel floor(pos * (size - 1)) per axis (random_gauss_init, not divided
+    by 10 here), channel 1 = half of it (test_multi_channel.py:25)."""
+    cfg = REFERENCE_MULTICHANNEL
+    n = cfg.n
+    D, H, W = cfg.vol
+    vol = sphere_phantom(cfg.vol, np.random.default_rng(seed))
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    pos = torch.rand((n, 3), generator=g, dtype=torch.float32)
+    scale = torch.tensor([0.03, 0.01, 0.02], dtype=torch.float32).expand(n, 3).contiguous()
+    quat = torch.zeros((n, 4), dtype=torch.float32)
+    quat[:, 0] = 1.0
+    size_xyz = torch.tensor([W, H, D], dtype=torch.float32)
+    idx = torch.clamp((pos * (size_xyz - 1)).long(), min=0)
+    one = vol[idx[:, 2], idx[:, 1], idx[:, 0]].unsqueeze(-1)
+    inten = torch.cat([one, one / 2], dim=1).contiguous()
+    work = Workload(cfg, pos.contiguous(), scale, quat, inten, {"kind": "spheres"}, seed)
+    return work, vol
+
+
 def volume_scaling_scenario(edge: int, seed: int = 0, base_edge: int = 96,
                             base_gaussians: int = 6000) -> Workload:
     """The reference's volume-scaling case (test/test_volume_scaling.py:53-64,

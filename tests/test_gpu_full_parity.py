@@ -3,7 +3,9 @@
 BASELINE configuration 3 (256^3, 200,000 Gaussians, the headline) and
 configuration 2 (128^3, all 50,000 Gaussians), plus the reference's own value
 scenario (test/test_gs_voxelizer.py:15-26: 100,000 Gaussians on (100,150,80),
-~495 pairs per tile), each checked on:
+~495 pairs per tile) and its multi-channel scenario (test/test_multi_channel.py:
+15-26: 5,000 Gaussians in a (1.0, 1.5, 0.8) world, channels I and I / 2, where
+the reference asserts only finite leaf gradients), each checked on:
 
 - the whole volume, every voxel;
 - every element of dpos3d_radii, dconics and dintensities from the dominant
@@ -45,12 +47,15 @@ def _scene(key):
     if key == "reference_scenario":
         work, target = S.reference_value_scenario(seed=0)
         return work, target
+    if key == "reference_multichannel":
+        return S.reference_multichannel_scenario(seed=0)
     work = S.make_gaussians(S.CONFIGS[key], seed=0)
     return work, S.phantom(work)
 
 
-@pytest.fixture(scope="module", params=[3, 2, "reference_scenario"],
-                ids=["cfg3_256cube_200k", "cfg2_128cube_50k", "reference_value_scenario"])
+@pytest.fixture(scope="module", params=[3, 2, "reference_scenario", "reference_multichannel"],
+                ids=["cfg3_256cube_200k", "cfg2_128cube_50k", "reference_value_scenario",
+                     "reference_multichannel_scenario"])
 def scene(request, device):
     """GPU projection, binning and forward of the whole scene, and the oracle's."""
     import gs_voxelizer.cuda as _C
