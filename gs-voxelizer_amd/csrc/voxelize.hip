@@ -672,17 +672,26 @@ struct Moments {
 struct RowForm {
     float al, be, ga, be2, ga2, ga3;  // coefficients of p'
     float tc, ec, zc;                 // tau, eta, zeta at the tile centre
-    float r_ell;                      // w^T Q^-1 w, w = 2k (0, b, c): the slope's spread over the gate
 };
 
-// The LDL^T factor of a conic (binary64) and the row form of the pair whose
-// Gaussian lies at (mx, my, mz) from the tile centre.  False (the pair then
-// takes the exact path) unless the binary64 pivots are positive and each
+// The part of the row form that depends on the conic alone: the LDL^T factor
+// (binary64 unit-triangle entries, binary32 square roots of the k-scaled
+// pivots) and the binary32 coefficients of p'.
+struct RowFactor {
+    double l21, l31, l32;
+    float al, b2, g3;   // sqrt(k D1), sqrt(k D2), sqrt(k D3)
+    float be, ga, ga2;  // al l21, al l31, b2 l32
+    float r_ell;        // w^T Q^-1 w, w = 2k (0, b, c): the slope's spread over the gate
+};
+
+// The LDL^T factor of a conic (binary64).  False (the Gaussian's pairs then
+// take the exact path) unless the binary64 pivots are positive and each
 // k * pivot lies in [2^-100, 2^100], where its binary32 square root is a
 // normal number.  Zero coefficients otherwise.
-__device__ __forceinline__ bool row_form(float ca, float cb, float cc, float cd, float ce,
-                                         float cf, float mx, float my, float mz, RowForm &f) {
-    f.al = f.be = f.ga = f.be2 = f.ga2 = f.ga3 = f.tc = f.ec = f.zc = f.r_ell = 0.f;
+__device__ __forceinline__ bool row_factor(float ca, float cb, float cc, float cd, float ce,
+                                           float cf, RowFactor &F) {
+    F.l21 = F.l31 = F.l32 = 0.0;
+    F.al = F.b2 = F.g3 = F.be = F.ga = F.ga2 = F.r_ell = 0.f;
     constexpr double k = 0.72134752044448170368;  // log2(e) / 2
     const double a = ca, b = cb, c = cc, d = cd, e = ce, ff = cf;
     const double ia = 1.0 / a;
@@ -695,20 +704,35 @@ __device__ __forceinline__ bool row_form(float ca, float cb, float cc, float cd,
     if (!(p1 >= lo && p1 <= hi && p2 >= lo && p2 <= hi && p3 >= lo && p3 <= hi)) return false;
     const float al = __builtin_amdgcn_sqrtf((float)p1);
     const float b2 = __builtin_amdgcn_sqrtf((float)p2);
-    const float g3 = __builtin_amdgcn_sqrtf((float)p3);
-    f.al = al;
-    f.be = (float)(al * l21);
-    f.ga = (float)(al * l31);
-    f.be2 = b2;
-    f.ga2 = (float)(b2 * l32);
-    f.ga3 = g3;
-    f.tc = (float)(al * fma(l31, (double)mz, fma(l21, (double)my, (double)mx)));
-    f.ec = (float)(b2 * fma(l32, (double)mz, (double)my));
-    f.zc = g3 * mz;
+    F.l21 = l21; F.l31 = l31; F.l32 = l32;
+    F.al = al;
+    F.b2 = b2;
+    F.g3 = __builtin_amdgcn_sqrtf((float)p3);
+    F.be = (float)(al * l21);
+    F.ga = (float)(al * l31);
+    F.ga2 = (float)(b2 * l32);
     // y = L^-1 w, w = 2k (0, b, c): w^T Q^-1 w = y2^2 / D2 + y3^2 / D3
     const double y2 = 2.0 * k * b, y3 = fma(-l32, y2, 2.0 * k * c);
-    f.r_ell = (float)(y2 * y2 / d2 + y3 * y3 / d3);
+    F.r_ell = (float)(y2 * y2 / d2 + y3 * y3 / d3);
     return true;
+}
+
+// The row form of the pair whose Gaussian lies at (mx, my, mz) from the tile
+// centre, from its factor's binary32 square roots al, b2, g3 and the binary64
+// products be = al l21, ga = al l31, ga2 = b2 l32: the tile-centre terms in
+// binary64 (al mx and b2 my are exact there), the coefficients their binary32
+// roundings.
+__device__ __forceinline__ void row_centre(float al, float b2, float g3, double be, double ga,
+                                           double ga2, float mx, float my, float mz, RowForm &f) {
+    f.al = al;
+    f.be = (float)be;
+    f.ga = (float)ga;
+    f.be2 = b2;
+    f.ga2 = (float)ga2;
+    f.ga3 = g3;
+    f.tc = (float)fma(ga, (double)mz, fma(be, (double)my, (double)al * (double)mx));
+    f.ec = (float)fma(ga2, (double)mz, (double)b2 * (double)my);
+    f.zc = g3 * mz;
 }
 
 // Adds to M the moments of h = a * G about the Gaussian's centre for one lane's pair:
@@ -753,7 +777,8 @@ template <int C, int kMode>
 __device__ __forceinline__ void pair_moments(const float4 *s_rows, float mxl, float myl, float mzl,
                                              const RowForm &f, float A2, float Bn, float Cn,
                                              float Dn, float En, float Fn, float shift, float bound,
-                                             float K, const float (&I)[C], Moments<C> &M) {
+                                             float K, const float (&Gt)[GSV_TILE],
+                                             const float (&I)[C], Moments<C> &M) {
     constexpr bool kForm = kMode != kRowsExact, kChain = kMode == kRowsChain;
     // Sxx is only needed whole: the loop sums h per voxel column (col[u], a
     // two-operand add per voxel) and Sxx = sum_u dx_u^2 col[u] is formed once at
@@ -768,26 +793,12 @@ __device__ __forceinline__ void pair_moments(const float4 *s_rows, float mxl, fl
     // kRowsForm: 2^off, a normal number on live lanes (off in [-126, -66]) and 0
     // at the dead offset, where the form is 0 (zero coefficients) and a = 1 * 0
     const float Fb = kMode == kRowsForm ? __builtin_amdgcn_exp2f(bound) : 0.f;
-    // kRowsChain: G_u = 2^(-x_u^2 - K) at the positions the chain implies,
-    // x_u = x_a + (u - a) al from its anchor a (0 or 4; x_0 and x_4 as the
-    // anchors' exponents take them, x_4 = al/2 exactly) and the step's exact
-    // multiples of al: x_u^2 in binary64, its binary32 rounding residual applied
-    // as the factor 1 + lo ln 2, so each G_u is within ~1e-7 of its value;
-    // 2^-K is applied exactly.  (G_u from the separately rounded al p'_u
-    // instead differs from the chain's exponents by 2 u_r (x_u - x_a - (u - a)
-    // al), the same in every row and tile of the Gaussian, which does not
-    // average out of its sums: at cfg5 1.3x as many dpos and dintensities
-    // elements outside rel 1e-4 / abs 1e-6 for an N(0,1) vol_grad.)
+    // kRowsChain: G_u = 2^(-x_u^2 - K), Gt[u] = 2^(-x_u^2) being the
+    // Gaussian's column factor (column_factors); 2^-K is applied exactly.
     float G[GSV_TILE];
     if (kChain) {
 #pragma unroll
-        for (int u = 0; u < GSV_TILE; ++u) {
-            const double xe = (double)xu[u < 4 ? 0 : 4] + (double)f.al * (u < 4 ? u : u - 4);
-            const double d = -xe * xe;
-            const float hi = (float)d;
-            const float lo = (float)(d - (double)hi);
-            G[u] = ldexpf(__builtin_amdgcn_exp2f(hi) * fmaf(lo, kLn2, 1.0f), -(int)K);
-        }
+        for (int u = 0; u < GSV_TILE; ++u) G[u] = ldexpf(Gt[u], -(int)K);
     }
     // the per-plane constant: the chain's offset and K (its E), the exact
     // path's shift
@@ -960,6 +971,8 @@ struct BwdArgs {
     float l1_numel;
     float *dpos, *dconic, *dint;
     const int *tile_min, *tile_max, *cum;
+    // The per-Gaussian records k_bwd_prep wrote (kBwdRecF4 float4 per Gaussian)
+    const float4 *rec;
     float *partial;
     const int64_t *d_count;  // live pair count on the device (n_isect is then the capacity)
     // Optional work list: order[0 .. *d_work) holds the sorted positions of the
@@ -1000,13 +1013,175 @@ template <int C>
 struct BwdLane {
     int tile, slot, g, p;
     bool valid, live, fast;
-    float mxl, myl, mzl, ca, cb, cc, cd, ce, cf;
+    float mxl, myl, mzl;
     float I[C];
-    Gate gt;
+    float off, fscale;  // the gate-free path's offset and its 2^-off
     TileGeom tg;
     RowForm rf;  // gate-free pairs: the row form about the tile centre
     float kch;   // gate-free pairs: chain_shift's K, or -1
+    int slot_e;  // deterministic mode: the pair's emission slot (< 2^31), or -1
+    const float4 *rp;  // the Gaussian's record (valid lanes with a Gaussian in range)
 };
+
+// ---------------------------------------------- per-Gaussian backward record --
+//
+// Everything a backward pair reads of its Gaussian, and the parts of its
+// set-up that do not depend on the tile, in one 128-byte record (one cache
+// line) per Gaussian: the centre, the gate, the LDL^T factor of the conic,
+// the tile-independent terms of the chain's shift bound, the column factors
+// 2^(-x_u^2), the first channel's intensity and the emission box.
+// k_bwd_prep forms them once per Gaussian (one lane each) instead of once per
+// (tile, Gaussian) pair (~16 pairs per Gaussian at 256^3 / 200k: the factor's
+// four binary64 divisions, the gate's log2, the column factors' exp2), and a
+// pair reads one line where its position, conic, intensity, box and cum
+// gathers touched six to nine.  The conic itself is not needed: the
+// deterministic mode applies it per Gaussian in k_pair_reduce.  float4 fields:
+//   0  px, py, pz, flags          1  off, s_ell, m_reach, al
+//   2  b2, g3, I0, t2             3  al l21, al l31 (binary64)
+//   4  b2 l32 (binary64), ebase   5  extent x, extent y, cum[g-1], cum[g]
+//   6  Gt[0..3]                   7  Gt[4..7]
+// ebase (int64) = cum[g-1] - (min.z * ny + min.y) * nx - min.x, so that a
+// pair's emission slot is ebase + (tz * ny + ty) * nx + tx; the ints of
+// field 5 are nx, ny and the Gaussian's slot range.  The chain terms (see
+// chain_shift): m_reach = 2 al^2 (3.5 + sqrt(k2 / a)), s_ell = sqrt(k2 r_ell),
+// k2 = -2 ln2 t2; the pair forms k_max = floor(120 - 12.25 al^2), rint(-off)
+// and 2^-off itself.  Bits of flags: kRecLive (the gate can pass),
+// kRecBounded (a finite positive mean), kRecFast (gate-free with a valid row
+// factor).  The factor, chain and column fields are zero unless kRecFast; the
+// box fields are zero in the atomic mode, which has none.
+constexpr int kBwdRecF4 = 8;
+constexpr unsigned kRecLive = 1u, kRecFast = 2u, kRecBounded = 4u;
+constexpr int kPrepThreads = 256;
+constexpr int kPrepStride = kBwdRecF4 + 1;  // LDS float4 per staged record: +1 spreads the banks
+
+// Column factors of the chained rows: Gt[u] = 2^(-x_u^2) at the positions the
+// chain implies, x_u = x_a + (u - a) al from its anchor a (0 or 4; x_0 and x_4
+// as the anchors' exponents take them: fl(al * -3.5) and al / 2 exactly) and
+// the step's exact multiples of al: x_u^2 in binary64, its binary32 rounding
+// residual applied as the factor 1 + lo ln 2, so each factor is within ~1e-7
+// of its value.  (Factors from the separately rounded al p'_u instead differ
+// from the chain's exponents by 2 u_r (x_u - x_a - (u - a) al), the same in
+// every row and tile of the Gaussian, which does not average out of its sums:
+// at cfg5 1.3x as many dpos and dintensities elements outside rel 1e-4 /
+// abs 1e-6 for an N(0,1) vol_grad.)
+__device__ __forceinline__ void column_factors(float al, float (&Gt)[GSV_TILE]) {
+    const float x0 = al * (0.0f - 3.5f), x4 = al * (4.0f - 3.5f);
+#pragma unroll
+    for (int u = 0; u < GSV_TILE; ++u) {
+        const double xe = (double)(u < 4 ? x0 : x4) + (double)al * (u < 4 ? u : u - 4);
+        const double d = -xe * xe;
+        const float hi = (float)d;
+        const float lo = (float)(d - (double)hi);
+        Gt[u] = __builtin_amdgcn_exp2f(hi) * fmaf(lo, kLn2, 1.0f);
+    }
+}
+
+// The record pass's inputs and output.  tile_min, tile_max and cum are NULL
+// in the atomic mode.
+struct PrepArgs {
+    int n;
+    const float4 *pos_radii;
+    const float2 *conics;
+    const float *intens;
+    const int *tile_min, *tile_max, *cum;
+    float4 *rec;
+};
+
+// Block `blk` of the record pass: one lane per Gaussian, its record (layout
+// above) staged in LDS (s_rec: kPrepThreads * kPrepStride float4) so that the
+// block writes its 256 records as one coalesced run (scattered 16-byte stores
+// at the record stride take twice as long).
+template <int C>
+__device__ __forceinline__ void bwd_prep_block(int blk, const PrepArgs &P, float4 *s_rec) {
+    const int n = P.n;
+    const float4 *__restrict__ pos_radii = P.pos_radii;
+    const float2 *__restrict__ conics = P.conics;
+    const float *__restrict__ intens = P.intens;
+    const int *__restrict__ tile_min = P.tile_min, *__restrict__ tile_max = P.tile_max;
+    const int *__restrict__ cum = P.cum;
+    float4 *__restrict__ rec = P.rec;
+    const int t = (int)threadIdx.x, g0 = blk * kPrepThreads, g = g0 + t;
+    if (g < n) {
+        const float4 pr = pos_radii[g];
+        const float2 c01 = conics[3 * g], c23 = conics[3 * g + 1], c45 = conics[3 * g + 2];
+        float I0 = 0.f, mean = 0.f, max_abs = 0.f;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const float v = intens[(size_t)g * C + c];
+            if (c == 0) I0 = v;
+            mean += v;
+            max_abs = fmaxf(max_abs, fabsf(v));
+        }
+        mean /= (float)C;
+        const Gate gt = make_gate(mean);
+        unsigned flags = (gt.live ? kRecLive : 0u) | (gt.bounded ? kRecBounded : 0u);
+        RowFactor F{};
+        bool fast = gt.live && gate_free_ok(gt, max_abs, pr.x, pr.y, pr.z, c01.x, c01.y, c23.x,
+                                            c23.y, c45.x, c45.y);
+        if (fast) fast = row_factor(c01.x, c01.y, c23.x, c23.y, c45.x, c45.y, F);
+        float s_ell = 0.f, m_reach = 0.f;
+        double be_d = 0.0, ga_d = 0.0, ga2_d = 0.0;
+        float Gt[GSV_TILE];
+#pragma unroll
+        for (int u = 0; u < GSV_TILE; ++u) Gt[u] = 0.f;
+        if (fast) {
+            flags |= kRecFast;
+            const float a2 = F.al * F.al;
+            const float k2 = -2.0f * kLn2 * gt.t2;
+            m_reach = 2.0f * a2 *
+                      (3.5f + __builtin_amdgcn_sqrtf(fmaxf(k2 * __builtin_amdgcn_rcpf(c01.x), 0.f)));
+            s_ell = __builtin_amdgcn_sqrtf(fmaxf(k2 * F.r_ell, 0.f));
+            be_d = F.al * F.l21;
+            ga_d = F.al * F.l31;
+            ga2_d = F.b2 * F.l32;
+            column_factors(F.al, Gt);
+        }
+        int nx = 0, ny = 0, base = 0, end = 0;
+        int64_t ebase = 0;
+        if (cum != nullptr) {
+            const int mnx = tile_min[3 * g], mny = tile_min[3 * g + 1], mnz = tile_min[3 * g + 2];
+            nx = tile_max[3 * g] - mnx;
+            ny = tile_max[3 * g + 1] - mny;
+            base = g == 0 ? 0 : cum[g - 1];
+            end = cum[g];
+            ebase = (int64_t)base - ((int64_t)mnz * ny + mny) * nx - mnx;
+        }
+        const auto bits = [](int v) { return __int_as_float(v); };
+        const auto dlo = [](double v) {
+            return __int_as_float((int)(uint32_t)__double_as_longlong(v));
+        };
+        const auto dhi = [](double v) {
+            return __int_as_float((int)(uint32_t)((uint64_t)__double_as_longlong(v) >> 32));
+        };
+        const double eb = __longlong_as_double((long long)ebase);  // the int64's bits
+        float4 *r = s_rec + t * kPrepStride;
+        r[0] = make_float4(pr.x, pr.y, pr.z, bits((int)flags));
+        r[1] = make_float4(gt.off, s_ell, m_reach, F.al);
+        r[2] = make_float4(F.b2, F.g3, I0, gt.t2);
+        r[3] = make_float4(dlo(be_d), dhi(be_d), dlo(ga_d), dhi(ga_d));
+        r[4] = make_float4(dlo(ga2_d), dhi(ga2_d), dlo(eb), dhi(eb));
+        r[5] = make_float4(bits(nx), bits(ny), bits(base), bits(end));
+        r[6] = make_float4(Gt[0], Gt[1], Gt[2], Gt[3]);
+        r[7] = make_float4(Gt[4], Gt[5], Gt[6], Gt[7]);
+    }
+    __syncthreads();
+    const int cnt = min(kPrepThreads, n - g0) * kBwdRecF4;  // g0 < n: the grid covers n exactly
+    float4 *dst = rec + (size_t)g0 * kBwdRecF4;
+    for (int i = t; i < cnt; i += kPrepThreads)
+        dst[i] = s_rec[(i / kBwdRecF4) * kPrepStride + (i % kBwdRecF4)];
+}
+
+// The record pass alone (the backward without a work list).
+template <int C>
+__global__ __launch_bounds__(kPrepThreads) void k_bwd_prep(PrepArgs P) {
+    __shared__ float4 s_rec[kPrepThreads * kPrepStride];
+    bwd_prep_block<C>((int)blockIdx.x, P, s_rec);
+}
+
+__device__ __forceinline__ double rec_double(float lo, float hi) {
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)__float_as_int(hi) << 32) |
+                                            (uint64_t)(uint32_t)__float_as_int(lo)));
+}
 
 // Emission slot of the pair (tile, g): e = cum[g-1] + ((tz-min.z)*ny +
 // (ty-min.y))*nx + (tx-min.x), the order the pairs were duplicated in
@@ -1066,18 +1241,31 @@ __device__ __forceinline__ unsigned keep_mask(const uint8_t *flags, int64_t i0, 
     return m;
 }
 
+// Blocks [0, nprep): the record pass (bwd_prep_block); blocks nprep + b: the
+// kept count of flags [4096 b, 4096 (b + 1)) into part[b].  The two are
+// independent, so one launch runs them side by side: the counts take ~5 us
+// as a launch of their own, and run under the record pass here.
+template <int C>
 __global__ __launch_bounds__(kKeepThreads) void k_keep_count(const uint8_t *__restrict__ flags,
                                                              int cap,
                                                              const int64_t *__restrict__ d_count,
-                                                             int32_t *__restrict__ part) {
+                                                             int32_t *__restrict__ part,
+                                                             int nprep, PrepArgs P) {
+    static_assert(kKeepThreads == kPrepThreads, "one block size for both");
+    __shared__ float4 s_rec[kPrepThreads * kPrepStride];
     __shared__ int lds_waves[kKeepThreads / kWave];
+    if ((int)blockIdx.x < nprep) {  // uniform per block
+        bwd_prep_block<C>((int)blockIdx.x, P, s_rec);
+        return;
+    }
+    const int blk = (int)blockIdx.x - nprep;
     const int np = live_pairs(cap, d_count);
-    const int64_t i0 = (int64_t)blockIdx.x * kKeepTile + (int64_t)threadIdx.x * kKeepItems;
+    const int64_t i0 = (int64_t)blk * kKeepTile + (int64_t)threadIdx.x * kKeepItems;
     int valid;
     const int c = __popc(keep_mask(flags, i0, np, &valid));
     int total;
     (void)scan_detail::block_exclusive(c, lds_waves, &total);
-    if (threadIdx.x == 0) part[blockIdx.x] = total;
+    if (threadIdx.x == 0) part[blk] = total;
 }
 
 // direct: part holds raw block counts (nb <= 2048); otherwise part holds their
@@ -1193,73 +1381,100 @@ __device__ __forceinline__ bool bwd_slots(const BwdArgs &a, int64_t p0, BwdLane<
 // Gaussian's centre instead, x_u - al mx, step only by the form's coupling
 // but carry |x_u - al mx|^2 into E; measured at cfg3 they left ~1.9x as many
 // dconics elements outside rel 1e-4 / abs 1e-6 for an N(0,1) vol_grad.)
-// Binary32 margins: 1e-3 relative and 0.01 on M.
-template <int C>
-__device__ __forceinline__ float chain_shift(const BwdLane<C> &L) {
-    const RowForm &f = L.rf;
+// Binary32 margins: 1e-3 relative and 0.01 on M.  The terms that depend on
+// the Gaussian alone come from its record: k_max = floor(120 - 12.25 al^2),
+// m_reach, s_ell = sqrt(k2 r_ell) and rint(-off).
+__device__ __forceinline__ float chain_shift(const RowForm &f, float mxl, float k_max,
+                                             float m_reach, float s_ell, float kch0) {
     const float a2 = f.al * f.al;
     const float m_tile = 2.0f * f.al * (fabsf(f.tc) + 3.5f * (fabsf(f.be) + fabsf(f.ga)));
     if (!(m_tile < 120.0f)) return -1.0f;
-    const float k_max = floorf(120.0f - 12.25f * a2);
-    const float k2 = -2.0f * kLn2 * L.gt.t2;
-    const float m_reach =
-        2.0f * a2 * (3.5f + __builtin_amdgcn_sqrtf(fmaxf(k2 * __builtin_amdgcn_rcpf(L.ca), 0.f)));
-    const float m_ell =
-        2.0f * a2 * fabsf(L.mxl) + __builtin_amdgcn_sqrtf(fmaxf(k2 * f.r_ell, 0.f));
+    const float m_ell = 2.0f * a2 * fabsf(mxl) + s_ell;
     const float M = fminf(m_tile, fminf(m_ell, m_reach)) * 1.001f + 0.01f;
     const float k_min = ceilf(3.0f * M) + 2.0f;
     if (!(k_min <= k_max)) return -1.0f;
-    return fminf(k_max, fmaxf(k_min, rintf(-L.gt.off)));
+    return fminf(k_max, fmaxf(k_min, kch0));
 }
 
-// The lane's Gaussian, its gate and its offsets from the tile centre.
+// The lane's Gaussian (its record), its gate, its offsets from the tile centre
+// and, in the deterministic mode, its emission slot.
 template <int C>
 __device__ __forceinline__ void bwd_gaussian(const BwdArgs &a, BwdLane<C> &L) {
     L.live = L.fast = false;
     L.g = 0;
     L.mxl = L.myl = L.mzl = 0.f;
-    L.ca = L.cb = L.cc = L.cd = L.ce = L.cf = 0.f;
 #pragma unroll
     for (int c = 0; c < C; ++c) L.I[c] = 0.f;
-    L.gt = make_gate(0.f);
+    L.off = kDeadOffset;
+    L.fscale = 0.f;
     L.rf = RowForm{};
     L.kch = -1.0f;
+    L.slot_e = -1;
+    L.rp = nullptr;
     L.tg = tile_geom(L.valid ? L.tile : 0, a.fx, a.Tx, a.fy, a.Ty, a.D, a.H, a.W);
     if (!L.valid) return;
     const int g = a.ids[L.p];
     L.g = g;
     if ((unsigned)g >= (unsigned)a.n) return;
-    const float4 pr = a.pos_radii[g];
-    const float2 c01 = a.conics[3 * g], c23 = a.conics[3 * g + 1], c45 = a.conics[3 * g + 2];
-    L.ca = c01.x; L.cb = c01.y; L.cc = c23.x; L.cd = c23.y; L.ce = c45.x; L.cf = c45.y;
-    float mean = 0.f, max_abs = 0.f;
+    const float4 *rp = a.rec + (size_t)g * kBwdRecF4;
+    L.rp = rp;
+    const float4 r0 = rp[0], r1 = rp[1], r2 = rp[2];
+    L.I[0] = r2.z;
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-        L.I[c] = a.intens[(size_t)g * C + c];
-        mean += L.I[c];
-        max_abs = fmaxf(max_abs, fabsf(L.I[c]));
-    }
-    mean /= (float)C;
-    L.gt = make_gate(mean);
-    L.live = L.gt.live;
+    for (int c = 1; c < C; ++c) L.I[c] = a.intens[(size_t)g * C + c];
     const TileGeom &tg = L.tg;
+    if (a.partial != nullptr) {
+        // e = cum[g-1] + ((tz-min.z)*ny + (ty-min.y))*nx + (tx-min.x), the order
+        // the pairs were duplicated in; -1 outside [cum[g-1], cum[g]) or past
+        // the pair count (as emission_slot_at)
+        const float4 r4 = rp[4], r5 = rp[5];
+        const int tx = tg.x0 / GSV_TILE, ty = tg.y0 / GSV_TILE, tz = tg.z0 / GSV_TILE;
+        const int nx = __float_as_int(r5.x), ny = __float_as_int(r5.y);
+        const int64_t base = __float_as_int(r5.z), end = __float_as_int(r5.w);
+        const int64_t e = (int64_t)__double_as_longlong(rec_double(r4.z, r4.w)) +
+                          ((int64_t)tz * ny + ty) * nx + tx;
+        L.slot_e = (e >= base && e < end && e < (int64_t)a.n_isect) ? (int)e : -1;
+    }
+    const unsigned flags = (unsigned)__float_as_int(r0.w);
+    L.off = r1.x;
+    L.live = (flags & kRecLive) != 0;
     // A work list holds only pairs the forward's identical test kept, so the
     // test is not repeated for them (a pair it would cull has no passing
     // voxel and yields zero moments either way).
-    if (L.live && L.gt.bounded && a.order == nullptr)
-        L.live = may_touch(pr.x, pr.y, pr.z, L.ca, L.cb, L.cc, L.cd, L.ce, L.cf, L.gt.t2, tg.xlo,
-                           tg.xhi, tg.ylo, tg.yhi, tg.zlo, tg.zhi);
+    if (L.live && (flags & kRecBounded) && a.order == nullptr) {
+        const float2 c01 = a.conics[3 * g], c23 = a.conics[3 * g + 1], c45 = a.conics[3 * g + 2];
+        L.live = may_touch(r0.x, r0.y, r0.z, c01.x, c01.y, c23.x, c23.y, c45.x, c45.y, r2.w,
+                           tg.xlo, tg.xhi, tg.ylo, tg.yhi, tg.zlo, tg.zhi);
+    }
     if (L.live) {
-        L.fast = gate_free_ok(L.gt, max_abs, pr.x, pr.y, pr.z, L.ca, L.cb, L.cc, L.cd, L.ce, L.cf);
+        L.fast = (flags & kRecFast) != 0;
         // delta = mu - p = (mu - tile centre) - p', p' = local index - 3.5
-        L.mxl = pr.x - (float)tg.x0 - 4.0f;
-        L.myl = pr.y - (float)tg.y0 - 4.0f;
-        L.mzl = pr.z - (float)tg.z0 - 4.0f;
+        L.mxl = r0.x - (float)tg.x0 - 4.0f;
+        L.myl = r0.y - (float)tg.y0 - 4.0f;
+        L.mzl = r0.z - (float)tg.z0 - 4.0f;
         if (L.fast) {
-            L.fast = row_form(L.ca, L.cb, L.cc, L.cd, L.ce, L.cf, L.mxl, L.myl, L.mzl, L.rf);
-            if (L.fast) L.kch = chain_shift(L);
+            // 2^-off of the rounded offset, as make_gate forms it
+            L.fscale = __builtin_amdgcn_exp2f(-L.off);
+            const float4 r3 = rp[3], r4 = rp[4];
+            const float al = r1.w;
+            row_centre(al, r2.x, r2.y, rec_double(r3.x, r3.y), rec_double(r3.z, r3.w),
+                       rec_double(r4.x, r4.y), L.mxl, L.myl, L.mzl, L.rf);
+            const float k_max = floorf(120.0f - 12.25f * (al * al));
+            L.kch = chain_shift(L.rf, L.mxl, k_max, r1.z, r1.y, rintf(-L.off));
         }
     }
+}
+
+// The gate of the lane's Gaussian from its intensities (the exact path's
+// shift, half-width and scale), as make_gate takes it; make_gate(0) for a lane
+// without a Gaussian.
+template <int C>
+__device__ __forceinline__ Gate lane_gate(const BwdLane<C> &L) {
+    float mean = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) mean += L.I[c];
+    mean /= (float)C;
+    return make_gate(mean);
 }
 
 // Exponent e such that m * 2^e lies in [2^(kGradScaleExp-1), 2^kGradScaleExp);
@@ -1418,21 +1633,38 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
         if (wave_fast) {
             // lanes outside the group: a zero form (zero coefficients) at the dead offset
             const RowForm rf = in_grp ? L.rf : RowForm{};
-            const float off = in_grp ? L.gt.off : kDeadOffset;
+            const float off = in_grp ? L.off : kDeadOffset;
             const float kshift = in_grp ? L.kch : 2.0f;
-            if (a.chain && __all(kshift >= 0.f))
+            float Gt[GSV_TILE];
+#pragma unroll
+            for (int u = 0; u < GSV_TILE; ++u) Gt[u] = 1.0f;
+            if (a.chain && __all(kshift >= 0.f)) {
+                if (in_grp) {  // the Gaussian's column factors (read here, not held across the staging)
+                    const float4 r6 = L.rp[6], r7 = L.rp[7];
+                    Gt[0] = r6.x; Gt[1] = r6.y; Gt[2] = r6.z; Gt[3] = r6.w;
+                    Gt[4] = r7.x; Gt[5] = r7.y; Gt[6] = r7.z; Gt[7] = r7.w;
+                }
                 pair_moments<C, kRowsChain>(s_g + my * kSlot, gx, gy, gz, rf, 0.f, 0.f, 0.f, 0.f, 0.f,
-                                            0.f, 0.f, off, kshift, L.I, M);
-            else
+                                            0.f, 0.f, off, kshift, Gt, L.I, M);
+            } else {
                 pair_moments<C, kRowsForm>(s_g + my * kSlot, gx, gy, gz, rf, 0.f, 0.f, 0.f, 0.f, 0.f,
-                                           0.f, 0.f, off, 0.f, L.I, M);
+                                           0.f, 0.f, off, 0.f, Gt, L.I, M);
+            }
         } else {
             // lanes outside the group: a zero form, never inside the gate (|s| <= -1)
-            const float A2 = in_grp ? -0.5f * kLog2e * L.ca : 0.f, Bn = in_grp ? -kLog2e * L.cb : 0.f;
-            const float Cn = in_grp ? -kLog2e * L.cc : 0.f, Dn = in_grp ? -0.5f * kLog2e * L.cd : 0.f;
-            const float En = in_grp ? -kLog2e * L.ce : 0.f, Fn = in_grp ? -0.5f * kLog2e * L.cf : 0.f;
+            float2 c01 = make_float2(0.f, 0.f), c23 = c01, c45 = c01;
+            if (in_grp) {
+                c01 = a.conics[3 * L.g];
+                c23 = a.conics[3 * L.g + 1];
+                c45 = a.conics[3 * L.g + 2];
+            }
+            const Gate gt = lane_gate(L);
+            const float A2 = in_grp ? -0.5f * kLog2e * c01.x : 0.f, Bn = in_grp ? -kLog2e * c01.y : 0.f;
+            const float Cn = in_grp ? -kLog2e * c23.x : 0.f, Dn = in_grp ? -0.5f * kLog2e * c23.y : 0.f;
+            const float En = in_grp ? -kLog2e * c45.x : 0.f, Fn = in_grp ? -0.5f * kLog2e * c45.y : 0.f;
+            const float Gt[GSV_TILE] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};  // unused
             pair_moments<C, kRowsExact>(s_g + my * kSlot, gx, gy, gz, RowForm{}, A2, Bn, Cn, Dn, En,
-                                        Fn, L.gt.shift, in_grp ? L.gt.half : -1.f, 0.f, L.I, M);
+                                        Fn, gt.shift, in_grp ? gt.half : -1.f, 0.f, Gt, L.I, M);
         }
         __syncthreads();  // a later group restages the slots
     }
@@ -1445,10 +1677,10 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
     int we = 0;
     if (L.live) {
         if (wave_fast) {
-            ws = frexpf(L.gt.fscale, &we);
+            ws = frexpf(L.fscale, &we);
             we -= gexp;
         } else {
-            ws = L.gt.scale;
+            ws = lane_gate(L).scale;
         }
     }
     const float w = (C == 1) ? ws * L.I[0] : ws;
@@ -1459,9 +1691,26 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
     out[3] = ldexpf(-w * M.Syy, we - 1);
     out[4] = ldexpf(-w * M.Syz, we);
     out[5] = ldexpf(-w * M.Szz, we - 1);
-    out[6] = ldexpf(-w * fmaf(L.ca, M.Sx, fmaf(L.cb, M.Sy, L.cc * M.Sz)), we);
-    out[7] = ldexpf(-w * fmaf(L.cb, M.Sx, fmaf(L.cd, M.Sy, L.ce * M.Sz)), we);
-    out[8] = ldexpf(-w * fmaf(L.cc, M.Sx, fmaf(L.ce, M.Sy, L.cf * M.Sz)), we);
+    // dpos = Q (-w S): the deterministic mode stores -w S and k_pair_reduce
+    // applies the conic once per Gaussian to the binary64 sum (linear, so the
+    // same gradient, with one rounding of Q S instead of one per pair); the
+    // atomic mode applies it here
+    if (a.partial != nullptr) {
+        out[6] = ldexpf(-w * M.Sx, we);
+        out[7] = ldexpf(-w * M.Sy, we);
+        out[8] = ldexpf(-w * M.Sz, we);
+    } else {
+        // read again rather than held across the loop (zero without a Gaussian)
+        float2 q01 = make_float2(0.f, 0.f), q23 = q01, q45 = q01;
+        if ((unsigned)L.g < (unsigned)a.n && L.valid) {
+            q01 = a.conics[3 * L.g];
+            q23 = a.conics[3 * L.g + 1];
+            q45 = a.conics[3 * L.g + 2];
+        }
+        out[6] = ldexpf(-w * fmaf(q01.x, M.Sx, fmaf(q01.y, M.Sy, q23.x * M.Sz)), we);
+        out[7] = ldexpf(-w * fmaf(q01.y, M.Sx, fmaf(q23.y, M.Sy, q45.x * M.Sz)), we);
+        out[8] = ldexpf(-w * fmaf(q23.x, M.Sx, fmaf(q45.x, M.Sy, q45.y * M.Sz)), we);
+    }
     if (C == 1) {
         out[9] = ldexpf(ws * M.S0, we);
     } else {
@@ -1471,9 +1720,7 @@ __device__ __forceinline__ void bwd_group(const BwdArgs &a, const BwdLane<C> &L,
     const int g = L.g;
     if (a.partial != nullptr) {
         // Deterministic path: this pair's partial goes to its emission slot
-        const int64_t e = emission_slot_at(g, L.tg.x0 / GSV_TILE, L.tg.y0 / GSV_TILE,
-                                           L.tg.z0 / GSV_TILE, a.n, a.tile_min, a.tile_max, a.cum,
-                                           a.n_isect);
+        const int64_t e = L.slot_e;
         if (e >= 0) {
             float *dst = a.partial + e * (9 + C);
 #pragma unroll
@@ -1597,8 +1844,9 @@ __global__ __launch_bounds__(kWave) void k_vox_bwd_rest(BwdArgs a) {
 // Gaussian g.  Lane r of the row sums slots cum[g-1] + r, + r + 16, ... of
 // [cum[g-1], cum[g]) (a row's loads cover 16 consecutive slots), then a fixed
 // row_shr 1, 2, 4, 8 scan adds the 16 lane sums; all in binary64, lane 15
-// writes every output element.  DPP keeps the cross-lane sums on the VALU (an
-// xor-shuffle butterfly goes through the LDS crossbar, 2 ops per double).
+// writes every output element, dpos as the conic times the summed -w S of the
+// partials.  DPP keeps the cross-lane sums on the VALU (an xor-shuffle
+// butterfly goes through the LDS crossbar, 2 ops per double).
 constexpr int kRowLanes = 16;
 constexpr int kReduceThreads = 256;
 
@@ -1607,6 +1855,11 @@ __device__ __forceinline__ double row_shr(double x) {
     const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(x), kCtrl, 0xf, 0xf, true);
     const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(x), kCtrl, 0xf, 0xf, true);
     return __hiloint2double(hi, lo);
+}
+
+template <int kCtrl>
+__device__ __forceinline__ float row_shr_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, true));
 }
 
 // Inclusive scan within each 16-lane row; lane 15 ends with the row total.
@@ -1620,17 +1873,23 @@ __device__ __forceinline__ double row_total(double x) {
 
 template <int C>
 __global__ __launch_bounds__(kReduceThreads) void k_pair_reduce(
-    int n, int cap, const int64_t *__restrict__ d_count, const int *__restrict__ cum,
-    const float *__restrict__ partial, float *__restrict__ dpos, float *__restrict__ dconic,
-    float *__restrict__ dint) {
+    int n, int cap, const int64_t *__restrict__ d_count, const float4 *__restrict__ rec,
+    const float *__restrict__ partial, const float *__restrict__ conics,
+    float *__restrict__ dpos, float *__restrict__ dconic, float *__restrict__ dint) {
     const int n_isect = live_pairs(cap, d_count);
     constexpr int F = 9 + C;
     const int r = threadIdx.x & (kRowLanes - 1);
     const int g = (int)(((int64_t)blockIdx.x * kReduceThreads + threadIdx.x) / kRowLanes);
     int64_t b = 0, e = 0;
+    // the conic for dpos = Q T: lane r < 6 of the row reads element r, before
+    // the partials so that its latency overlaps them (one load for the wave)
+    float qv = 0.f;
     if (g < n) {  // rows past n reduce zeros; every lane stays for the DPP steps
-        b = g == 0 ? 0 : max(0, cum[g - 1]);
-        e = min<int64_t>(cum[g], n_isect);
+        // [cum[g-1], cum[g]) from the Gaussian's record, which the backward just read
+        const float4 r5 = rec[(size_t)g * kBwdRecF4 + 5];
+        b = max(0, __float_as_int(r5.z));
+        e = min<int64_t>(__float_as_int(r5.w), n_isect);
+        if (r < 6) qv = conics[6 * (size_t)g + r];
     }
     double acc[F];
 #pragma unroll
@@ -1642,29 +1901,44 @@ __global__ __launch_bounds__(kReduceThreads) void k_pair_reduce(
     }
 #pragma unroll
     for (int q = 0; q < F; ++q) acc[q] = row_total(acc[q]);
+    // conic element k from lane k to lane 15 of the row (row_shr 15 - k)
+    const float qa = row_shr_f32<0x11f>(qv), qb = row_shr_f32<0x11e>(qv);
+    const float qc = row_shr_f32<0x11d>(qv), qd = row_shr_f32<0x11c>(qv);
+    const float qe = row_shr_f32<0x11b>(qv), qf = row_shr_f32<0x11a>(qv);
     if (r != kRowLanes - 1 || g >= n) return;
     float2 *dc = reinterpret_cast<float2 *>(dconic + 6 * (size_t)g);
     dc[0] = make_float2((float)acc[0], (float)acc[1]);
     dc[1] = make_float2((float)acc[2], (float)acc[3]);
     dc[2] = make_float2((float)acc[4], (float)acc[5]);
-    reinterpret_cast<float4 *>(dpos)[g] = make_float4((float)acc[6], (float)acc[7], (float)acc[8], 0.f);
+    // dpos = Q T, T = the summed -w S of the pairs (binary64); a Gaussian without
+    // pairs gets zeros whatever its conic
+    float4 dp = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (b < e) {
+        const double a = qa, bb = qb, c = qc, d = qd, ee = qe, f = qf;
+        dp.x = (float)(a * acc[6] + bb * acc[7] + c * acc[8]);
+        dp.y = (float)(bb * acc[6] + d * acc[7] + ee * acc[8]);
+        dp.z = (float)(c * acc[6] + ee * acc[7] + f * acc[8]);
+    }
+    reinterpret_cast<float4 *>(dpos)[g] = dp;
 #pragma unroll
     for (int c = 0; c < C; ++c) dint[(size_t)C * g + c] = (float)acc[9 + c];
 }
 
 struct BwdLayout {
-    size_t tiles, partial, order, part, kept, rest, end;
+    size_t rec, tiles, partial, order, part, kept, rest, end;
 };
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-// pair -> tile map (n_isect ints; unused when the caller passes the binning's
-// sorted keys), the per-pair partials in pairs mode, the work list of the
-// culled mode (order, the per-block counts and the kept count), then the
-// backward's per-wave rest flags.
-BwdLayout bwd_layout(int64_t n_isect, int channels, bool pairs) {
+// the per-Gaussian records (n * 160 bytes), the pair -> tile map (n_isect
+// ints; unused when the caller passes the binning's sorted keys), the per-pair
+// partials in pairs mode, the work list of the culled mode (order, the
+// per-block counts and the kept count), then the backward's per-wave rest
+// flags.
+BwdLayout bwd_layout(int64_t n, int64_t n_isect, int channels, bool pairs) {
     BwdLayout L{};
     size_t off = 0;
+    L.rec = off; off += align256((size_t)imax64(n, 1) * kBwdRecF4 * sizeof(float4));
     L.tiles = off; off += align256((size_t)imax64(n_isect, 1) * 4);
     L.partial = off;
     if (pairs) off += align256((size_t)n_isect * (9 + channels) * 4);
@@ -1768,7 +2042,7 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     const int Tx = gsv_tiles_along(W), Ty = gsv_tiles_along(H), Tz = gsv_tiles_along(D);
     const int64_t T = (int64_t)Tx * Ty * Tz;
     if (T > INT32_MAX || num_intersects > INT32_MAX) return GSV_ERR_SIZE_OVERFLOW;
-    const BwdLayout L = bwd_layout(num_intersects, channels, pairs);
+    const BwdLayout L = bwd_layout(n, num_intersects, channels, pairs);
     if (!workspace || workspace_bytes < L.end) return GSV_ERR_WORKSPACE_TOO_SMALL;
     char *ws = static_cast<char *>(workspace);
     const int *pair_tiles = tiles_sorted;
@@ -1781,6 +2055,26 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
         if (int st = check_launch()) return st;
         pair_tiles = own;
     }
+    // the per-Gaussian records: in the work list's count launch when there is
+    // one, else a launch of their own
+    PrepArgs prep;
+    prep.n = n;
+    prep.pos_radii = reinterpret_cast<const float4 *>(pos3d_radii);
+    prep.conics = reinterpret_cast<const float2 *>(conics);
+    prep.intens = intensities;
+    prep.tile_min = tile_min; prep.tile_max = tile_max; prep.cum = cum_tiles_hit;
+    prep.rec = reinterpret_cast<float4 *>(ws + L.rec);
+    const int nprep = (int)((n + kPrepThreads - 1) / kPrepThreads);
+    if (!pair_live) {
+        const dim3 pgrid((unsigned)nprep), pblock(kPrepThreads);
+        switch (channels) {
+            case 1: hipLaunchKernelGGL(k_bwd_prep<1>, pgrid, pblock, 0, s, prep); break;
+            case 2: hipLaunchKernelGGL(k_bwd_prep<2>, pgrid, pblock, 0, s, prep); break;
+            case 3: hipLaunchKernelGGL(k_bwd_prep<3>, pgrid, pblock, 0, s, prep); break;
+            default: hipLaunchKernelGGL(k_bwd_prep<4>, pgrid, pblock, 0, s, prep); break;
+        }
+        if (int st = check_launch()) return st;
+    }
     const int *order = nullptr;
     const int64_t *d_work = nullptr;
     if (pair_live) {  // the work list of the pairs the forward kept
@@ -1790,8 +2084,17 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
         int64_t *kept = reinterpret_cast<int64_t *>(ws + L.kept);
         const int64_t nb = (num_intersects + kKeepTile - 1) / kKeepTile;
         const int direct = nb <= scan_detail::kDirectBlocks ? 1 : 0;
-        hipLaunchKernelGGL(k_keep_count, dim3((unsigned)nb), dim3(kKeepThreads), 0, s, pair_live,
-                           ni, count_dev, part);
+        const dim3 kgrid((unsigned)(nprep + nb)), kblock(kKeepThreads);
+#define GSV_KC(CH)                                                                                 \
+    hipLaunchKernelGGL(k_keep_count<CH>, kgrid, kblock, 0, s, pair_live, ni, count_dev, part,      \
+                       nprep, prep)
+        switch (channels) {
+            case 1: GSV_KC(1); break;
+            case 2: GSV_KC(2); break;
+            case 3: GSV_KC(3); break;
+            default: GSV_KC(4); break;
+        }
+#undef GSV_KC
         if (int st = check_launch()) return st;
         if (!direct) {
             hipLaunchKernelGGL(scan_detail::k_scan_block_sums, dim3(1),
@@ -1821,6 +2124,7 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
     args.l1_sgn = l1_sgn; args.l1_grad = l1_grad; args.l1_numel = numel;
     args.dpos = dpos3d_radii; args.dconic = dconics; args.dint = dintensities;
     args.tile_min = tile_min; args.tile_max = tile_max; args.cum = cum_tiles_hit;
+    args.rec = reinterpret_cast<const float4 *>(ws + L.rec);
     args.partial = partial;
     args.d_count = count_dev;
     args.order = order;
@@ -1854,8 +2158,9 @@ int voxelize_bwd_impl(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t
         hipLaunchKernelGGL(k_pair_reduce<CH>,                                                      \
                            dim3((unsigned)(((int64_t)n * kRowLanes + kReduceThreads - 1) /          \
                                            kReduceThreads)),                                        \
-                           dim3(kReduceThreads), 0, s, n, ni, count_dev,                            \
-                           cum_tiles_hit, partial, dpos3d_radii, dconics, dintensities);            \
+                           dim3(kReduceThreads), 0, s, n, ni, count_dev, args.rec, partial,        \
+                           conics, dpos3d_radii, dconics,                                           \
+                           dintensities);                                                           \
     }
     // pairs per tile from the count the grids are sized for (an upper bound
     // when the live count is on the device)
@@ -1912,11 +2217,12 @@ extern "C" int gsv_voxelize_fwd_l1(int32_t D, int32_t H, int32_t W, int32_t chan
 }
 
 extern "C" int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W,
-                                                int32_t channels, int64_t num_intersects,
-                                                int32_t deterministic, size_t *bytes) {
-    if (!bytes || D <= 0 || H <= 0 || W <= 0) return GSV_ERR_INVALID_ARGUMENT;
+                                                int32_t channels, int32_t n,
+                                                int64_t num_intersects, int32_t deterministic,
+                                                size_t *bytes) {
+    if (!bytes || D <= 0 || H <= 0 || W <= 0 || n < 0) return GSV_ERR_INVALID_ARGUMENT;
     if (channels < 1 || channels > GSV_MAX_CHANNELS) return GSV_ERR_UNSUPPORTED_CHANNELS;
-    *bytes = bwd_layout(num_intersects > 0 ? num_intersects : 0, channels, deterministic != 0).end;
+    *bytes = bwd_layout(n, num_intersects > 0 ? num_intersects : 0, channels, deterministic != 0).end;
     return GSV_OK;
 }
 

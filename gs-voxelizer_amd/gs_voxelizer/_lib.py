@@ -44,7 +44,7 @@ SIGNATURES = {
     "gsv_voxelize_fwd_l1_workspace_bytes": [_c_int, _c_int, _c_int, ctypes.POINTER(_c_size_t)],
     "gsv_voxelize_fwd_l1": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P,
                             _P, _P, _P, _P, _P, _P, _c_size_t, _P],
-    "gsv_voxelize_bwd_workspace_bytes": [_c_int, _c_int, _c_int, _c_int, _c_i64, _c_int,
+    "gsv_voxelize_bwd_workspace_bytes": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int,
                                          ctypes.POINTER(_c_size_t)],
     "gsv_voxelize_bwd": [_c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _P, _P, _P, _P, _P, _P,
                          _P, _P, _P, _P, _P, _P, _P, _P, _P, _c_int, _P, _c_size_t, _P],

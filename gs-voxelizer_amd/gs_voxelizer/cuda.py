@@ -420,7 +420,7 @@ def _voxelize_backward(variant, vol_size, gaussian_ids_sorted, tile_bins, pos3d,
     dconics = torch.empty((n, 6), **f32)
     dint = torch.empty((n, channels), **f32)
     nbytes = ctypes.c_size_t(0)
-    _call("voxelize_bwd_workspace_bytes", D, H, W, channels, I, int(deterministic),
+    _call("voxelize_bwd_workspace_bytes", D, H, W, channels, n, I, int(deterministic),
           ctypes.byref(nbytes))
     ws = torch.empty((max(nbytes.value, 1),), device=dev, dtype=torch.uint8)
     null = ctypes.c_void_p(0)

@@ -241,11 +241,15 @@ int gsv_voxelize_fwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t 
  * rounding depends on the pairs that share its wave, and the flags, the
  * capacity mode and the tile map change that grouping: the results then agree
  * to rounding (rel 1e-4 / abs 1e-6), not bit for bit.
- * Workspace size from gsv_voxelize_bwd_workspace_bytes (deterministic = 1 for
- * the second mode).
+ * Workspace size from gsv_voxelize_bwd_workspace_bytes (n = the Gaussian
+ * count, deterministic = 1 for the second mode): besides the per-pair arrays
+ * it holds one 128-byte record per Gaussian, which a first kernel fills with
+ * what the pairs read of their Gaussian and the parts of their set-up that do
+ * not depend on the tile (the gate, the binary64 factor of the conic, the
+ * chain bounds' Gaussian terms, the column factors, the emission box).
  */
 int gsv_voxelize_bwd_workspace_bytes(int32_t D, int32_t H, int32_t W, int32_t channels,
-                                     int64_t num_intersects, int32_t deterministic,
+                                     int32_t n, int64_t num_intersects, int32_t deterministic,
                                      size_t *bytes);
 int gsv_voxelize_bwd(int32_t D, int32_t H, int32_t W, int32_t channels, int32_t n,
                      int64_t num_intersects, const int32_t *gaussian_ids_sorted,

@@ -59,10 +59,15 @@ def test_workspace_sizes_are_host_only():
     assert b.value >= 3 * 3_542_885 * 4
     small = b.value
     assert L.gsv_bin_workspace_bytes(200_000, 2**31, 256, 256, 256, ctypes.byref(b)) == 4
-    assert L.gsv_voxelize_bwd_workspace_bytes(256, 256, 256, 1, 3_542_885, 1, ctypes.byref(b)) == 0
+    assert L.gsv_voxelize_bwd_workspace_bytes(256, 256, 256, 1, 200_000, 3_542_885, 1,
+                                              ctypes.byref(b)) == 0
     det = b.value
-    assert L.gsv_voxelize_bwd_workspace_bytes(256, 256, 256, 1, 3_542_885, 0, ctypes.byref(b)) == 0
+    assert L.gsv_voxelize_bwd_workspace_bytes(256, 256, 256, 1, 200_000, 3_542_885, 0,
+                                              ctypes.byref(b)) == 0
     assert det - b.value >= 3_542_885 * 10 * 4  # per-pair partials of the deterministic mode
+    assert b.value >= 200_000 * 128  # one 128-byte record per Gaussian
+    assert L.gsv_voxelize_bwd_workspace_bytes(256, 256, 256, 1, -1, 3_542_885, 0,
+                                              ctypes.byref(b)) == 1  # GSV_ERR_INVALID_ARGUMENT
     assert small > 0
 
 

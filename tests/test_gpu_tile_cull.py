@@ -175,7 +175,7 @@ def _bwd_on_workspace(R, cfg, gd, fill, with_flags):
     D, H, W = cfg.vol
     C = _C._channels(w.intensities)
     nbytes = ctypes.c_size_t(0)
-    _C._call("voxelize_bwd_workspace_bytes", D, H, W, C, I, 1, ctypes.byref(nbytes))
+    _C._call("voxelize_bwd_workspace_bytes", D, H, W, C, n, I, 1, ctypes.byref(nbytes))
     ws = torch.full((nbytes.value,), fill, device=gd.device, dtype=torch.uint8)
     f32 = dict(device=gd.device, dtype=torch.float32)
     dpos, dconic, dint = (torch.empty((n, k), **f32) for k in (4, 6, C))

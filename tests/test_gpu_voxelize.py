@@ -307,3 +307,34 @@ def test_backward_chain_guard_on_needle_in_a_chained_wave(device):
             a = np32(a)
             assert np.isfinite(a).all(), f"needle {mode}: {nm} not finite"
             report_close(f"needle guard {mode}: {nm}", a, b, RTOL, ATOL, bound=1e-5 * s + m)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_backward_gaussians_without_pairs_get_zero_gradients(device, mode):
+    """A Gaussian with no (tile, Gaussian) pair gets zero gradients in both
+    reduction modes, whatever its conic holds: the per-pair mode applies each
+    Gaussian's conic once, to the sum of its pairs' moments, and only when it
+    has pairs.  The other Gaussians' gradients do not depend on those conics."""
+    work = S.make_gaussians(S.CONFIGS[1], seed=0)
+    outside = torch.arange(0, 40, 5)
+    work.pos3d[outside] = 5.0  # far outside the [0, 1]^3 world box: no tiles
+    cfg = work.cfg
+    P = _prepare(work, device)
+    nt = np.diff(np.concatenate([[0], np32(P["cum"]).astype(np.int64)]))
+    assert (nt[outside.numpy()] == 0).all() and (nt > 0).sum() > 1000
+    C = work.intensities.shape[1]
+    g = torch.from_numpy(np.random.default_rng(3).standard_normal(cfg.vol + (C,)).astype(np.float32))
+    g = g.to(device)
+    base = [np32(t) for t in _gpu_bwd(P, cfg, g, 1, mode)]
+    cn = P["cn"].clone()
+    cn[outside[::2].to(device)] = float("inf")
+    cn[outside[1::2].to(device)] = float("nan")
+    P2 = dict(P, cn=cn)
+    got = [np32(t) for t in _gpu_bwd(P2, cfg, g, 1, mode)]
+    torch.cuda.synchronize()
+    rest = np.ones(nt.shape[0], bool)
+    rest[outside.numpy()] = False
+    for nm, a, b in zip(("dpos3d_radii", "dconics", "dintensities"), got, base):
+        assert (a[outside.numpy()] == 0).all(), nm
+        if mode == "pairs":  # float atomics leave the last bits to the schedule
+            np.testing.assert_array_equal(a[rest], b[rest], err_msg=nm)
