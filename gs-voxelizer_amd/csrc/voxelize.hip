@@ -1762,9 +1762,14 @@ __device__ __forceinline__ void zero_partial(const BwdArgs &a, int64_t e) {
 // the work list of kept pairs), lane = pair, so no lane idles except in the
 // last wave.  The wave stages the first K tiles its pairs span (lane = row;
 // each lane reads its own tile's rows); the pairs of further tiles are left to
-// k_vox_bwd_rest.
+// k_vox_bwd_rest.  At C = 2 and 3 the kernel fits 128 VGPRs (4 waves per
+// SIMD), but left free the compiler's schedule for C = 2, K = 6 and C = 3,
+// K = 4 took all 256 and spilled into AGPRs (1 wave per SIMD): the bound
+// holds those two to the others' occupancy.  C = 1 (106 VGPRs) and C = 4
+// (3 waves) take the compiler's own choice.
 template <int C, int K>
-__global__ __launch_bounds__(kWave) void k_vox_bwd(BwdArgs a) {
+__global__ __launch_bounds__(kWave)
+__attribute__((amdgpu_waves_per_eu(C == 2 || C == 3 ? 2 : 1, 8))) void k_vox_bwd(BwdArgs a) {
     __shared__ float4 s_g[K * (kWave * 2 * C + 1)];
     bwd_counts(a);
     // XCD slabs sized by the live wave count (the grid may be sized for a
