@@ -1766,7 +1766,12 @@ __device__ __forceinline__ void zero_partial(const BwdArgs &a, int64_t e) {
 // SIMD), but left free the compiler's schedule for C = 2, K = 6 and C = 3,
 // K = 4 took all 256 and spilled into AGPRs (1 wave per SIMD): the bound
 // holds those two to the others' occupancy.  C = 1 (106 VGPRs) and C = 4
-// (3 waves) take the compiler's own choice.
+// (3 waves) take the compiler's own choice.  C = 3, K = 6 stages 36,960 bytes,
+// which LDS holds to one wave per SIMD: there the bound only caps the
+// registers (128 VGPRs, no AGPRs), and the compiler's note that it missed the
+// occupancy target is silenced.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wpass-failed"
 template <int C, int K>
 __global__ __launch_bounds__(kWave)
 __attribute__((amdgpu_waves_per_eu(C == 2 || C == 3 ? 2 : 1, 8))) void k_vox_bwd(BwdArgs a) {
@@ -1812,6 +1817,7 @@ __attribute__((amdgpu_waves_per_eu(C == 2 || C == 3 ? 2 : 1, 8))) void k_vox_bwd
         if (e >= 0) zero_partial<C>(a, e);
     }
 }
+#pragma clang diagnostic pop
 
 // The pairs that k_vox_bwd left: those of the waves spanning more than K tiles,
 // in groups of K tiles after the first.  A fixed grid of kRestBlocks
