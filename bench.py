@@ -23,7 +23,8 @@ arithmetic the kernel executes per launch, read from rocprofv3 counters of the
 same workload (profiles/valu_<workload>.json: 64 lanes x (2 FMA + ADD + MUL +
 TRANS) wave instructions), divided by that duration; `peak` is MI355X's FP32
 vector peak.  `ref_formulation_tflops` is the reference's flop count for the
-same evaluations (E x (65 + 4C), SURVEY's per-evaluation figure) over the same
+same evaluations (E x (65 + 4C): voxelize.cu:368-574's per-evaluation terms,
+delta 3, sigma 18, gate 1, 4C channel terms, dsigma 1, dconic 21, dmu 21) over the same
 duration; this kernel evaluates a cheaper but equivalent formulation and skips
 culled pairs, so that figure can exceed the peak and is not a utilisation.
 The kernel is co-limited by VALU issue and by per-wave memory latency (a timing
@@ -122,8 +123,9 @@ class KernelTimer:
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is "
-                                   "designed (DESIGN.md) but not built", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding "
+                                   "(z-slabs of tiles per GPU) is designed but not built",
+                          "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
     import torch.nn.functional as F
