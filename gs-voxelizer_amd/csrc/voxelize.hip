@@ -1941,7 +1941,7 @@ struct BwdLayout {
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-// the per-Gaussian records (n * 160 bytes), the pair -> tile map (n_isect
+// the per-Gaussian records (n * 128 bytes), the pair -> tile map (n_isect
 // ints; unused when the caller passes the binning's sorted keys), the per-pair
 // partials in pairs mode, the work list of the culled mode (order, the
 // per-block counts and the kept count), then the backward's per-wave rest
